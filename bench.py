@@ -1,0 +1,332 @@
+"""Decode-step benchmark of the MI355X selected-quant paged decode.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg3]
+
+Workload (default ``cfg3``, the configuration the headline metric is quoted
+on): Llama-3-8B GQA decode, batch 32, 32 query / 8 KV heads, head_dim 128,
+65536-token context per sequence in 16-token pages (4096 pages per sequence
+and KV head, 1,048,576 physical pages), 40 % of pages selected uniformly at
+random (1638 per sequence and KV head), physical page table a random
+permutation. Per-page precision at random: 25 % FP16, 25 % FP8-e4m3, 30 %
+INT8, 20 % INT4 (two codes per byte, one scale per page, KV head and
+32-channel group). K/V float16 N(0, 1) with 1 % of K elements set to 8*sign;
+Q N(0, 1)/sqrt(128). Codes and scales are the reference's fake-quant
+arithmetic (absmax/127 in float16, round half even), computed on the GPU with
+torch ops; tests check them bit-exact against the oracle.
+
+A step is one decode of the whole batch (split kernel + merge kernel) with
+every input already in HBM; the 2 GB the step reads exceed the 256 MB
+Infinity Cache, so consecutive steps do not hit in it. Timing: HIP events on
+the stream the kernels run on, around the K timed steps and around each
+step. ``value`` is the achieved algorithmic bandwidth (bytes the step must
+read and write / step time). The CPU baseline times the test oracle (numpy,
+one thread) on a bounded sample of rows of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "intent-attention-kernel_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+METRIC = ("decode-attn µs/step + achieved HBM GB/s (% of peak), Llama-3-8B GQA, 64k ctx, mixed")
+HBM_PEAK_GBPS = 8000.0
+PS = 16
+
+TAG_FP16, TAG_INT8, TAG_SKIP, TAG_FP8, TAG_INT4, TAG_INT4R = 0, 1, 2, 3, 4, 5
+
+CONFIGS = {
+    # name: B, Hq, Hkv, D, tokens, selected fraction or count, precision mix, outlier frac, q scale
+    "cfg2": dict(B=16, Hq=32, Hkv=8, D=128, T=32768, sel="cfg2", mix={TAG_FP16: 1.0}, outliers=0.0,
+                 q_scale=1 / math.sqrt(128)),
+    "cfg3": dict(B=32, Hq=32, Hkv=8, D=128, T=65536, sel=0.40,
+                 mix={TAG_FP16: .25, TAG_FP8: .25, TAG_INT8: .30, TAG_INT4: .20}, outliers=0.01,
+                 q_scale=1 / math.sqrt(128)),
+    "cfg4": dict(B=4, Hq=32, Hkv=8, D=128, T=131072, sel=0.15,
+                 mix={TAG_FP16: .10, TAG_INT8: .30, TAG_INT4R: .60}, outliers=0.0, q_scale=1.0),
+    # small all-precision case for tests and smoke runs
+    "tiny": dict(B=2, Hq=8, Hkv=2, D=128, T=2048, sel=0.40,
+                 mix={TAG_FP16: .2, TAG_FP8: .2, TAG_INT8: .2, TAG_INT4: .2, TAG_INT4R: .2}, outliers=0.01,
+                 q_scale=1 / math.sqrt(128)),
+}
+
+
+# --------------------------------------------------------------------------- #
+# Quantisation of synthetic pages (reference arithmetic, torch ops on device)
+# --------------------------------------------------------------------------- #
+
+def _div127(x: torch.Tensor) -> torch.Tensor:
+    # a tensor divisor keeps a true division on GPU tensors
+    return x / torch.full((1,), 127.0, dtype=x.dtype, device=x.device)
+
+
+def quantize_pages(x: torch.Tensor, tag: int, group: int = 32):
+    """x [n, 16, D] float16 -> (codes, scales) in the kernel's storage format.
+
+    FP8 / INT8 / INT4_RESIDUAL: one scale per page; INT4: one per ``group``
+    channels. float16 arithmetic as fake_quantize_tensor on float16 input.
+    """
+    n, ps, D = x.shape
+    if tag in (TAG_FP8, TAG_INT8, TAG_INT4R):
+        flat = x.reshape(n, -1)
+        scale = _div127(flat.abs().amax(dim=1, keepdim=True)).clamp(min=1e-8)
+        y = flat / scale
+        if tag == TAG_FP8:
+            codes = y.to(torch.float8_e4m3fn).view(torch.uint8)
+            return codes.reshape(n, ps, D), scale.reshape(n)
+        if tag == TAG_INT8:
+            return y.clamp(-127, 127).round().to(torch.int8).reshape(n, ps, D), scale.reshape(n)
+        q1 = y.clamp(-7, 7).round()
+        base = q1.float() * scale.float()
+        resid = flat.float() - base
+        s2 = (resid.abs().amax(dim=1, keepdim=True) / torch.full((1,), 127.0, device=x.device)).clamp(min=1e-8)
+        q2 = (resid / s2).clamp(-7, 7).round()
+        packed = ((q1.to(torch.int16) + 8) | ((q2.to(torch.int16) + 8) << 4)).to(torch.uint8)
+        return packed.reshape(n, ps, D), torch.stack([scale.float().reshape(n), s2.reshape(n)], dim=1)
+    if tag == TAG_INT4:
+        g = x.reshape(n, ps, D // group, group)
+        scale = _div127(g.abs().amax(dim=(1, 3), keepdim=True)).clamp(min=1e-8)
+        codes = (g / scale).clamp(-7, 7).round().to(torch.int16).reshape(n, ps, D) + 8
+        packed = (codes[..., 0::2] | (codes[..., 1::2] << 4)).to(torch.uint8)
+        return packed, scale.reshape(n, D // group)
+    raise ValueError(tag)
+
+
+# --------------------------------------------------------------------------- #
+# Workload
+# --------------------------------------------------------------------------- #
+
+def build_workload(name: str, device: torch.device, seed: int = 1234, chunk_pages: int = 65536):
+    from intent_attention import PagePools
+    cfg = CONFIGS[name]
+    B, Hq, Hkv, D, T = cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["D"], cfg["T"]
+    P = T // PS
+    NP = B * Hkv * P
+    g = torch.Generator(device=device).manual_seed(seed)
+    gc = torch.Generator().manual_seed(seed)
+
+    # per-physical-page precision
+    tags_list = list(cfg["mix"])
+    probs = torch.tensor([cfg["mix"][t] for t in tags_list])
+    tag_idx = torch.multinomial(probs, NP, replacement=True, generator=gc)
+    tags = torch.tensor(tags_list, dtype=torch.int32)[tag_idx].to(device)
+
+    # page table: random physical permutation; selection per (b, kv head)
+    perm = torch.randperm(NP, generator=gc).to(torch.int32).reshape(B * Hkv, P)
+    if cfg["sel"] == "cfg2":      # first 64 ALWAYS, last 256 RECENT, 704 random from the middle
+        mid = torch.stack([torch.randperm(P - 320, generator=gc)[:704] + 64 for _ in range(B * Hkv)])
+        logical = torch.cat([torch.arange(64).expand(B * Hkv, 64), mid.sort(dim=1).values,
+                             torch.arange(P - 256, P).expand(B * Hkv, 256)], dim=1)
+    else:
+        nsel = int(cfg["sel"] * P)
+        logical = torch.stack([torch.randperm(P, generator=gc)[:nsel].sort().values for _ in range(B * Hkv)])
+    table = torch.gather(perm, 1, logical).reshape(B, Hkv, -1).contiguous().to(device)
+    W = table.shape[2]
+    counts = torch.full((B, Hkv), W, dtype=torch.int32, device=device)
+
+    pools = PagePools(int4_group=32)
+    pools.k_fp16 = torch.empty((NP, PS, D), dtype=torch.float16, device=device)
+    pools.v_fp16 = torch.empty((NP, PS, D), dtype=torch.float16, device=device)
+    present = set(cfg["mix"])
+    if TAG_FP8 in present:
+        pools.k_fp8 = torch.zeros((NP, PS, D), dtype=torch.uint8, device=device)
+        pools.v_fp8 = torch.zeros_like(pools.k_fp8)
+        pools.k_fp8_scale = torch.zeros(NP, dtype=torch.float16, device=device)
+        pools.v_fp8_scale = torch.zeros_like(pools.k_fp8_scale)
+    if TAG_INT8 in present:
+        pools.k_int8 = torch.zeros((NP, PS, D), dtype=torch.int8, device=device)
+        pools.v_int8 = torch.zeros_like(pools.k_int8)
+        pools.k_int8_scale = torch.zeros(NP, dtype=torch.float16, device=device)
+        pools.v_int8_scale = torch.zeros_like(pools.k_int8_scale)
+    if TAG_INT4 in present:
+        pools.k_int4 = torch.full((NP, PS, D // 2), 0x88, dtype=torch.uint8, device=device)
+        pools.v_int4 = torch.full_like(pools.k_int4, 0x88)
+        pools.k_int4_scale = torch.zeros((NP, D // 32), dtype=torch.float16, device=device)
+        pools.v_int4_scale = torch.zeros_like(pools.k_int4_scale)
+    if TAG_INT4R in present:
+        pools.k_int4r = torch.full((NP, PS, D), 0x88, dtype=torch.uint8, device=device)
+        pools.v_int4r = torch.full_like(pools.k_int4r, 0x88)
+        pools.k_int4r_scale = torch.zeros((NP, 2), dtype=torch.float32, device=device)
+        pools.v_int4r_scale = torch.zeros_like(pools.k_int4r_scale)
+
+    dest = {TAG_FP8: ("fp8", "fp8_scale"), TAG_INT8: ("int8", "int8_scale"), TAG_INT4: ("int4", "int4_scale"),
+            TAG_INT4R: ("int4r", "int4r_scale")}
+    for lo in range(0, NP, chunk_pages):
+        hi = min(NP, lo + chunk_pages)
+        for w in ("k", "v"):
+            x = torch.randn((hi - lo, PS, D), generator=g, device=device, dtype=torch.float32)
+            if w == "k" and cfg["outliers"] > 0:
+                m = torch.rand(x.shape, generator=g, device=device) < cfg["outliers"]
+                x = torch.where(m, 8.0 * torch.sign(x), x)
+            x = x.half()
+            getattr(pools, f"{w}_fp16")[lo:hi] = x
+            t = tags[lo:hi]
+            for tag, (pool, sc) in dest.items():
+                if tag not in present:
+                    continue
+                idx = torch.nonzero(t == tag).flatten()
+                if idx.numel() == 0:
+                    continue
+                codes, scales = quantize_pages(x[idx], tag)
+                getattr(pools, f"{w}_{pool}")[lo + idx] = codes
+                getattr(pools, f"{w}_{sc}")[lo + idx] = scales.to(getattr(pools, f"{w}_{sc}").dtype)
+    q = (torch.randn((B, Hq, D), generator=g, device=device) * cfg["q_scale"]).half()
+    return dict(cfg=cfg, name=name, q=q, pools=pools, table=table, counts=counts, tags=tags, NP=NP, W=W)
+
+
+PAGE_BYTES = {  # K+V code bytes and scale bytes per page (D = 128, fp16 scales, INT4 groups of 32)
+    TAG_FP16: (2 * PS * 128 * 2, 0), TAG_FP8: (2 * PS * 128, 2 * 2), TAG_INT8: (2 * PS * 128, 2 * 2),
+    TAG_INT4: (2 * PS * 64, 2 * 4 * 2), TAG_INT4R: (2 * PS * 128, 2 * 2 * 4), TAG_SKIP: (0, 0),
+}
+
+
+def algorithmic_bytes(wl) -> dict:
+    """Bytes one step must move: each selected page's K+V codes and scales once
+    per KV head (GQA shares them), its page-table entry and tag, the counts,
+    Q in and O out."""
+    tags_sel = wl["tags"][wl["table"].long()].flatten()
+    n = {t: int((tags_sel == t).sum()) for t in PAGE_BYTES}
+    codes = sum(n[t] * PAGE_BYTES[t][0] for t in n)
+    scales = sum(n[t] * PAGE_BYTES[t][1] for t in n)
+    meta = tags_sel.numel() * (4 + 4) + wl["counts"].numel() * 4
+    qo = 2 * wl["q"].numel() * 2
+    return dict(total=codes + scales + meta + qo, codes=codes, scales=scales, meta=meta, qo=qo,
+                pages=int(tags_sel.numel()), per_tag={str(k): v for k, v in n.items()})
+
+
+def flops(wl) -> float:
+    cfg = wl["cfg"]
+    toks = int(wl["tags"][wl["table"].long()].ne(TAG_SKIP).sum()) * PS
+    return 4.0 * toks * (cfg["Hq"] // cfg["Hkv"]) * cfg["D"]
+
+
+# --------------------------------------------------------------------------- #
+# CPU baseline: the oracle on a bounded sample of rows
+# --------------------------------------------------------------------------- #
+
+def cpu_baseline(wl, rows: int, budget_s: float = 20.0) -> dict:
+    from threadpoolctl import threadpool_limits
+
+    from oracle.decode import paged_decode_oracle
+    cfg = wl["cfg"]
+    B, Hkv, G, D = cfg["B"], cfg["Hkv"], cfg["Hq"] // cfg["Hkv"], cfg["D"]
+    total_rows = B * Hkv
+    table = wl["table"].reshape(total_rows, -1)
+    pick = list(range(0, total_rows, max(1, total_rows // rows)))[:rows]
+    ids = table[pick].flatten()
+    uniq, inv = torch.unique(ids, return_inverse=True)
+    p = wl["pools"]
+
+    def host(t):
+        return None if t is None else t[uniq.long()].cpu().numpy()
+
+    pools = {"k_fp16": host(p.k_fp16), "v_fp16": host(p.v_fp16)}
+    for nm, src in (("fp8", "fp8"), ("i8", "int8"), ("i4", "int4"), ("i4r", "int4r")):
+        for w in ("k", "v"):
+            if getattr(p, f"{w}_{src}") is not None:
+                pools[f"{w}_{nm}"] = host(getattr(p, f"{w}_{src}"))
+                pools[f"{w}_{nm}_scale"] = host(getattr(p, f"{w}_{src}_scale"))
+    tags = wl["tags"][uniq.long()].cpu().numpy()
+    tbl = inv.reshape(len(pick), 1, -1).cpu().numpy().astype(np.int32)
+    cnt = wl["counts"].reshape(total_rows)[pick].reshape(len(pick), 1).cpu().numpy()
+    q = wl["q"].reshape(B, Hkv, G, D).reshape(total_rows, G, D)[pick].cpu().numpy()
+    done, t0 = 0, time.perf_counter()
+    with threadpool_limits(limits=1):
+        for i in range(len(pick)):
+            paged_decode_oracle(q[i:i + 1], pools, tbl[i:i + 1], cnt[i:i + 1], tags, dtype=np.float32)
+            done += 1
+            if time.perf_counter() - t0 > budget_s:
+                break
+    dt = time.perf_counter() - t0
+    step_s = dt * total_rows / done
+    ab = algorithmic_bytes(wl)["total"]
+    return {"value": ab / step_s / 1e9, "unit": "GB/s", "us_per_step": step_s * 1e6, "cores": 1,
+            "kind": "port",
+            "sample": f"oracle.decode.paged_decode_oracle (numpy float32, 1 thread) on {done} of "
+                      f"{total_rows} (batch, kv-head) rows of {wl['name']}, {dt:.1f} s, scaled to the full step"}
+
+
+# --------------------------------------------------------------------------- #
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS))
+    ap.add_argument("--pages-per-split", type=int, default=0)
+    ap.add_argument("--cpu-rows", type=int, default=64, help="rows of the step the CPU baseline times")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build's decode runs on a single device "
+              f"(--gpus {args.gpus} is not supported; multi-GPU sharding is a design note only)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    from intent_attention.decode_core import make_plan
+    dev = torch.device("cuda:0")
+    t_build = time.perf_counter()
+    wl = build_workload(args.config, dev)
+    torch.cuda.synchronize()
+    print(f"[bench] built {args.config}: NP={wl['NP']} W={wl['W']} in {time.perf_counter() - t_build:.1f}s",
+          file=sys.stderr, flush=True)
+    cfg = wl["cfg"]
+    out = torch.empty((cfg["B"], cfg["Hq"], cfg["D"]), dtype=torch.float16, device=dev)
+    plan = make_plan(wl["q"], wl["pools"], wl["table"], wl["counts"], wl["tags"], out=out,
+                     pages_per_split=args.pages_per_split)
+    stream = torch.cuda.current_stream(dev)
+    for _ in range(args.warmup):
+        plan.run()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    t_start, t_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_start.record(stream)
+    for s, e in ev:
+        s.record(stream)
+        plan.run()
+        e.record(stream)
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    total_ms = t_start.elapsed_time(t_end)
+    per = sorted(s.elapsed_time(e) for s, e in ev)
+    ms = total_ms / args.steps
+    ab = algorithmic_bytes(wl)
+    achieved = ab["total"] / (ms * 1e-3) / 1e9
+    med = per[len(per) // 2]
+    res = {
+        "metric": METRIC, "value": round(achieved, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+        "us_per_step": round(ms * 1e3, 2), "us_per_step_p10_p50_p90": [round(per[len(per) // 10] * 1e3, 2),
+                                                                       round(med * 1e3, 2),
+                                                                       round(per[(9 * len(per)) // 10] * 1e3, 2)],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+        "data": "synthetic (seeded torch generator; codes = reference fake-quant of N(0,1) fp16 pages)",
+        "config": {"workload": f"{args.config}: Llama-3-8B GQA decode B={cfg['B']} Hq={cfg['Hq']} "
+                               f"Hkv={cfg['Hkv']} D={cfg['D']} ctx={cfg['T']} page=16 "
+                               f"sel={wl['W']} pages/row mix={ {int(k): v for k, v in cfg['mix'].items()} }",
+                   "selected_pages": ab["pages"], "algorithmic_bytes": ab["total"],
+                   "bytes_breakdown": {k: ab[k] for k in ("codes", "scales", "meta", "qo")},
+                   "pages_per_tag": ab["per_tag"], "pages_per_split": plan.args.pages_per_split,
+                   "gflop": round(flops(wl) / 1e9, 3)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None},
+    }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline(wl, args.cpu_rows)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

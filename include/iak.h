@@ -1,0 +1,134 @@
+/*
+ * iak.h -- C ABI of the MI355X (gfx950) selected-quant paged decode library
+ * (libiak.so). Plain pointers, sizes and status codes; no torch or HIP types.
+ *
+ * Ownership: the caller owns every buffer (inputs, output, workspace). The
+ * library keeps no global state and allocates nothing; calls are asynchronous
+ * on the caller's HIP stream and never synchronise the host.
+ *
+ * Reference interfaces these entry points replace (paths relative to the
+ * reference's src/intent_attention/):
+ *   iak_paged_decode            fused_selected_quant_decode()          fused_selected_quant_decode.py:408-464
+ *                               (its Triton launch _launch_triton_kernel :472-513, kernel :87-255)
+ *                               and intent_quant_decode_attention_triton()
+ *                                                                      triton_intent_quant_attention.py:342-457
+ *   iak_paged_decode_workspace  (no counterpart: sizes the split-K partial buffer the caller allocates)
+ *   iak_status_string           (no counterpart: the reference raises ValueError/RuntimeError in Python)
+ */
+#ifndef IAK_H
+#define IAK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define IAK_ABI_VERSION 1
+
+typedef enum {
+  IAK_OK = 0,
+  IAK_EINVAL = 1,   /* bad argument (shape, dtype, pointer, size): Python maps it to ValueError */
+  IAK_ENOTSUP = 2,  /* valid but unsupported configuration (e.g. head_dim): ValueError          */
+  IAK_EHIP = 3      /* HIP runtime error (launch, device): RuntimeError                         */
+} iak_status;
+
+/* Native page precision tags: the reference's fused numbering
+ * (FusedKVPrecision, fused_selected_quant_decode.py:29-34) with the native
+ * precisions appended. */
+enum {
+  IAK_TAG_FP16 = 0,
+  IAK_TAG_INT8 = 1,
+  IAK_TAG_SKIP = 2,
+  IAK_TAG_FP8 = 3,           /* OCP e4m3fn codes, one scale per page            */
+  IAK_TAG_INT4 = 4,          /* two codes per byte, one scale per page x group   */
+  IAK_TAG_INT4_RESIDUAL = 5  /* base | residual<<4 per byte, two scales per page */
+};
+
+enum { IAK_DTYPE_F16 = 0, IAK_DTYPE_F32 = 1, IAK_DTYPE_BF16 = 2 };
+
+/*
+ * Arguments of one decode step. Pools are indexed by physical page id and
+ * laid out [num_pages, page_size, head_dim] (contiguous), as the reference's
+ * k_pages_fp16 / k_pages_int8 (fused_selected_quant_decode.py:427-433). A page
+ * holds one KV head of page_size tokens.
+ *
+ *   q            [batch, num_q_heads, head_dim], element strides q_stride_b / q_stride_h
+ *   out          [batch, num_q_heads, head_dim], element strides out_stride_b / out_stride_h
+ *   page_table   [batch, num_kv_heads, table_width] int32 (contiguous); row (b, h) lists the
+ *                physical pages attended by KV head h of sequence b; query heads
+ *                h*G .. h*G+G-1 (G = num_q_heads / num_kv_heads) share it.
+ *   page_counts  [batch, num_kv_heads] int32; entries are clamped to [0, table_width].
+ *   page_tags    [num_pages] int32 caller tags, translated by tag_map[tag] to a native tag;
+ *                tags outside [0, 8) and map entries outside the enum contribute nothing.
+ *   negative_ids 0: an id < 0 is an invalid page (contributes nothing);
+ *                1: an id in [-num_pages, 0) means id + num_pages (torch indexing).
+ *                Ids outside the pool always contribute nothing.
+ *
+ *   FP16 pages: k_fp16/v_fp16 f16.
+ *   FP8 pages:  k_fp8/v_fp8 e4m3fn bytes; k_fp8_scale/v_fp8_scale [num_pages] (scale_dtype).
+ *   INT8 pages: k_int8/v_int8 int8; k_int8_scale/v_int8_scale [num_pages] (scale_dtype).
+ *   INT4 pages: k_int4/v_int4 [num_pages, page_size, head_dim/2] bytes, element 2j in the
+ *               low nibble of byte j, each nibble = code + 8 (codes in [-7, 7]);
+ *               k_int4_scale/v_int4_scale [num_pages, head_dim/int4_group] (scale_dtype).
+ *   INT4_RESIDUAL pages: k_int4r/v_int4r [num_pages, page_size, head_dim] bytes,
+ *               (base code + 8) | (residual code + 8) << 4; k_int4r_scale/v_int4r_scale
+ *               [num_pages, 2] f32 (base scale, residual scale).
+ *   Dequantised value = code * scale (INT4_RESIDUAL: base*s0 + residual*s1).
+ *
+ *   sm_scale     softmax scale (the reference uses 1/sqrt(head_dim), :323).
+ *   pages_per_split  pages one wave reduces before the cross-split merge; 0 = automatic.
+ */
+typedef struct {
+  int32_t batch, num_q_heads, num_kv_heads, head_dim, page_size, table_width;
+  int64_t num_pages;
+
+  const void* q; int32_t q_dtype; int64_t q_stride_b, q_stride_h;
+  void* out; int32_t out_dtype; int64_t out_stride_b, out_stride_h;
+
+  const int32_t* page_table;
+  const int32_t* page_counts;
+  const int32_t* page_tags;
+  uint8_t tag_map[8];
+  int32_t negative_ids;
+
+  const void* k_fp16; const void* v_fp16;
+  const void* k_fp8;  const void* v_fp8;
+  const void* k_int8; const void* v_int8;
+  const void* k_int4; const void* v_int4;
+  const void* k_int4r; const void* v_int4r;
+
+  const void* k_fp8_scale;  const void* v_fp8_scale;  int32_t fp8_scale_dtype;
+  const void* k_int8_scale; const void* v_int8_scale; int32_t int8_scale_dtype;
+  const void* k_int4_scale; const void* v_int4_scale; int32_t int4_scale_dtype; int32_t int4_group;
+  const float* k_int4r_scale; const float* v_int4r_scale;
+
+  float sm_scale;
+  int32_t pages_per_split;
+} iak_paged_decode_args;
+
+/* ABI version of the loaded library (IAK_ABI_VERSION). */
+int iak_abi_version(void);
+
+/* Static description of a status code. */
+const char* iak_status_string(iak_status status);
+
+/* Detail of the last non-OK status returned on the calling thread. */
+const char* iak_last_error(void);
+
+/* Bytes of device workspace iak_paged_decode needs for these arguments
+ * (0 when the whole reduction fits one split). */
+iak_status iak_paged_decode_workspace(const iak_paged_decode_args* args, size_t* bytes);
+
+/* Selected-page mixed-precision decode attention, split-K over pages with an
+ * LSE merge. `workspace` must hold iak_paged_decode_workspace() bytes (may be
+ * NULL when that is 0). `stream` is a hipStream_t (NULL = default stream). */
+iak_status iak_paged_decode(const iak_paged_decode_args* args, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* IAK_H */

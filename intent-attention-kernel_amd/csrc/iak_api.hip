@@ -1,0 +1,196 @@
+// C ABI of libiak: argument validation, split planning, workspace layout and
+// kernel launch for the selected-page decode (declared in include/iak.h).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "iak.h"
+#include "iak_internal.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+iak_status fail(iak_status st, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return st;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+const char* tag_name(int t) {
+  switch (t) {
+    case IAK_TAG_FP16: return "FP16";
+    case IAK_TAG_INT8: return "INT8";
+    case IAK_TAG_FP8: return "FP8";
+    case IAK_TAG_INT4: return "INT4";
+    case IAK_TAG_INT4_RESIDUAL: return "INT4_RESIDUAL";
+    default: return "SKIP";
+  }
+}
+
+constexpr size_t WS_ALIGN = 256;
+size_t round_up(size_t x) { return (x + WS_ALIGN - 1) / WS_ALIGN * WS_ALIGN; }
+
+struct Plan {
+  int G, splits, chunk;
+  size_t ws_m, ws_l, ws_acc, total;   // byte offsets / total
+};
+
+iak_status validate(const iak_paged_decode_args* a, Plan* plan) {
+  if (!a) return fail(IAK_EINVAL, "args is NULL");
+  if (a->batch < 0 || a->num_q_heads <= 0 || a->num_kv_heads <= 0 || a->table_width < 0 || a->num_pages < 0)
+    return fail(IAK_EINVAL, "negative or zero size (batch=%d, num_q_heads=%d, num_kv_heads=%d, table_width=%d, num_pages=%lld)",
+                a->batch, a->num_q_heads, a->num_kv_heads, a->table_width, (long long)a->num_pages);
+  if (a->num_q_heads % a->num_kv_heads != 0)
+    return fail(IAK_EINVAL, "num_q_heads %d is not a multiple of num_kv_heads %d", a->num_q_heads, a->num_kv_heads);
+  const int G = a->num_q_heads / a->num_kv_heads;
+  if (G > 16) return fail(IAK_ENOTSUP, "GQA group %d > 16 is not supported", G);
+  if (a->head_dim != 64 && a->head_dim != 128)
+    return fail(IAK_ENOTSUP, "head_dim %d is not supported (64 or 128)", a->head_dim);
+  if (a->page_size != 16) return fail(IAK_ENOTSUP, "page_size %d is not supported (16)", a->page_size);
+  if (a->num_pages > 0x7FFFFFFFLL) return fail(IAK_EINVAL, "num_pages %lld exceeds int32 page ids", (long long)a->num_pages);
+  if (a->q_dtype < 0 || a->q_dtype > 2 || a->out_dtype < 0 || a->out_dtype > 2)
+    return fail(IAK_EINVAL, "bad q/out dtype (%d, %d)", a->q_dtype, a->out_dtype);
+  if (!std::isfinite(a->sm_scale)) return fail(IAK_EINVAL, "sm_scale is not finite");
+  if (a->pages_per_split < 0 || a->pages_per_split > 64)
+    return fail(IAK_EINVAL, "pages_per_split %d outside [0, 64]", a->pages_per_split);
+  const long long rows = (long long)a->batch * a->num_kv_heads;
+  if (rows > 0) {
+    if (!a->q || !a->out) return fail(IAK_EINVAL, "q/out is NULL");
+    if (!a->page_table || !a->page_counts) return fail(IAK_EINVAL, "page_table/page_counts is NULL");
+    if (a->num_pages > 0 && !a->page_tags) return fail(IAK_EINVAL, "page_tags is NULL");
+  }
+  // every native precision reachable through the tag map needs its pools
+  for (int t = 0; t < 8; ++t) {
+    const int n = a->tag_map[t];
+    const void *k = nullptr, *v = nullptr, *ks = nullptr, *vs = nullptr;
+    int sd = IAK_DTYPE_F32;
+    switch (n) {
+      case IAK_TAG_FP16: k = a->k_fp16; v = a->v_fp16; ks = vs = k; break;
+      case IAK_TAG_FP8: k = a->k_fp8; v = a->v_fp8; ks = a->k_fp8_scale; vs = a->v_fp8_scale; sd = a->fp8_scale_dtype; break;
+      case IAK_TAG_INT8: k = a->k_int8; v = a->v_int8; ks = a->k_int8_scale; vs = a->v_int8_scale; sd = a->int8_scale_dtype; break;
+      case IAK_TAG_INT4: k = a->k_int4; v = a->v_int4; ks = a->k_int4_scale; vs = a->v_int4_scale; sd = a->int4_scale_dtype; break;
+      case IAK_TAG_INT4_RESIDUAL: k = a->k_int4r; v = a->v_int4r; ks = a->k_int4r_scale; vs = a->v_int4r_scale; break;
+      default: continue;   // SKIP or unknown: contributes nothing
+    }
+    if (!k || !v || !ks || !vs)
+      return fail(IAK_EINVAL, "tag %d maps to %s but its K/V pool or scales are NULL", t, tag_name(n));
+    if (!aligned16(k) || !aligned16(v))
+      return fail(IAK_EINVAL, "%s K/V pools must be 16-byte aligned", tag_name(n));
+    if (sd != IAK_DTYPE_F16 && sd != IAK_DTYPE_F32)
+      return fail(IAK_EINVAL, "%s scale dtype %d must be f16 or f32", tag_name(n), sd);
+    if (n == IAK_TAG_INT4) {
+      const int grp = a->int4_group, D = a->head_dim;
+      if (grp <= 0 || D % grp != 0 || grp % (D / 4) != 0)
+        return fail(IAK_ENOTSUP, "int4_group %d must divide head_dim %d and be a multiple of %d", grp, D, D / 4);
+    }
+  }
+
+  // split plan: enough waves to fill 256 CUs several times over
+  int chunk = a->pages_per_split;
+  const int W = a->table_width;
+  if (chunk == 0) {
+    chunk = 64;
+    while (chunk > 16 && rows * ((W + chunk - 1) / chunk) < 8192) chunk /= 2;
+  }
+  int splits = W > 0 ? (W + chunk - 1) / chunk : 1;
+  if (splits < 1) splits = 1;
+  if (rows * (long long)splits > 0x7FFFFFFFLL) return fail(IAK_EINVAL, "too many splits");
+  plan->G = G;
+  plan->splits = splits;
+  plan->chunk = chunk;
+  if (splits == 1) {
+    plan->ws_m = plan->ws_l = plan->ws_acc = plan->total = 0;
+  } else {
+    const size_t slots = (size_t)rows * splits * G;
+    plan->ws_m = 0;
+    plan->ws_l = round_up(slots * sizeof(float));
+    plan->ws_acc = plan->ws_l + round_up(slots * sizeof(float));
+    plan->total = plan->ws_acc + round_up(slots * a->head_dim * sizeof(float));
+  }
+  return IAK_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int iak_abi_version(void) { return IAK_ABI_VERSION; }
+
+const char* iak_status_string(iak_status s) {
+  switch (s) {
+    case IAK_OK: return "ok";
+    case IAK_EINVAL: return "invalid argument";
+    case IAK_ENOTSUP: return "unsupported configuration";
+    case IAK_EHIP: return "HIP runtime error";
+  }
+  return "unknown status";
+}
+
+const char* iak_last_error(void) { return g_err; }
+
+iak_status iak_paged_decode_workspace(const iak_paged_decode_args* args, size_t* bytes) {
+  if (!bytes) return fail(IAK_EINVAL, "bytes is NULL");
+  Plan plan;
+  const iak_status st = validate(args, &plan);
+  if (st != IAK_OK) return st;
+  *bytes = plan.total;
+  return IAK_OK;
+}
+
+iak_status iak_paged_decode(const iak_paged_decode_args* a, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+  Plan plan;
+  iak_status st = validate(a, &plan);
+  if (st != IAK_OK) return st;
+  const long long rows = (long long)a->batch * a->num_kv_heads;
+  if (rows == 0) return IAK_OK;
+  if (plan.total > 0 && (!workspace || workspace_bytes < plan.total))
+    return fail(IAK_EINVAL, "workspace of %zu bytes is smaller than the %zu bytes required", workspace_bytes, plan.total);
+
+  iak::KArgs k;
+  std::memset(&k, 0, sizeof(k));
+  k.B = a->batch; k.Hq = a->num_q_heads; k.Hkv = a->num_kv_heads; k.G = plan.G; k.D = a->head_dim;
+  k.W = a->table_width; k.NP = a->num_pages;
+  k.splits = plan.splits; k.chunk = plan.chunk; k.items = (int)(rows * plan.splits);
+  k.q = a->q; k.q_dtype = a->q_dtype; k.q_f32 = a->q_dtype != IAK_DTYPE_F16;
+  k.qsb = a->q_stride_b; k.qsh = a->q_stride_h;
+  k.out = a->out; k.out_dtype = a->out_dtype; k.osb = a->out_stride_b; k.osh = a->out_stride_h;
+  k.table = a->page_table; k.counts = a->page_counts; k.tags = a->page_tags;
+  uint64_t map = 0;
+  for (int t = 0; t < 8; ++t) {
+    int n = a->tag_map[t];
+    if (n != IAK_TAG_FP16 && n != IAK_TAG_INT8 && n != IAK_TAG_FP8 && n != IAK_TAG_INT4 && n != IAK_TAG_INT4_RESIDUAL)
+      n = IAK_TAG_SKIP;
+    map |= (uint64_t)n << (8 * t);
+  }
+  k.tagmap = map;
+  k.neg_wrap = a->negative_ids != 0;
+  k.k_fp16 = a->k_fp16; k.v_fp16 = a->v_fp16; k.k_fp8 = a->k_fp8; k.v_fp8 = a->v_fp8;
+  k.k_int8 = a->k_int8; k.v_int8 = a->v_int8; k.k_int4 = a->k_int4; k.v_int4 = a->v_int4;
+  k.k_int4r = a->k_int4r; k.v_int4r = a->v_int4r;
+  k.k_fp8_scale = a->k_fp8_scale; k.v_fp8_scale = a->v_fp8_scale; k.fp8_sd = a->fp8_scale_dtype;
+  k.k_int8_scale = a->k_int8_scale; k.v_int8_scale = a->v_int8_scale; k.int8_sd = a->int8_scale_dtype;
+  k.k_int4_scale = a->k_int4_scale; k.v_int4_scale = a->v_int4_scale; k.int4_sd = a->int4_scale_dtype;
+  k.int4_group = a->int4_group > 0 ? a->int4_group : a->head_dim;
+  k.k_int4r_scale = a->k_int4r_scale; k.v_int4r_scale = a->v_int4r_scale;
+  k.score_mult = a->sm_scale * 1.4426950408889634f;
+  if (plan.total > 0) {
+    char* ws = static_cast<char*>(workspace);
+    k.ws_m = reinterpret_cast<float*>(ws + plan.ws_m);
+    k.ws_l = reinterpret_cast<float*>(ws + plan.ws_l);
+    k.ws_acc = reinterpret_cast<float*>(ws + plan.ws_acc);
+  }
+  const hipError_t e = iak::launch_paged_decode(k, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(IAK_EHIP, "kernel launch failed: %s", hipGetErrorString(e));
+  return IAK_OK;
+}
+
+}  // extern "C"

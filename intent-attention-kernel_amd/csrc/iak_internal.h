@@ -1,0 +1,50 @@
+// Kernel-side argument block of libiak (device pointers and derived sizes),
+// built by the C ABI layer (iak_api.hip) from iak_paged_decode_args.
+#ifndef IAK_INTERNAL_H
+#define IAK_INTERNAL_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define IAK_WAVES_PER_BLOCK 4
+
+namespace iak {
+
+struct KArgs {
+  int B, Hq, Hkv, G, D, W;
+  int64_t NP;
+  int splits;   // splits per (batch, kv head) row
+  int chunk;    // pages per split (<= 64)
+  int items;    // B * Hkv * splits waves
+
+  const void* q; int q_dtype; int q_f32; int64_t qsb, qsh;
+  void* out; int out_dtype; int64_t osb, osh;
+
+  const int32_t* table;
+  const int32_t* counts;
+  const int32_t* tags;
+  uint64_t tagmap;   // byte t = native tag of caller tag t
+  int neg_wrap;
+
+  const void* k_fp16; const void* v_fp16;
+  const void* k_fp8; const void* v_fp8;
+  const void* k_int8; const void* v_int8;
+  const void* k_int4; const void* v_int4;
+  const void* k_int4r; const void* v_int4r;
+  const void* k_fp8_scale; const void* v_fp8_scale; int fp8_sd;
+  const void* k_int8_scale; const void* v_int8_scale; int int8_sd;
+  const void* k_int4_scale; const void* v_int4_scale; int int4_sd; int int4_group;
+  const float* k_int4r_scale; const float* v_int4r_scale;
+
+  float score_mult;   // sm_scale * log2(e)
+
+  float* ws_m;        // [B, Hkv, splits, G]
+  float* ws_l;        // [B, Hkv, splits, G]
+  float* ws_acc;      // [B, Hkv, splits, G, D]
+};
+
+hipError_t launch_paged_decode(const KArgs& k, hipStream_t stream);
+
+}  // namespace iak
+
+#endif

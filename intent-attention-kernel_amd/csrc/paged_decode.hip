@@ -1,0 +1,645 @@
+// Selected-page mixed-precision decode attention for gfx950 (MI355X).
+//
+// Reference semantics: fused_selected_quant_decode_reference
+// (src/intent_attention/fused_selected_quant_decode.py:267-336): for each
+// (batch, head) walk the page list, skip SKIP pages (no softmax mass), dequantise
+// each page (code * scale), scores q.k / sqrt(D), softmax over every visited
+// token, output sum(p v) / sum(p) (0 when nothing was visited).
+//
+// Work decomposition
+//   One wave64 reduces one split: up to `chunk` (<= 64) consecutive entries of
+//   one page-table row (batch b, KV head hk). Lane i reads entry i's page id
+//   and tag; ballots sort the split's pages into one list per precision so
+//   every page loop below runs wave-uniform code. The G = Hq / Hkv query heads
+//   of the row share every K/V byte the wave loads (GQA): they are the N
+//   columns of the MFMA products. Splits write (m, l, acc) partials; a merge
+//   kernel combines them with the log-sum-exp rule. A row that fits one split
+//   writes the output directly.
+//
+// Per page (16 tokens) and wave, lane = c + 16*g (c, g = lane % 16, lane / 16):
+//   scores  S^T[16 tok x 16 heads] = K[16 tok x D] . Q^T[D x 16 heads]
+//           v_mfma_f32_16x16x32_f16, D/32 k-steps. A operand: lane holds token c,
+//           dims (D/4)g + 8i .. +7 at step i (K dequantised to f16 in registers);
+//           B operand: lane holds head c (zero for c >= G), the same dims.
+//           Result: lane holds head c, tokens 4g .. 4g+3.
+//   softmax exp2 domain; the running max per head is shared by the 4 lane groups
+//           (two cross-lane max steps per page) and only moves when a page
+//           exceeds it by more than 8 (2^8 head-room in p), so the accumulator
+//           rescale is rare.
+//   values  O^T[D x 16 heads] += V^T[D x 16 tok] . P^T[16 tok x 16 heads]
+//           v_mfma_f32_16x16x16_f16, D/16 row blocks. A operand: lane holds dim
+//           (D/16)c + mb of tokens 4g..4g+3; B operand: p of head c, tokens
+//           4g..4g+3 -- exactly the score result layout, converted to f16.
+//           Accumulator: lane holds head c, dims (D/4)g .. (D/4)g + D/4 - 1.
+//   Per-page scalar scales fold into the score multiplier (K) and into p (V);
+//   INT4 group scales and INT4_RESIDUAL values are applied in f16 during
+//   dequantisation.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "iak.h"
+#include "iak_internal.h"
+
+namespace iak {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+
+constexpr int PS = 16;
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float RESCALE_SLACK = 8.0f;      // p <= 2^8 between rescales
+constexpr uint32_t MAGIC_I8 = 0x64646464u;  // f16 0x64xx = 1024 + xx
+constexpr uint32_t MAGIC_I4 = 0x64006400u;
+
+__device__ __forceinline__ uint32_t bits(h2 v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
+__device__ __forceinline__ h2 splat2(_Float16 x) { return h2{x, x}; }
+
+__device__ __forceinline__ h8 make_h8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  u4 v = {a, b, c, d};
+  return __builtin_bit_cast(h8, v);
+}
+__device__ __forceinline__ h4 make_h4(uint32_t a, uint32_t b) {
+  u2 v = {a, b};
+  return __builtin_bit_cast(h4, v);
+}
+
+// (lo16(x), lo16(y)) and (hi16(x), hi16(y)) as one dword
+__device__ __forceinline__ uint32_t pack_lo(uint32_t x, uint32_t y) {
+  return __builtin_amdgcn_perm(y, x, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t pack_hi(uint32_t x, uint32_t y) {
+  return __builtin_amdgcn_perm(y, x, 0x07060302u);
+}
+
+// Four signed int8 -> two f16 pairs (b0,b1), (b2,b3), exactly.
+__device__ __forceinline__ void i8x4_to_f16(uint32_t x, uint32_t& lo, uint32_t& hi) {
+  const uint32_t u = x ^ 0x80808080u;                          // b + 128
+  const h2 off = splat2((_Float16)-1152.0f);                   // 1024 + 128
+  lo = bits(as_h2(__builtin_amdgcn_perm(MAGIC_I8, u, 0x04010400u)) + off);
+  hi = bits(as_h2(__builtin_amdgcn_perm(MAGIC_I8, u, 0x04030402u)) + off);
+}
+
+// Four e4m3fn bytes -> two f16 pairs (b0,b1), (b2,b3), exactly.
+__device__ __forceinline__ void fp8x4_to_f16(uint32_t x, uint32_t& lo, uint32_t& hi) {
+  lo = bits(__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x, 1.0f, false));
+  hi = bits(__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x, 1.0f, true));
+}
+
+// Nibbles at bits 0-3 and 16-19 of y (code + 8) -> f16 pair of codes, exactly.
+__device__ __forceinline__ h2 nib_pair(uint32_t y) {
+  return as_h2((y & 0x000F000Fu) | MAGIC_I4) + splat2((_Float16)-1032.0f);
+}
+
+// Eight packed INT4 codes (element j = nibble j) -> four f16 pairs in element
+// order, multiplied by scale s.
+__device__ __forceinline__ void i4x8_to_f16(uint32_t x, h2 s, uint32_t o[4]) {
+  const h2 p04 = nib_pair(x) * s;         // (e0, e4)
+  const h2 p15 = nib_pair(x >> 4) * s;    // (e1, e5)
+  const h2 p26 = nib_pair(x >> 8) * s;    // (e2, e6)
+  const h2 p37 = nib_pair(x >> 12) * s;   // (e3, e7)
+  o[0] = pack_lo(bits(p04), bits(p15));
+  o[1] = pack_lo(bits(p26), bits(p37));
+  o[2] = pack_hi(bits(p04), bits(p15));
+  o[3] = pack_hi(bits(p26), bits(p37));
+}
+
+// Four INT4_RESIDUAL bytes (base | resid<<4) -> two f16 pairs of base*s0 + resid*s1.
+__device__ __forceinline__ void i4r_x4_to_f16(uint32_t x, h2 s0, h2 s1, uint32_t& lo, uint32_t& hi) {
+  const h2 b02 = nib_pair(x), r02 = nib_pair(x >> 4);
+  const h2 b13 = nib_pair(x >> 8), r13 = nib_pair(x >> 12);
+  const h2 v02 = __builtin_elementwise_fma(r02, s1, b02 * s0);
+  const h2 v13 = __builtin_elementwise_fma(r13, s1, b13 * s0);
+  lo = pack_lo(bits(v02), bits(v13));
+  hi = pack_hi(bits(v02), bits(v13));
+}
+
+__device__ __forceinline__ float xmax16_32(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16));
+  return fmaxf(v, __shfl_xor(v, 32));
+}
+__device__ __forceinline__ float xsum16_32(float v) {
+  v += __shfl_xor(v, 16);
+  return v + __shfl_xor(v, 32);
+}
+
+__device__ __forceinline__ float load_scale(const void* p, int64_t idx, int dtype) {
+  if (dtype == IAK_DTYPE_F32) return reinterpret_cast<const float*>(p)[idx];
+  return (float)reinterpret_cast<const _Float16*>(p)[idx];
+}
+
+// --------------------------------------------------------------------------- //
+// Raw page data as each lane loads it, per precision and head_dim.
+// --------------------------------------------------------------------------- //
+
+template <int D> struct Raw16 {   // FP16: K token c dims (D/4)g..; V tokens 4g+k dims (D/16)c..
+  u4 k[D / 32];                    // D/4 halves = D/32 u4
+  uint32_t v[4][D / 32];           // D/16 halves per token = D/32 dwords
+};
+template <int D> struct Raw8 {    // FP8 / INT8 / INT4_RESIDUAL (one byte per element)
+  uint32_t k[D / 16];              // D/4 bytes
+  uint32_t v[4][D / 64 > 0 ? D / 64 : 1];  // D/16 bytes per token
+};
+template <int D> struct Raw4 {    // INT4 (half a byte per element)
+  uint32_t k[D / 32];              // D/8 bytes
+  uint32_t v[4];                   // D/32 bytes per token (<= 4)
+};
+
+template <int D> __device__ __forceinline__ void load16(Raw16<D>& r, const _Float16* kp, const _Float16* vp,
+                                                       int c, int g) {
+  const u4* kr = reinterpret_cast<const u4*>(kp + c * D + (D / 4) * g);
+#pragma unroll
+  for (int i = 0; i < D / 32; ++i) r.k[i] = __builtin_nontemporal_load(kr + i);
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const _Float16* row = vp + (4 * g + t) * D + (D / 16) * c;
+    if constexpr (D == 128) {
+      u4 x = __builtin_nontemporal_load(reinterpret_cast<const u4*>(row));
+      r.v[t][0] = x[0]; r.v[t][1] = x[1]; r.v[t][2] = x[2]; r.v[t][3] = x[3];
+    } else {
+      u2 x = __builtin_nontemporal_load(reinterpret_cast<const u2*>(row));
+      r.v[t][0] = x[0]; r.v[t][1] = x[1];
+    }
+  }
+}
+
+template <int D> __device__ __forceinline__ void load8(Raw8<D>& r, const uint8_t* kp, const uint8_t* vp,
+                                                      int c, int g) {
+  const u4* kr = reinterpret_cast<const u4*>(kp + c * D + (D / 4) * g);
+#pragma unroll
+  for (int i = 0; i < D / 64; ++i) {
+    u4 x = __builtin_nontemporal_load(kr + i);
+    r.k[4 * i + 0] = x[0]; r.k[4 * i + 1] = x[1]; r.k[4 * i + 2] = x[2]; r.k[4 * i + 3] = x[3];
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const uint8_t* row = vp + (4 * g + t) * D + (D / 16) * c;
+    if constexpr (D == 128) {
+      u2 x = __builtin_nontemporal_load(reinterpret_cast<const u2*>(row));
+      r.v[t][0] = x[0]; r.v[t][1] = x[1];
+    } else {
+      r.v[t][0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(row));
+    }
+  }
+}
+
+template <int D> __device__ __forceinline__ void load4(Raw4<D>& r, const uint8_t* kp, const uint8_t* vp,
+                                                      int c, int g) {
+  const uint8_t* krow = kp + c * (D / 2) + (D / 8) * g;
+  if constexpr (D == 128) {
+    u4 x = __builtin_nontemporal_load(reinterpret_cast<const u4*>(krow));
+    r.k[0] = x[0]; r.k[1] = x[1]; r.k[2] = x[2]; r.k[3] = x[3];
+  } else {
+    u2 x = __builtin_nontemporal_load(reinterpret_cast<const u2*>(krow));
+    r.k[0] = x[0]; r.k[1] = x[1];
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const uint8_t* row = vp + (4 * g + t) * (D / 2) + (D / 32) * c;
+    if constexpr (D == 128) {
+      r.v[t] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(row));
+    } else {
+      r.v[t] = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(row));
+    }
+  }
+}
+
+// --------------------------------------------------------------------------- //
+// Wave state and the per-page update shared by all precisions.
+// --------------------------------------------------------------------------- //
+
+template <int D, bool QF32> struct Wave {
+  h8 qhi[D / 32];
+  h8 qlo[QF32 ? D / 32 : 1];
+  f4 acc[D / 16];
+  float m;   // running max of head c (exp2 domain), equal in the 4 lane groups
+  float l;   // partial denominator over this lane's tokens
+};
+
+template <int D, bool QF32>
+__device__ __forceinline__ f4 scores(const Wave<D, QF32>& w, const h8 (&ka)[D / 32]) {
+  f4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < D / 32; ++i) {
+    s = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[i], w.qhi[i], s, 0, 0, 0);
+    if constexpr (QF32) s = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[i], w.qlo[i], s, 0, 0, 0);
+  }
+  return s;
+}
+
+// Online-softmax update for one page whose raw scores are `s` (lane: head c,
+// tokens 4g..4g+3); `smul` = softmax scale * log2(e) * K scale; `vmul` = V page
+// scale (1 when V carries its own scale). Returns the P operand (f16).
+template <int D, bool QF32>
+__device__ __forceinline__ h4 softmax_step(Wave<D, QF32>& w, f4 s, float smul, float vmul) {
+  s *= smul;
+  float pm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+  pm = xmax16_32(pm);
+  const bool grow = pm > w.m + RESCALE_SLACK;
+  if (__builtin_amdgcn_ballot_w64(grow)) {        // wave-uniform, rare after the first page
+    const float mn = grow ? pm : w.m;
+    const float alpha = __builtin_amdgcn_exp2f(w.m - mn);   // 0 on the first page (m = -inf)
+    w.l *= alpha;
+#pragma unroll
+    for (int mb = 0; mb < D / 16; ++mb) w.acc[mb] *= alpha;
+    w.m = mn;
+  }
+  float p0 = __builtin_amdgcn_exp2f(s[0] - w.m);
+  float p1 = __builtin_amdgcn_exp2f(s[1] - w.m);
+  float p2 = __builtin_amdgcn_exp2f(s[2] - w.m);
+  float p3 = __builtin_amdgcn_exp2f(s[3] - w.m);
+  w.l += (p0 + p1) + (p2 + p3);
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  const h2 a = __builtin_convertvector((f2{p0, p1} * vmul), h2);
+  const h2 b = __builtin_convertvector((f2{p2, p3} * vmul), h2);
+  return make_h4(bits(a), bits(b));
+}
+
+// V operand of row block mb from four f16-pair rows vt[t][w] = dims (2w, 2w+1)
+// of token 4g+t: the dim (D/16)c + mb of tokens 4g .. 4g+3.
+template <int D>
+__device__ __forceinline__ h4 rows_to_a(const uint32_t (&vt)[4][D / 32], int mb) {
+  const int wd = mb >> 1;
+  if (mb & 1) return make_h4(pack_hi(vt[0][wd], vt[1][wd]), pack_hi(vt[2][wd], vt[3][wd]));
+  return make_h4(pack_lo(vt[0][wd], vt[1][wd]), pack_lo(vt[2][wd], vt[3][wd]));
+}
+
+// O^T += V^T P^T, one v_mfma_f32_16x16x16f16 per row block of 16 dims.
+template <int D, bool QF32>
+__device__ __forceinline__ void pv(Wave<D, QF32>& w, const h4 (&va)[D / 16], h4 pb) {
+#pragma unroll
+  for (int mb = 0; mb < D / 16; ++mb)
+    w.acc[mb] = __builtin_amdgcn_mfma_f32_16x16x16f16(va[mb], pb, w.acc[mb], 0, 0, 0);
+}
+
+template <int D, bool QF32>
+__device__ __forceinline__ void pv_rows(Wave<D, QF32>& w, const uint32_t (&vt)[4][D / 32], h4 pb) {
+  h4 va[D / 16];
+#pragma unroll
+  for (int mb = 0; mb < D / 16; ++mb) va[mb] = rows_to_a<D>(vt, mb);
+  pv(w, va, pb);
+}
+
+// --------------------------------------------------------------------------- //
+// Per-precision page compute
+// --------------------------------------------------------------------------- //
+
+template <int D, bool QF32>
+__device__ __forceinline__ void page_fp16(Wave<D, QF32>& w, const Raw16<D>& r, float smul) {
+  h8 ka[D / 32];
+#pragma unroll
+  for (int i = 0; i < D / 32; ++i) ka[i] = __builtin_bit_cast(h8, r.k[i]);
+  const h4 pb = softmax_step(w, scores(w, ka), smul, 1.0f);
+  pv_rows(w, r.v, pb);
+}
+
+template <int D, bool QF32, int TAG>
+__device__ __forceinline__ void page_byte(Wave<D, QF32>& w, const Raw8<D>& r, float smul, float vmul,
+                                          h2 ks0, h2 ks1, h2 vs0, h2 vs1) {
+  h8 ka[D / 32];
+#pragma unroll
+  for (int i = 0; i < D / 32; ++i) {
+    uint32_t o[4];
+    if constexpr (TAG == IAK_TAG_FP8) {
+      fp8x4_to_f16(r.k[2 * i], o[0], o[1]); fp8x4_to_f16(r.k[2 * i + 1], o[2], o[3]);
+    } else if constexpr (TAG == IAK_TAG_INT8) {
+      i8x4_to_f16(r.k[2 * i], o[0], o[1]); i8x4_to_f16(r.k[2 * i + 1], o[2], o[3]);
+    } else {
+      i4r_x4_to_f16(r.k[2 * i], ks0, ks1, o[0], o[1]); i4r_x4_to_f16(r.k[2 * i + 1], ks0, ks1, o[2], o[3]);
+    }
+    ka[i] = make_h8(o[0], o[1], o[2], o[3]);
+  }
+  const h4 pb = softmax_step(w, scores(w, ka), smul, vmul);
+  uint32_t vt[4][D / 32];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+#pragma unroll
+    for (int j = 0; j < D / 64; ++j) {
+      if constexpr (TAG == IAK_TAG_FP8) fp8x4_to_f16(r.v[t][j], vt[t][2 * j], vt[t][2 * j + 1]);
+      else if constexpr (TAG == IAK_TAG_INT8) i8x4_to_f16(r.v[t][j], vt[t][2 * j], vt[t][2 * j + 1]);
+      else i4r_x4_to_f16(r.v[t][j], vs0, vs1, vt[t][2 * j], vt[t][2 * j + 1]);
+    }
+  }
+  pv_rows(w, vt, pb);
+}
+
+template <int D, bool QF32>
+__device__ __forceinline__ void page_int4(Wave<D, QF32>& w, const Raw4<D>& r, float smul, h2 ks, h2 vs) {
+  h8 ka[D / 32];
+#pragma unroll
+  for (int i = 0; i < D / 32; ++i) {
+    uint32_t o[4];
+    i4x8_to_f16(r.k[i], ks, o);
+    ka[i] = make_h8(o[0], o[1], o[2], o[3]);
+  }
+  const h4 pb = softmax_step(w, scores(w, ka), smul, 1.0f);
+  // V: tokens (0,1) and (2,3) interleaved per 16 bits, then one nibble per dim
+  // gives the (t0, t1) and (t2, t3) halves of the A operand of that dim directly.
+  h4 va[D / 16];
+  if constexpr (D == 128) {
+    const uint32_t y01l = pack_lo(r.v[0], r.v[1]), y01h = pack_hi(r.v[0], r.v[1]);
+    const uint32_t y23l = pack_lo(r.v[2], r.v[3]), y23h = pack_hi(r.v[2], r.v[3]);
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      const uint32_t y01 = d < 4 ? y01l : y01h, y23 = d < 4 ? y23l : y23h;
+      const int sh = 4 * (d & 3);
+      va[d] = make_h4(bits(nib_pair(y01 >> sh) * vs), bits(nib_pair(y23 >> sh) * vs));
+    }
+  } else {   // D == 64: two bytes (4 dims) per token
+    const uint32_t y01 = pack_lo(r.v[0], r.v[1]), y23 = pack_lo(r.v[2], r.v[3]);
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+      va[d] = make_h4(bits(nib_pair(y01 >> (4 * d)) * vs), bits(nib_pair(y23 >> (4 * d)) * vs));
+  }
+  pv(w, va, pb);
+}
+
+// --------------------------------------------------------------------------- //
+// The split kernel
+// --------------------------------------------------------------------------- //
+
+struct Split {
+  int b, hk, split, n;   // n = pages in this split
+};
+
+__device__ __forceinline__ int take(uint64_t& mask) {
+  const int idx = __builtin_ctzll(mask);
+  mask &= mask - 1;
+  return idx;
+}
+
+template <int D, bool QF32>
+__device__ void write_result(const KArgs& a, const Split& sp, Wave<D, QF32>& w, int c, int g) {
+  const float l = xsum16_32(w.l);
+  const int h = sp.hk * a.G + c;
+  if (a.splits == 1) {
+    if (c >= a.G) return;
+    const float inv = l > 0.f ? 1.0f / l : 0.0f;
+    const int64_t base = (int64_t)sp.b * a.osb + (int64_t)h * a.osh + (D / 4) * g;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v[D / 16];
+#pragma unroll
+      for (int mb = 0; mb < D / 16; ++mb) v[mb] = w.acc[mb][r] * inv;
+      const int64_t o = base + (D / 16) * r;
+      if (a.out_dtype == IAK_DTYPE_F32) {
+        float* op = reinterpret_cast<float*>(a.out) + o;
+#pragma unroll
+        for (int mb = 0; mb < D / 16; ++mb) op[mb] = v[mb];
+      } else if (a.out_dtype == IAK_DTYPE_F16) {
+        _Float16* op = reinterpret_cast<_Float16*>(a.out) + o;
+#pragma unroll
+        for (int mb = 0; mb < D / 16; ++mb) op[mb] = (_Float16)v[mb];
+      } else {
+        __bf16* op = reinterpret_cast<__bf16*>(a.out) + o;
+#pragma unroll
+        for (int mb = 0; mb < D / 16; ++mb) op[mb] = (__bf16)v[mb];
+      }
+    }
+    return;
+  }
+  if (c >= a.G) return;
+  const int64_t slot = (((int64_t)sp.b * a.Hkv + sp.hk) * a.splits + sp.split) * a.G + c;
+  if (g == 0) { a.ws_m[slot] = w.m; a.ws_l[slot] = l; }
+  float* op = a.ws_acc + slot * D + (D / 4) * g;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+#pragma unroll
+    for (int mb = 0; mb < D / 16; ++mb) op[(D / 16) * r + mb] = w.acc[mb][r];
+  }
+}
+
+template <int D, bool QF32>
+__global__ __launch_bounds__(64 * IAK_WAVES_PER_BLOCK) void paged_decode_kernel(const KArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int wid = blockIdx.x * IAK_WAVES_PER_BLOCK + (threadIdx.x >> 6);
+  if (wid >= a.items) return;
+  const int c = lane & 15, g = lane >> 4;
+
+  Split sp;
+  {
+    const int unit = wid / a.splits;
+    sp.split = wid - unit * a.splits;
+    sp.b = unit / a.Hkv;
+    sp.hk = unit - sp.b * a.Hkv;
+    int cnt = a.counts[unit];
+    cnt = cnt < 0 ? 0 : (cnt > a.W ? a.W : cnt);
+    const int start = sp.split * a.chunk;
+    sp.n = cnt - start < a.chunk ? cnt - start : a.chunk;
+    if (sp.n < 0) sp.n = 0;
+  }
+
+  // Page ids and native tags: lane i holds entry i of the split.
+  int pid = -1, tag = IAK_TAG_SKIP;
+  if (lane < sp.n) {
+    const int64_t unit = (int64_t)sp.b * a.Hkv + sp.hk;
+    pid = a.table[unit * a.W + (int64_t)sp.split * a.chunk + lane];
+    if (a.neg_wrap && pid < 0 && (int64_t)pid >= -a.NP) pid = (int)((int64_t)pid + a.NP);
+    if (pid >= 0 && (int64_t)pid < a.NP) {
+      const int t = a.tags[pid];
+      tag = (t >= 0 && t < 8) ? (int)((a.tagmap >> (8 * t)) & 0xFFu) : IAK_TAG_SKIP;
+    } else {
+      pid = -1;
+    }
+  }
+
+  Wave<D, QF32> w;
+  w.m = -__builtin_inff();
+  w.l = 0.f;
+#pragma unroll
+  for (int mb = 0; mb < D / 16; ++mb) w.acc[mb] = f4{0.f, 0.f, 0.f, 0.f};
+  {
+    // Q operand: head c (zero for padding columns), dims (D/4)g + 8i .. +7.
+    const int h = sp.hk * a.G + c;
+    const bool live = c < a.G;
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) {
+      float qv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qv[e] = 0.f;
+      if (live) {
+        const int64_t off = (int64_t)sp.b * a.qsb + (int64_t)h * a.qsh + (D / 4) * g + 8 * i;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if (a.q_dtype == IAK_DTYPE_F16) qv[e] = (float)reinterpret_cast<const _Float16*>(a.q)[off + e];
+          else if (a.q_dtype == IAK_DTYPE_F32) qv[e] = reinterpret_cast<const float*>(a.q)[off + e];
+          else qv[e] = (float)reinterpret_cast<const __bf16*>(a.q)[off + e];
+        }
+      }
+      h8 hi, lo;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        hi[e] = (_Float16)qv[e];
+        lo[e] = (_Float16)(qv[e] - (float)hi[e]);
+      }
+      w.qhi[i] = hi;
+      if constexpr (QF32) w.qlo[i] = lo;
+    }
+  }
+
+  const float smul0 = a.score_mult;
+
+  // ---- FP16 pages ----
+  uint64_t mask = __builtin_amdgcn_ballot_w64(tag == IAK_TAG_FP16);
+  if (mask) {
+    const _Float16* kpool = reinterpret_cast<const _Float16*>(a.k_fp16);
+    const _Float16* vpool = reinterpret_cast<const _Float16*>(a.v_fp16);
+    Raw16<D> cur, nxt;
+    int p = __builtin_amdgcn_readlane(pid, take(mask));
+    load16<D>(cur, kpool + (int64_t)p * PS * D, vpool + (int64_t)p * PS * D, c, g);
+    while (true) {
+      const bool more = mask != 0;
+      if (more) {
+        p = __builtin_amdgcn_readlane(pid, take(mask));
+        load16<D>(nxt, kpool + (int64_t)p * PS * D, vpool + (int64_t)p * PS * D, c, g);
+      }
+      page_fp16(w, cur, smul0);
+      if (!more) break;
+      cur = nxt;
+    }
+  }
+
+  // ---- FP8 / INT8 / INT4_RESIDUAL pages (one byte per element) ----
+#define IAK_BYTE_CLASS(TAGV, KPOOL, VPOOL)                                                        \
+  mask = __builtin_amdgcn_ballot_w64(tag == TAGV);                                                 \
+  if (mask) {                                                                                      \
+    const uint8_t* kpool = reinterpret_cast<const uint8_t*>(KPOOL);                                \
+    const uint8_t* vpool = reinterpret_cast<const uint8_t*>(VPOOL);                                \
+    Raw8<D> cur, nxt;                                                                              \
+    float ksc, vsc, ksn = 0.f, vsn = 0.f, ks1 = 0.f, vs1 = 0.f, ks1n = 0.f, vs1n = 0.f;             \
+    int p = __builtin_amdgcn_readlane(pid, take(mask));                                            \
+    load8<D>(cur, kpool + (int64_t)p * PS * D, vpool + (int64_t)p * PS * D, c, g);                \
+    if constexpr (TAGV == IAK_TAG_FP8) {                                                           \
+      ksc = load_scale(a.k_fp8_scale, p, a.fp8_sd); vsc = load_scale(a.v_fp8_scale, p, a.fp8_sd);  \
+    } else if constexpr (TAGV == IAK_TAG_INT8) {                                                   \
+      ksc = load_scale(a.k_int8_scale, p, a.int8_sd); vsc = load_scale(a.v_int8_scale, p, a.int8_sd); \
+    } else {                                                                                       \
+      ksc = a.k_int4r_scale[2 * (int64_t)p]; ks1 = a.k_int4r_scale[2 * (int64_t)p + 1];            \
+      vsc = a.v_int4r_scale[2 * (int64_t)p]; vs1 = a.v_int4r_scale[2 * (int64_t)p + 1];            \
+    }                                                                                              \
+    while (true) {                                                                                 \
+      const bool more = mask != 0;                                                                 \
+      if (more) {                                                                                  \
+        p = __builtin_amdgcn_readlane(pid, take(mask));                                            \
+        load8<D>(nxt, kpool + (int64_t)p * PS * D, vpool + (int64_t)p * PS * D, c, g);            \
+        if constexpr (TAGV == IAK_TAG_FP8) {                                                       \
+          ksn = load_scale(a.k_fp8_scale, p, a.fp8_sd); vsn = load_scale(a.v_fp8_scale, p, a.fp8_sd); \
+        } else if constexpr (TAGV == IAK_TAG_INT8) {                                               \
+          ksn = load_scale(a.k_int8_scale, p, a.int8_sd); vsn = load_scale(a.v_int8_scale, p, a.int8_sd); \
+        } else {                                                                                   \
+          ksn = a.k_int4r_scale[2 * (int64_t)p]; ks1n = a.k_int4r_scale[2 * (int64_t)p + 1];       \
+          vsn = a.v_int4r_scale[2 * (int64_t)p]; vs1n = a.v_int4r_scale[2 * (int64_t)p + 1];       \
+        }                                                                                          \
+      }                                                                                            \
+      if constexpr (TAGV == IAK_TAG_INT4_RESIDUAL) {                                               \
+        page_byte<D, QF32, TAGV>(w, cur, smul0, 1.0f, splat2((_Float16)ksc), splat2((_Float16)ks1), \
+                                 splat2((_Float16)vsc), splat2((_Float16)vs1));                    \
+      } else {                                                                                     \
+        const h2 one = splat2((_Float16)1.0f);                                                     \
+        page_byte<D, QF32, TAGV>(w, cur, smul0 * ksc, vsc, one, one, one, one);                    \
+      }                                                                                            \
+      if (!more) break;                                                                            \
+      cur = nxt; ksc = ksn; vsc = vsn; ks1 = ks1n; vs1 = vs1n;                                     \
+    }                                                                                              \
+  }
+
+  IAK_BYTE_CLASS(IAK_TAG_FP8, a.k_fp8, a.v_fp8)
+  IAK_BYTE_CLASS(IAK_TAG_INT8, a.k_int8, a.v_int8)
+  IAK_BYTE_CLASS(IAK_TAG_INT4_RESIDUAL, a.k_int4r, a.v_int4r)
+#undef IAK_BYTE_CLASS
+
+  // ---- INT4 pages (group scales: lane's K dims are group (D/4)g / grp, V dims (D/16)c / grp) ----
+  mask = __builtin_amdgcn_ballot_w64(tag == IAK_TAG_INT4);
+  if (mask) {
+    const uint8_t* kpool = reinterpret_cast<const uint8_t*>(a.k_int4);
+    const uint8_t* vpool = reinterpret_cast<const uint8_t*>(a.v_int4);
+    const int ngroups = D / a.int4_group;
+    const int kgrp = ((D / 4) * g) / a.int4_group;
+    const int vgrp = ((D / 16) * c) / a.int4_group;
+    Raw4<D> cur, nxt;
+    int p = __builtin_amdgcn_readlane(pid, take(mask));
+    load4<D>(cur, kpool + (int64_t)p * PS * (D / 2), vpool + (int64_t)p * PS * (D / 2), c, g);
+    float ksc = load_scale(a.k_int4_scale, (int64_t)p * ngroups + kgrp, a.int4_sd);
+    float vsc = load_scale(a.v_int4_scale, (int64_t)p * ngroups + vgrp, a.int4_sd);
+    float ksn = 0.f, vsn = 0.f;
+    while (true) {
+      const bool more = mask != 0;
+      if (more) {
+        p = __builtin_amdgcn_readlane(pid, take(mask));
+        load4<D>(nxt, kpool + (int64_t)p * PS * (D / 2), vpool + (int64_t)p * PS * (D / 2), c, g);
+        ksn = load_scale(a.k_int4_scale, (int64_t)p * ngroups + kgrp, a.int4_sd);
+        vsn = load_scale(a.v_int4_scale, (int64_t)p * ngroups + vgrp, a.int4_sd);
+      }
+      page_int4(w, cur, smul0, splat2((_Float16)ksc), splat2((_Float16)vsc));
+      if (!more) break;
+      cur = nxt; ksc = ksn; vsc = vsn;
+    }
+  }
+
+  write_result(a, sp, w, c, g);
+}
+
+// --------------------------------------------------------------------------- //
+// Cross-split merge: one wave per (batch, query head).
+// --------------------------------------------------------------------------- //
+
+template <int D>
+__global__ __launch_bounds__(256) void splitk_merge_kernel(const KArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int bh = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (bh >= a.B * a.Hq) return;
+  const int b = bh / a.Hq, h = bh - b * a.Hq;
+  const int hk = h / a.G, c = h - hk * a.G;
+  const int64_t first = (((int64_t)b * a.Hkv + hk) * a.splits) * a.G + c;   // slot of split 0
+  float M = -__builtin_inff();
+  for (int s = 0; s < a.splits; ++s) M = fmaxf(M, a.ws_m[first + (int64_t)s * a.G]);
+  constexpr int PER = D / 64;   // dims per lane
+  float o[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) o[j] = 0.f;
+  float L = 0.f;
+  if (M > -__builtin_inff()) {
+    for (int s = 0; s < a.splits; ++s) {
+      const int64_t slot = first + (int64_t)s * a.G;
+      const float ms = a.ws_m[slot];
+      const float wgt = __builtin_amdgcn_exp2f(ms - M);   // 0 for empty splits (m = -inf)
+      L += wgt * a.ws_l[slot];
+      const float* ap = a.ws_acc + slot * D + PER * lane;
+#pragma unroll
+      for (int j = 0; j < PER; ++j) o[j] += wgt * ap[j];
+    }
+  }
+  const float inv = L > 0.f ? 1.0f / L : 0.f;
+  const int64_t base = (int64_t)b * a.osb + (int64_t)h * a.osh + PER * lane;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const float v = o[j] * inv;
+    if (a.out_dtype == IAK_DTYPE_F32) reinterpret_cast<float*>(a.out)[base + j] = v;
+    else if (a.out_dtype == IAK_DTYPE_F16) reinterpret_cast<_Float16*>(a.out)[base + j] = (_Float16)v;
+    else reinterpret_cast<__bf16*>(a.out)[base + j] = (__bf16)v;
+  }
+}
+
+template <int D, bool QF32>
+hipError_t launch_decode(const KArgs& k, hipStream_t stream) {
+  const int blocks = (k.items + IAK_WAVES_PER_BLOCK - 1) / IAK_WAVES_PER_BLOCK;
+  hipLaunchKernelGGL((paged_decode_kernel<D, QF32>), dim3(blocks), dim3(64 * IAK_WAVES_PER_BLOCK), 0,
+                     stream, k);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || k.splits == 1) return e;
+  const int mblocks = (k.B * k.Hq + 3) / 4;
+  hipLaunchKernelGGL((splitk_merge_kernel<D>), dim3(mblocks), dim3(256), 0, stream, k);
+  return hipGetLastError();
+}
+
+hipError_t launch_paged_decode(const KArgs& k, hipStream_t stream) {
+  if (k.D == 128) return k.q_f32 ? launch_decode<128, true>(k, stream) : launch_decode<128, false>(k, stream);
+  return k.q_f32 ? launch_decode<64, true>(k, stream) : launch_decode<64, false>(k, stream);
+}
+
+}  // namespace iak

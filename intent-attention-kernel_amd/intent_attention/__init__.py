@@ -1,0 +1,53 @@
+"""MI355X-native selected-quant paged decode (drop-in for the hot path of
+manishklach/intent-attention-kernel).
+
+Host-side policy (router, precision policy, kernel metadata) runs on the CPU
+as in the reference; the decode itself runs only in libiak.so, the HIP/gfx950
+library behind the C ABI in include/iak.h.
+"""
+from .block_metadata import SELECTED_POLICIES, BlockLayout, BlockPolicy, SemanticBlock
+from .block_router import (
+    BlockDecision,
+    BlockRouter,
+    RoutedBlock,
+    RouterConfig,
+    compute_block_scores,
+    routing_to_kernel_metadata,
+)
+from .fused_selected_quant_decode import (
+    FusedDecodeConfig,
+    FusedKVPrecision,
+    fused_selected_quant_decode,
+    is_native_available,
+    metadata_to_kernel_tensors,
+)
+from .intent_quant import (
+    IntentQuantizer,
+    KVPrecision,
+    QuantPolicy,
+    compute_quant_error,
+    fake_dequantize_tensor,
+    fake_quantize_tensor,
+)
+from .intent_quant_decode import (
+    IntentQuantKernelConfig,
+    TritonKVPrecision,
+    fake_int8_pages_from_fp16,
+    intent_quant_decode_attention_triton,
+    make_page_tables_from_selected_pages,
+    make_precision_tensor,
+)
+from .decode_core import PagePools, paged_decode
+
+__all__ = [
+    "SELECTED_POLICIES", "BlockLayout", "BlockPolicy", "SemanticBlock",
+    "BlockDecision", "BlockRouter", "RoutedBlock", "RouterConfig", "compute_block_scores",
+    "routing_to_kernel_metadata",
+    "FusedDecodeConfig", "FusedKVPrecision", "fused_selected_quant_decode", "is_native_available",
+    "metadata_to_kernel_tensors",
+    "IntentQuantizer", "KVPrecision", "QuantPolicy", "compute_quant_error", "fake_dequantize_tensor",
+    "fake_quantize_tensor",
+    "IntentQuantKernelConfig", "TritonKVPrecision", "fake_int8_pages_from_fp16",
+    "intent_quant_decode_attention_triton", "make_page_tables_from_selected_pages", "make_precision_tensor",
+    "PagePools", "paged_decode",
+]

@@ -1,0 +1,111 @@
+"""ctypes binding of libiak.so, the C ABI declared in include/iak.h.
+
+The library is built in-tree (``make -C intent-attention-kernel_amd/csrc``)
+next to this file. Nothing here falls back to another implementation: if the
+library is missing or was built for another ABI version, every entry point
+raises RuntimeError.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libiak.so")
+ABI_VERSION = 1
+
+IAK_OK, IAK_EINVAL, IAK_ENOTSUP, IAK_EHIP = 0, 1, 2, 3
+
+TAG_FP16, TAG_INT8, TAG_SKIP, TAG_FP8, TAG_INT4, TAG_INT4_RESIDUAL = 0, 1, 2, 3, 4, 5
+DTYPE_F16, DTYPE_F32, DTYPE_BF16 = 0, 1, 2
+
+c_i32, c_i64, c_void_p, c_float = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p, ctypes.c_float
+
+
+class PagedDecodeArgs(ctypes.Structure):
+    """Mirror of ``iak_paged_decode_args`` (include/iak.h)."""
+
+    _fields_ = [
+        ("batch", c_i32), ("num_q_heads", c_i32), ("num_kv_heads", c_i32), ("head_dim", c_i32),
+        ("page_size", c_i32), ("table_width", c_i32),
+        ("num_pages", c_i64),
+        ("q", c_void_p), ("q_dtype", c_i32), ("q_stride_b", c_i64), ("q_stride_h", c_i64),
+        ("out", c_void_p), ("out_dtype", c_i32), ("out_stride_b", c_i64), ("out_stride_h", c_i64),
+        ("page_table", c_void_p), ("page_counts", c_void_p), ("page_tags", c_void_p),
+        ("tag_map", ctypes.c_uint8 * 8),
+        ("negative_ids", c_i32),
+        ("k_fp16", c_void_p), ("v_fp16", c_void_p),
+        ("k_fp8", c_void_p), ("v_fp8", c_void_p),
+        ("k_int8", c_void_p), ("v_int8", c_void_p),
+        ("k_int4", c_void_p), ("v_int4", c_void_p),
+        ("k_int4r", c_void_p), ("v_int4r", c_void_p),
+        ("k_fp8_scale", c_void_p), ("v_fp8_scale", c_void_p), ("fp8_scale_dtype", c_i32),
+        ("k_int8_scale", c_void_p), ("v_int8_scale", c_void_p), ("int8_scale_dtype", c_i32),
+        ("k_int4_scale", c_void_p), ("v_int4_scale", c_void_p), ("int4_scale_dtype", c_i32),
+        ("int4_group", c_i32),
+        ("k_int4r_scale", c_void_p), ("v_int4r_scale", c_void_p),
+        ("sm_scale", c_float),
+        ("pages_per_split", c_i32),
+    ]
+
+
+EXPORTED = ("iak_abi_version", "iak_status_string", "iak_last_error",
+            "iak_paged_decode_workspace", "iak_paged_decode")
+
+_lib: Optional[ctypes.CDLL] = None
+_load_error: Optional[str] = None
+
+
+def load() -> ctypes.CDLL:
+    """Load libiak.so once; RuntimeError if it is absent or mismatched."""
+    global _lib, _load_error
+    if _lib is not None:
+        return _lib
+    if _load_error is not None:
+        raise RuntimeError(_load_error)
+    if not os.path.exists(LIB_PATH):
+        _load_error = (f"libiak.so not found at {LIB_PATH}; build it with "
+                       "`make -C intent-attention-kernel_amd/csrc` (or __graft_entry__.build())")
+        raise RuntimeError(_load_error)
+    try:
+        lib = ctypes.CDLL(LIB_PATH)
+    except OSError as e:
+        _load_error = f"cannot load {LIB_PATH}: {e}"
+        raise RuntimeError(_load_error) from e
+    lib.iak_abi_version.restype = ctypes.c_int
+    lib.iak_status_string.restype = ctypes.c_char_p
+    lib.iak_status_string.argtypes = [ctypes.c_int]
+    lib.iak_last_error.restype = ctypes.c_char_p
+    lib.iak_paged_decode_workspace.restype = ctypes.c_int
+    lib.iak_paged_decode_workspace.argtypes = [ctypes.POINTER(PagedDecodeArgs), ctypes.POINTER(ctypes.c_size_t)]
+    lib.iak_paged_decode.restype = ctypes.c_int
+    lib.iak_paged_decode.argtypes = [ctypes.POINTER(PagedDecodeArgs), c_void_p, ctypes.c_size_t, c_void_p]
+    ver = lib.iak_abi_version()
+    if ver != ABI_VERSION:
+        _load_error = f"libiak.so ABI version {ver} != expected {ABI_VERSION}; rebuild the library"
+        raise RuntimeError(_load_error)
+    _lib = lib
+    return lib
+
+
+def check(status: int) -> None:
+    """Map a status to the reference's exception types (ValueError / RuntimeError)."""
+    if status == IAK_OK:
+        return
+    lib = load()
+    msg = (lib.iak_last_error() or b"").decode(errors="replace")
+    what = (lib.iak_status_string(status) or b"").decode()
+    if status in (IAK_EINVAL, IAK_ENOTSUP):
+        raise ValueError(f"{msg} ({what})")
+    raise RuntimeError(f"{msg} ({what})")
+
+
+def workspace_bytes(args: PagedDecodeArgs) -> int:
+    n = ctypes.c_size_t(0)
+    check(load().iak_paged_decode_workspace(ctypes.byref(args), ctypes.byref(n)))
+    return int(n.value)
+
+
+def paged_decode(args: PagedDecodeArgs, workspace_ptr: int, workspace_size: int, stream: int) -> None:
+    check(load().iak_paged_decode(ctypes.byref(args), workspace_ptr or None, workspace_size, stream or None))

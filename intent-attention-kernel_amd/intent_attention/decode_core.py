@@ -1,0 +1,242 @@
+"""Device entry point of the selected-page decode: torch tensors -> C ABI.
+
+``paged_decode`` is the one function both reference-shaped APIs
+(``fused_selected_quant_decode`` and ``intent_quant_decode_attention_triton``)
+call. It checks shapes, fills ``iak_paged_decode_args`` with device pointers,
+allocates the split-K workspace from torch's caching allocator and launches
+on torch's current HIP stream. It never runs on the CPU: host tensors or a
+missing libiak.so raise.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, fields
+from typing import Dict, Optional, Sequence
+
+import torch
+
+from . import _native as N
+
+PAGE_SIZE = 16
+
+_DT = {torch.float16: N.DTYPE_F16, torch.float32: N.DTYPE_F32, torch.bfloat16: N.DTYPE_BF16}
+
+# Native tag identity map (IAK_TAG_*); unused slots are SKIP.
+NATIVE_TAG_MAP = (N.TAG_FP16, N.TAG_INT8, N.TAG_SKIP, N.TAG_FP8, N.TAG_INT4, N.TAG_INT4_RESIDUAL,
+                  N.TAG_SKIP, N.TAG_SKIP)
+
+
+@dataclass
+class PagePools:
+    """Per-precision K/V page pools, each indexed by physical page id.
+
+    Shapes (NP pages of PS=16 tokens, head_dim D):
+      k_fp16, v_fp16            [NP, 16, D] float16
+      k_fp8, v_fp8              [NP, 16, D] uint8 (e4m3fn codes); *_fp8_scale [NP] f16/f32
+      k_int8, v_int8            [NP, 16, D] int8;                  *_int8_scale [NP] f16/f32
+      k_int4, v_int4            [NP, 16, D/2] uint8 (element 2j low nibble of byte j,
+                                nibble = code + 8);                *_int4_scale [NP, D/int4_group]
+      k_int4r, v_int4r          [NP, 16, D] uint8 ((base+8) | (residual+8) << 4);
+                                *_int4r_scale [NP, 2] float32 (base, residual)
+    Absent precisions stay None; pages tagged with them must not be reachable.
+    """
+
+    k_fp16: Optional[torch.Tensor] = None
+    v_fp16: Optional[torch.Tensor] = None
+    k_fp8: Optional[torch.Tensor] = None
+    v_fp8: Optional[torch.Tensor] = None
+    k_fp8_scale: Optional[torch.Tensor] = None
+    v_fp8_scale: Optional[torch.Tensor] = None
+    k_int8: Optional[torch.Tensor] = None
+    v_int8: Optional[torch.Tensor] = None
+    k_int8_scale: Optional[torch.Tensor] = None
+    v_int8_scale: Optional[torch.Tensor] = None
+    k_int4: Optional[torch.Tensor] = None
+    v_int4: Optional[torch.Tensor] = None
+    k_int4_scale: Optional[torch.Tensor] = None
+    v_int4_scale: Optional[torch.Tensor] = None
+    int4_group: int = 32
+    k_int4r: Optional[torch.Tensor] = None
+    v_int4r: Optional[torch.Tensor] = None
+    k_int4r_scale: Optional[torch.Tensor] = None
+    v_int4r_scale: Optional[torch.Tensor] = None
+
+    def tensors(self) -> Dict[str, torch.Tensor]:
+        return {f.name: getattr(self, f.name) for f in fields(self)
+                if isinstance(getattr(self, f.name), torch.Tensor)}
+
+    def has(self, tag: int) -> bool:
+        need = {N.TAG_FP16: ("k_fp16", "v_fp16"),
+                N.TAG_INT8: ("k_int8", "v_int8", "k_int8_scale", "v_int8_scale"),
+                N.TAG_FP8: ("k_fp8", "v_fp8", "k_fp8_scale", "v_fp8_scale"),
+                N.TAG_INT4: ("k_int4", "v_int4", "k_int4_scale", "v_int4_scale"),
+                N.TAG_INT4_RESIDUAL: ("k_int4r", "v_int4r", "k_int4r_scale", "v_int4r_scale")}.get(tag, ())
+        return bool(need) and all(getattr(self, n) is not None for n in need)
+
+
+def require_device(*tensors: torch.Tensor, what: str = "fused selected-quant decode") -> torch.device:
+    """All tensors on one ROCm device, or RuntimeError (no host path exists)."""
+    devs = {t.device for t in tensors if isinstance(t, torch.Tensor)}
+    if not devs or any(d.type != "cuda" for d in devs):
+        raise RuntimeError(
+            f"{what} runs on the MI355X HIP kernels only: pass tensors on a ROCm device "
+            f"(got {sorted(str(d) for d in devs)}); the CPU restatement is test code, not a fallback")
+    if len(devs) != 1:
+        raise ValueError(f"all tensors must be on one device, got {sorted(str(d) for d in devs)}")
+    N.load()
+    return devs.pop()
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _check_pool(name: str, t: Optional[torch.Tensor], NP: int, row: Sequence[int], dtypes) -> None:
+    if t is None:
+        return
+    if t.dtype not in dtypes:
+        raise ValueError(f"{name} must have dtype in {[str(d) for d in dtypes]}, got {t.dtype}")
+    if tuple(t.shape) != (NP, *row):
+        raise ValueError(f"{name} must have shape {(NP, *row)}, got {tuple(t.shape)}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def _scale_dtype(name: str, *ts: Optional[torch.Tensor]) -> int:
+    dts = {t.dtype for t in ts if t is not None}
+    if not dts:
+        return N.DTYPE_F32
+    if len(dts) != 1 or next(iter(dts)) not in (torch.float16, torch.float32):
+        raise ValueError(f"{name} scales must both be float16 or both float32, got {dts}")
+    return _DT[next(iter(dts))]
+
+
+def paged_decode(q: torch.Tensor, pools: PagePools, page_table: torch.Tensor, page_counts: torch.Tensor,
+                 page_tags: torch.Tensor, *, tag_map: Optional[Sequence[int]] = None,
+                 negative_ids: bool = False, sm_scale: Optional[float] = None,
+                 out: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None,
+                 pages_per_split: int = 0) -> torch.Tensor:
+    """Selected-page decode attention on the GPU.
+
+    q [B, Hq, D] (f16 / f32 / bf16, any strides with unit last stride);
+    page_table [B, Hkv, W] int32; page_counts [B, Hkv] int32; page_tags [NP]
+    int32 caller tags mapped through ``tag_map`` (8 entries of IAK_TAG_*);
+    the default maps each native tag whose pools are present to itself and
+    every other tag to SKIP (contributes nothing). Query head h uses row
+    h // (Hq // Hkv). Returns out [B, Hq, D].
+    """
+    plan = make_plan(q, pools, page_table, page_counts, page_tags, tag_map=tag_map, negative_ids=negative_ids,
+                     sm_scale=sm_scale, out=out, out_dtype=out_dtype, pages_per_split=pages_per_split)
+    plan.run()
+    return plan.out
+
+
+def make_plan(q: torch.Tensor, pools: PagePools, page_table: torch.Tensor, page_counts: torch.Tensor,
+              page_tags: torch.Tensor, *, tag_map: Optional[Sequence[int]] = None,
+              negative_ids: bool = False, sm_scale: Optional[float] = None,
+              out: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None,
+              pages_per_split: int = 0) -> "DecodePlan":
+    """Validate the arguments of ``paged_decode`` once; the returned plan
+    re-launches the decode on the same tensors with ``run()``."""
+    if q.dim() != 3:
+        raise ValueError(f"q must have shape [B, H, D], got {tuple(q.shape)}")
+    B, Hq, D = q.shape
+    if page_table.dim() != 3 or page_table.shape[0] != B:
+        raise ValueError(f"page_table must have shape [B, Hkv, W] with B={B}, got {tuple(page_table.shape)}")
+    Hkv, W = int(page_table.shape[1]), int(page_table.shape[2])
+    if Hkv == 0 or Hq % Hkv != 0:
+        raise ValueError(f"query heads {Hq} must be a multiple of page-table heads {Hkv}")
+    if tuple(page_counts.shape) != (B, Hkv):
+        raise ValueError(f"page_counts must have shape {(B, Hkv)}, got {tuple(page_counts.shape)}")
+    if page_tags.dim() != 1:
+        raise ValueError(f"page_precision must have shape [num_pages], got {tuple(page_tags.shape)}")
+    NP = int(page_tags.shape[0])
+    dev = require_device(q, page_table, page_counts, page_tags, *pools.tensors().values())
+    for name, t in (("page_table", page_table), ("page_counts", page_counts), ("page_precision", page_tags)):
+        if t.dtype != torch.int32:
+            raise ValueError(f"{name} must be int32, got {t.dtype}")
+    page_table, page_counts, page_tags = (t.contiguous() for t in (page_table, page_counts, page_tags))
+    if q.dtype not in _DT:
+        raise ValueError(f"q dtype {q.dtype} not supported")
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+
+    f16, u8, i8 = (torch.float16,), (torch.uint8,), (torch.int8,)
+    _check_pool("k_fp16", pools.k_fp16, NP, (PAGE_SIZE, D), f16)
+    _check_pool("v_fp16", pools.v_fp16, NP, (PAGE_SIZE, D), f16)
+    _check_pool("k_fp8", pools.k_fp8, NP, (PAGE_SIZE, D), u8 + (torch.float8_e4m3fn,))
+    _check_pool("v_fp8", pools.v_fp8, NP, (PAGE_SIZE, D), u8 + (torch.float8_e4m3fn,))
+    _check_pool("k_int8", pools.k_int8, NP, (PAGE_SIZE, D), i8)
+    _check_pool("v_int8", pools.v_int8, NP, (PAGE_SIZE, D), i8)
+    _check_pool("k_int4", pools.k_int4, NP, (PAGE_SIZE, D // 2), u8)
+    _check_pool("v_int4", pools.v_int4, NP, (PAGE_SIZE, D // 2), u8)
+    _check_pool("k_int4r", pools.k_int4r, NP, (PAGE_SIZE, D), u8)
+    _check_pool("v_int4r", pools.v_int4r, NP, (PAGE_SIZE, D), u8)
+    sc = (torch.float16, torch.float32)
+    for n in ("k_fp8_scale", "v_fp8_scale", "k_int8_scale", "v_int8_scale"):
+        t = getattr(pools, n)
+        if t is not None and (t.dtype not in sc or t.numel() != NP):
+            raise ValueError(f"{n} must be [{NP}] float16/float32, got {tuple(t.shape)} {t.dtype}")
+    grp = pools.int4_group
+    for n in ("k_int4_scale", "v_int4_scale"):
+        t = getattr(pools, n)
+        if t is not None and (t.dtype not in sc or t.numel() != NP * (D // grp)):
+            raise ValueError(f"{n} must be [{NP}, {D // grp}] float16/float32, got {tuple(t.shape)}")
+    for n in ("k_int4r_scale", "v_int4r_scale"):
+        t = getattr(pools, n)
+        if t is not None and (t.dtype != torch.float32 or t.numel() != 2 * NP):
+            raise ValueError(f"{n} must be [{NP}, 2] float32, got {tuple(t.shape)} {t.dtype}")
+    for n, t in pools.tensors().items():
+        if not t.is_contiguous():
+            raise ValueError(f"{n} must be contiguous")
+
+    if out is None:
+        out = torch.empty((B, Hq, D), dtype=out_dtype or q.dtype, device=dev)
+    else:
+        if tuple(out.shape[-3:]) != (B, Hq, D) or out.dtype not in _DT or out.stride(-1) != 1:
+            raise ValueError(f"out must be [B, H, D] with unit last stride, got {tuple(out.shape)}")
+
+    a = N.PagedDecodeArgs()
+    a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim = B, Hq, Hkv, D
+    a.page_size, a.table_width, a.num_pages = PAGE_SIZE, W, NP
+    a.q, a.q_dtype, a.q_stride_b, a.q_stride_h = q.data_ptr(), _DT[q.dtype], q.stride(0), q.stride(1)
+    a.out, a.out_dtype = out.data_ptr(), _DT[out.dtype]
+    a.out_stride_b, a.out_stride_h = out.stride(-3), out.stride(-2)
+    a.page_table, a.page_counts, a.page_tags = page_table.data_ptr(), page_counts.data_ptr(), page_tags.data_ptr()
+    if tag_map is None:
+        tag_map = [t if pools.has(t) else N.TAG_SKIP for t in NATIVE_TAG_MAP]
+    tm = list(tag_map) + [N.TAG_SKIP] * (8 - len(tag_map))
+    for i in range(8):
+        a.tag_map[i] = int(tm[i])
+    a.negative_ids = 1 if negative_ids else 0
+    for n in ("k_fp16", "v_fp16", "k_fp8", "v_fp8", "k_int8", "v_int8", "k_int4", "v_int4",
+              "k_int4r", "v_int4r", "k_fp8_scale", "v_fp8_scale", "k_int8_scale", "v_int8_scale",
+              "k_int4_scale", "v_int4_scale", "k_int4r_scale", "v_int4r_scale"):
+        setattr(a, n, _ptr(getattr(pools, n)))
+    a.fp8_scale_dtype = _scale_dtype("fp8", pools.k_fp8_scale, pools.v_fp8_scale)
+    a.int8_scale_dtype = _scale_dtype("int8", pools.k_int8_scale, pools.v_int8_scale)
+    a.int4_scale_dtype = _scale_dtype("int4", pools.k_int4_scale, pools.v_int4_scale)
+    a.int4_group = grp
+    a.sm_scale = (1.0 / math.sqrt(D)) if sm_scale is None else float(sm_scale)
+    a.pages_per_split = int(pages_per_split)
+
+    return DecodePlan(a, dev, out, keep=(q, page_table, page_counts, page_tags, pools))
+
+
+class DecodePlan:
+    """Validated launch arguments plus workspace for repeated steps over the
+    same tensors (``run`` is one C call on the current stream; the tensors
+    are held so their memory stays valid)."""
+
+    def __init__(self, args: N.PagedDecodeArgs, device: torch.device, out: torch.Tensor, keep=()) -> None:
+        self.args = args
+        self.device = device
+        self.out = out
+        self._keep = keep
+        self.workspace_bytes = N.workspace_bytes(args)
+        self._ws = (torch.empty(self.workspace_bytes, dtype=torch.uint8, device=device)
+                    if self.workspace_bytes else None)
+
+    def run(self, stream: Optional[int] = None) -> None:
+        s = torch.cuda.current_stream(self.device).cuda_stream if stream is None else stream
+        N.paged_decode(self.args, self._ws.data_ptr() if self._ws is not None else 0, self.workspace_bytes, s)

@@ -1,0 +1,77 @@
+"""The C-ABI library: loads, exports every function include/iak.h declares, and
+the ctypes mirror of iak_paged_decode_args matches the C layout (checked by
+compiling a small offsetof probe of the header with gcc). No GPU calls."""
+import ctypes
+import os
+import re
+import subprocess
+import tempfile
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "iak.h")
+
+
+def _declared_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(iak_[a-z_]+)\s*\(", src)))
+
+
+def test_library_exports_every_declared_symbol():
+    from intent_attention import _native as N
+    lib = N.load()
+    declared = _declared_functions()
+    assert "iak_paged_decode" in declared and len(declared) >= 5
+    for name in declared:
+        assert hasattr(lib, name), f"libiak.so does not export {name}"
+    assert set(N.EXPORTED) <= set(declared)
+    assert lib.iak_abi_version() == N.ABI_VERSION
+    assert lib.iak_status_string(0) == b"ok"
+
+
+def test_ctypes_struct_matches_c_layout():
+    from intent_attention import _native as N
+    fields = [f[0] for f in N.PagedDecodeArgs._fields_]
+    prog = ['#include <stdio.h>', '#include <stddef.h>', '#include "iak.h"', 'int main(void){',
+            'printf("size %zu\\n", sizeof(iak_paged_decode_args));']
+    prog += [f'printf("{f} %zu\\n", offsetof(iak_paged_decode_args, {f}));' for f in fields]
+    prog += ["return 0;}"]
+    with tempfile.TemporaryDirectory() as d:
+        c = os.path.join(d, "probe.c")
+        open(c, "w").write("\n".join(prog))
+        exe = os.path.join(d, "probe")
+        subprocess.run(["gcc", "-std=c11", "-I", os.path.join(ROOT, "include"), c, "-o", exe], check=True)
+        got = dict(line.split() for line in subprocess.run([exe], capture_output=True, text=True,
+                                                           check=True).stdout.splitlines())
+    assert int(got["size"]) == ctypes.sizeof(N.PagedDecodeArgs)
+    for f in fields:
+        assert int(got[f]) == getattr(N.PagedDecodeArgs, f).offset, f
+
+
+def test_validation_errors_without_gpu():
+    """Argument checks run on the host before any launch."""
+    from intent_attention import _native as N
+    a = N.PagedDecodeArgs()
+    a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim, a.page_size = 1, 8, 2, 96, 16
+    with pytest.raises(ValueError, match="head_dim 96"):
+        N.workspace_bytes(a)
+    a.head_dim = 128
+    a.num_q_heads = 7
+    with pytest.raises(ValueError, match="multiple"):
+        N.workspace_bytes(a)
+    a.num_q_heads, a.page_size = 8, 32
+    with pytest.raises(ValueError, match="page_size 32"):
+        N.workspace_bytes(a)
+    a.page_size, a.table_width, a.num_pages = 16, 100, 10
+    a.q = a.out = a.page_table = a.page_counts = a.page_tags = 16
+    for i in range(8):
+        a.tag_map[i] = N.TAG_SKIP
+    a.tag_map[3] = N.TAG_FP8     # FP8 reachable but no FP8 pool
+    with pytest.raises(ValueError, match="FP8"):
+        N.workspace_bytes(a)
+    a.tag_map[3] = N.TAG_SKIP
+    a.sm_scale = 0.1
+    n = N.workspace_bytes(a)     # 2 rows x 100 pages: split into several chunks -> workspace
+    assert n > 0 and n % 256 == 0

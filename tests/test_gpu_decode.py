@@ -1,0 +1,225 @@
+"""GPU parity of the HIP selected-page decode against the CPU oracle.
+
+Every case calls libiak through the C ABI (``intent_attention.paged_decode``
+and the two reference-shaped APIs) and compares with
+``oracle.decode.paged_decode_oracle`` (float64 attention over the
+reference's dequantised values) on the same seeded inputs:
+max-abs <= 2e-3 when only FP16 pages are visited, <= 1e-2 with quantised pages.
+The fused API is also checked against the reference's own output
+(tests/golden/g3_fused_decode.npz).
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import decode as Dm
+from tests._pools import random_case, to_device_pools
+
+pytestmark = pytest.mark.gpu
+
+TOL_FP16 = 2e-3
+TOL_QUANT = 1e-2
+
+
+def _say(*a):
+    print("[gpu-case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def dev():
+    import torch
+    return torch.device("cuda:0")
+
+
+def _run(dev, q, pools_np, table, counts, tags, **kw):
+    import torch
+    from intent_attention import paged_decode
+    pools = to_device_pools(pools_np, dev)
+    qt = torch.from_numpy(q).to(dev)
+    out = paged_decode(qt, pools, torch.from_numpy(table).to(dev), torch.from_numpy(counts).to(dev),
+                       torch.from_numpy(tags).to(dev), **kw)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+CASES = [
+    # name, seed, B, Hq, Hkv, D, NP, W, mix
+    ("fp16_gqa4_d128", 11, 2, 8, 2, 128, 48, 40, {"FP16": 1}),
+    ("fp16_mha_d64", 12, 2, 4, 4, 64, 32, 20, {"FP16": 1}),
+    ("int8_gqa4_d128", 13, 2, 8, 2, 128, 48, 40, {"INT8": 1}),
+    ("fp8_gqa4_d128", 14, 2, 8, 2, 128, 48, 40, {"FP8": 1}),
+    ("int4_gqa4_d128", 15, 2, 8, 2, 128, 48, 40, {"INT4": 1}),
+    ("int4r_gqa4_d128", 16, 2, 8, 2, 128, 48, 40, {"INT4_RESIDUAL": 1}),
+    ("mixed_gqa4_d128", 17, 3, 8, 2, 128, 96, 70,
+     {"FP16": .25, "FP8": .2, "INT8": .25, "INT4": .15, "INT4_RESIDUAL": .1, "SKIP": .05}),
+    ("mixed_mha_d64", 18, 2, 4, 4, 64, 64, 50,
+     {"FP16": .3, "FP8": .2, "INT8": .2, "INT4": .2, "INT4_RESIDUAL": .1}),
+    ("mixed_gqa8_d128", 19, 2, 16, 2, 128, 64, 33, {"FP16": .5, "INT8": .3, "INT4": .2}),
+    ("mixed_gqa16_d64", 20, 1, 16, 1, 64, 64, 64, {"FP16": .4, "FP8": .3, "INT4": .3}),
+]
+
+
+@pytest.mark.parametrize("name,seed,B,Hq,Hkv,D,NP,W,mix", CASES, ids=[c[0] for c in CASES])
+@pytest.mark.parametrize("pps", [0, 16, 64])
+def test_paged_decode_matches_oracle(dev, name, seed, B, Hq, Hkv, D, NP, W, mix, pps):
+    _say(name, f"seed={seed} B={B} Hq={Hq} Hkv={Hkv} D={D} NP={NP} W={W} pages_per_split={pps}")
+    q, pools, table, counts, tags = random_case(seed, B, Hq, Hkv, D, NP, W, mix, outliers=0.01)
+    got = _run(dev, q, pools, table, counts, tags, pages_per_split=pps)
+    ref = Dm.paged_decode_oracle(q, pools, table, counts, tags)
+    tol = TOL_FP16 if set(mix) == {"FP16"} else TOL_QUANT
+    err = np.abs(got - ref).max()
+    assert err <= tol, f"{name}: max abs err {err:.3e} > {tol}"
+    # rows that visit no page are exactly zero
+    for b in range(B):
+        for hk in range(Hkv):
+            if counts[b, hk] == 0:
+                G = Hq // Hkv
+                assert np.all(got[b, hk * G:(hk + 1) * G] == 0)
+
+
+@pytest.mark.parametrize("qdt,odt", [("f32", "f32"), ("f16", "f32"), ("f32", "f16"), ("bf16", "bf16")])
+def test_q_and_out_dtypes(dev, qdt, odt):
+    import torch
+    _say("dtypes", qdt, odt)
+    q, pools, table, counts, tags = random_case(31, 2, 8, 2, 128, 40, 30,
+                                                {"FP16": .5, "INT8": .3, "FP8": .2})
+    q32 = np.random.default_rng(5).standard_normal(q.shape).astype(np.float32)
+    tdt = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
+    qt = torch.from_numpy(q32).to(tdt[qdt])
+    qref = qt.float().numpy()
+    from intent_attention import paged_decode
+    out = paged_decode(qt.to(dev), to_device_pools(pools, dev), torch.from_numpy(table).to(dev),
+                       torch.from_numpy(counts).to(dev), torch.from_numpy(tags).to(dev), out_dtype=tdt[odt])
+    assert out.dtype == tdt[odt]
+    ref = Dm.paged_decode_oracle(qref, pools, table, counts, tags)
+    tol = TOL_QUANT + (1e-2 if odt == "bf16" else 0)
+    assert np.abs(out.float().cpu().numpy() - ref).max() <= tol
+
+
+def test_invalid_ids_and_clamped_counts(dev):
+    import torch
+    _say("invalid ids / clamped counts")
+    q, pools, table, counts, tags = random_case(41, 2, 4, 2, 64, 32, 12, {"FP16": .6, "INT8": .4})
+    table[0, 0, 3] = -1        # negative: invalid in this mode
+    table[0, 1, 5] = 32        # past the pool: invalid
+    table[1, 0, 0] = -33       # below -NP: invalid even with wrap
+    counts[1, 1] = 99          # clamped to the width
+    got = _run(dev, q, pools, table, counts, tags)
+    ref = Dm.paged_decode_oracle(q, pools, table, counts, tags)
+    assert np.abs(got - ref).max() <= TOL_QUANT
+    table[0, 0, 4] = -2        # wraps to page 30 with negative_ids
+    got = _run(dev, q, pools, table, counts, tags, negative_ids=True)
+    ref = Dm.paged_decode_oracle(q, pools, table, counts, tags, neg_ids_wrap=True)
+    assert np.abs(got - ref).max() <= TOL_QUANT
+
+
+def test_selection_is_exact(dev):
+    """q = 0 gives a uniform softmax, so the output is the mean of the visited
+    pages' V rows; with V[page p] = e_p the visited multiset is recovered."""
+    import torch
+    _say("selection exactness probe")
+    D, NP, W = 64, 64, 40
+    rng = np.random.default_rng(3)
+    tags = np.zeros(NP, np.int32)
+    tags[rng.choice(NP, 10, replace=False)] = Dm.SKIP
+    pools = {"k_fp16": rng.standard_normal((NP, 16, D)).astype(np.float16),
+             "v_fp16": np.zeros((NP, 16, D), np.float16)}
+    for p in range(NP):
+        pools["v_fp16"][p, :, p] = 1.0
+    from intent_attention import PagePools, paged_decode
+    pp = PagePools(k_fp16=torch.from_numpy(pools["k_fp16"]).to(dev), v_fp16=torch.from_numpy(pools["v_fp16"]).to(dev))
+    table = rng.integers(0, NP, size=(3, 2, W)).astype(np.int32)
+    counts = np.array([[40, 17], [1, 0], [33, 40]], np.int32)
+    q = np.zeros((3, 2, D), np.float16)
+    out = paged_decode(torch.from_numpy(q).to(dev), pp, torch.from_numpy(table).to(dev),
+                       torch.from_numpy(counts).to(dev), torch.from_numpy(tags).to(dev),
+                       out_dtype=torch.float32).cpu().numpy()
+    for b in range(3):
+        for h in range(2):
+            vis = [p for p in table[b, h, :counts[b, h]] if tags[p] != Dm.SKIP]
+            exp = np.zeros(D)
+            for p in vis:
+                exp[p] += 1.0 / len(vis)
+            assert np.abs(out[b, h] - exp).max() < 1e-3, (b, h)
+
+
+@pytest.fixture(scope="module")
+def g3(golden_dir):
+    return dict(np.load(os.path.join(golden_dir, "g3_fused_decode.npz")))
+
+
+@pytest.mark.parametrize("variant", ["fused_fp16_scales", "triton_fp32_scales"])
+def test_fused_api_matches_reference_golden(dev, g3, variant):
+    """fused_selected_quant_decode on the GPU vs the reference's own CPU output."""
+    import torch
+    from intent_attention import FusedDecodeConfig, fused_selected_quant_decode
+    _say("fused API vs golden", variant)
+    pre = "t" if variant.startswith("triton") else ""
+    t = lambda k: torch.from_numpy(g3[k]).to(dev)  # noqa: E731
+    cfg = FusedDecodeConfig(page_size=16, head_dim=64, max_selected_pages=g3["page_table"].shape[2])
+    out = fused_selected_quant_decode(t("q"), t("k16"), t("v16"), t(f"{pre}k8"), t(f"{pre}v8"), t(f"{pre}ks"),
+                                      t(f"{pre}vs"), t("page_table"), t("page_precision"), t("page_counts"), cfg)
+    assert out.shape == (2, 4, 1, 64) and out.dtype == torch.float16 and out.is_cuda
+    ref = g3["out_triton_scales" if pre else "out"].astype(np.float32)
+    assert np.abs(out.float().cpu().numpy() - ref).max() <= TOL_FP16
+
+
+def test_fused_api_reference_test_facts(dev):
+    """test_fused_selected_quant_decode.py facts on the GPU: all-SKIP -> 0, zero pages -> 0,
+    FP16 path == dense attention over the gathered pages."""
+    import torch
+    from intent_attention import FusedDecodeConfig, FusedKVPrecision, fake_int8_pages_from_fp16
+    from intent_attention import fused_selected_quant_decode
+    from intent_attention.fused_selected_quant_decode import fake_int8_pages_from_fp16 as fused_fake_int8
+    _say("fused API reference facts")
+    g = torch.Generator().manual_seed(0)
+    B, H, D, PS, NP, W = 2, 4, 64, 16, 8, 4
+    k16 = torch.randn(NP, PS, D, generator=g).half()
+    v16 = torch.randn(NP, PS, D, generator=g).half()
+    k8, ks = fused_fake_int8(k16)
+    v8, vs = fused_fake_int8(v16)
+    q = torch.randn(B, H, 1, D, generator=g).half()
+    pt = torch.arange(W, dtype=torch.int32).repeat(B, H, 1)
+    pc = torch.full((B, H), W, dtype=torch.int32)
+    prec = torch.full((NP,), int(FusedKVPrecision.FP16), dtype=torch.int32)
+    cfg = FusedDecodeConfig(page_size=PS, head_dim=D, max_selected_pages=W)
+    args = [x.to(dev) for x in (q, k16, v16, k8, v8, ks, vs, pt, prec, pc)]
+    out = fused_selected_quant_decode(*args, cfg).float().cpu()
+    kk = k16[:W].reshape(-1, D).float()
+    vv = v16[:W].reshape(-1, D).float()
+    dense = torch.softmax(q[:, :, 0].float() @ kk.T / D ** 0.5, -1) @ vv
+    assert (out[:, :, 0] - dense).abs().max() < 1e-2
+    skip = torch.full((NP,), int(FusedKVPrecision.SKIP), dtype=torch.int32).to(dev)
+    assert fused_selected_quant_decode(*args[:8], skip, args[9], cfg).abs().max().item() < 1e-6
+    zero = torch.zeros(B, H, dtype=torch.int32).to(dev)
+    assert fused_selected_quant_decode(*args[:9], zero, cfg).abs().max().item() < 1e-6
+    with pytest.raises(ValueError, match="head_dim"):
+        fused_selected_quant_decode(*args, FusedDecodeConfig(head_dim=128))
+    del fake_int8_pages_from_fp16
+
+
+def test_sibling_api_triton_numbering(dev):
+    """intent_quant_decode_attention_triton: tags 0 FP16, 1-4 read the INT8 pool, 5 / id<0 invalid."""
+    import torch
+    from intent_attention import (IntentQuantKernelConfig, TritonKVPrecision, intent_quant_decode_attention_triton,
+                                  make_page_tables_from_selected_pages)
+    _say("sibling API")
+    rng = np.random.default_rng(9)
+    B, H, D, NP = 2, 4, 64, 12
+    q, pools, table, counts, tags = random_case(51, B, H, H, D, NP, 8, {"FP16": .5, "INT8": .5}, scale_f32=True)
+    ttags = np.where(tags == Dm.FP16, 0, rng.choice([1, 2, 3, 4], size=NP)).astype(np.int32)
+    ttags[0] = int(TritonKVPrecision.SKIP)
+    sel = torch.tensor([0, 3, 5, 7, 2, 11], dtype=torch.int32)
+    ids, cnt = make_page_tables_from_selected_pages(sel, B, H, max_selected_pages=8)
+    cfg = IntentQuantKernelConfig(page_size=16, head_dim=D, max_selected_pages=8)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)  # noqa: E731
+    out = intent_quant_decode_attention_triton(
+        t(q), t(pools["k_fp16"]), t(pools["v_fp16"]), t(pools["k_i8"]), t(pools["v_i8"]),
+        t(pools["k_i8_scale"]), t(pools["v_i8_scale"]), ids.to(dev), cnt.to(dev), t(ttags), config=cfg)
+    assert out.dtype == torch.float16 and out.shape == (B, H, D)
+    native = np.where(ttags == 0, Dm.FP16, np.where(ttags == 5, Dm.SKIP, Dm.INT8)).astype(np.int32)
+    ref = Dm.paged_decode_oracle(q, pools, ids.numpy(), cnt.numpy(), native)
+    assert np.abs(out.float().cpu().numpy() - ref).max() <= TOL_QUANT

@@ -1,0 +1,152 @@
+"""Host-side logic of the product package against the oracle and the goldens:
+router + metadata (exact, list order included), precision policy (exhaustive
+grid), fake-quant and fake_int8 utilities (bit-exact on CPU tensors), and the
+device requirement of the decode entry points."""
+import itertools
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import intent_attention as ia
+import importlib
+from intent_attention import intent_quant_decode as iqd
+from oracle import policy as P
+from oracle import quant as Q
+
+# the package re-exports a function under the submodule's name
+fsq_mod = importlib.import_module("intent_attention.fused_selected_quant_decode")
+
+
+@pytest.fixture(scope="module")
+def g2(golden_dir):
+    with open(os.path.join(golden_dir, "g2_router_metadata.json")) as f:
+        return json.load(f)
+
+
+def _product_layout(blocks):
+    return ia.BlockLayout([ia.SemanticBlock(n, s, e, ia.BlockPolicy(pol), sc) for n, s, e, pol, sc in blocks])
+
+
+def test_product_router_matches_reference_golden(g2):
+    for rec in g2:
+        router = ia.BlockRouter(ia.RouterConfig(**rec["config"]))
+        routed = router.route_layout(_product_layout(rec["blocks"]), rec["total_tokens"])
+        assert [[r.name, r.decision.value, r.precision.value, r.reason] for r in routed] == rec["routed"]
+        ps = rec["page_size"]
+        assert router.selected_page_ids(routed, ps) == rec["selected_page_ids_router"]
+        assert router.prefetch_page_ids(routed, ps) == rec["prefetch_page_ids_router"]
+        meta = ia.routing_to_kernel_metadata(routed, ps)
+        assert meta == rec["meta"]
+        assert list(meta["block_precision_by_page"]) == list(rec["meta"]["block_precision_by_page"])
+        num_pages = (rec["total_tokens"] + ps - 1) // ps
+        pt, prec, pc = ia.metadata_to_kernel_tensors(meta, num_pages, B=2, H=3,
+                                                     config=ia.FusedDecodeConfig(max_selected_pages=40))
+        assert pt.dtype == torch.int32 and prec.dtype == torch.int32 and pc.dtype == torch.int32
+        assert pt.tolist() == rec["kernel"]["page_table"]
+        assert prec.tolist() == rec["kernel"]["page_precision"]
+        assert pc.tolist() == rec["kernel"]["page_counts"]
+        # the native mapping differs only where the reference folds FP8 / INT4*
+        _, prec_n, _ = ia.metadata_to_kernel_tensors(meta, num_pages, native_precisions=True)
+        _, prec_o, _ = P.metadata_to_kernel_tensors(meta, num_pages, native_precisions=True)
+        assert prec_n.tolist() == prec_o.tolist()
+
+
+def test_product_router_matches_oracle_on_random_layouts():
+    rng = np.random.default_rng(99)
+    pols = ["ALWAYS", "ATTEND", "ATTEND", "SKIP", "RECENT", "GLOBAL"]
+    for trial in range(60):
+        blocks, t = [], 0
+        for i in range(int(rng.integers(1, 25))):
+            ln = int(rng.integers(1, 200))
+            pol = pols[int(rng.integers(0, len(pols)))]
+            sc = float(np.round(rng.random(), 1)) if (pol == "ATTEND" or rng.random() < .4) else None
+            blocks.append([f"b{i}", t, t + ln, pol, sc])
+            t += ln + int(rng.integers(0, 40))
+        cfg = dict(top_k_blocks=int(rng.integers(0, 10)), score_threshold=float(rng.random()),
+                   memory_pressure=float(np.round(rng.random(), 2)), prefetch_top_k=int(rng.integers(0, 6)))
+        ps = int(rng.choice([1, 3, 16, 64]))
+        r_o = P.BlockRouter(P.RouterConfig(**cfg))
+        ro = r_o.route_layout(P.BlockLayout([P.SemanticBlock(*b) for b in blocks]), t)
+        r_p = ia.BlockRouter(ia.RouterConfig(**cfg))
+        rp = r_p.route_layout(_product_layout(blocks), t)
+        assert [(r.name, r.decision, r.precision, r.reason) for r in ro] == \
+            [(r.name, r.decision.value, r.precision.value, r.reason) for r in rp]
+        assert P.routing_to_kernel_metadata(ro, ps) == ia.routing_to_kernel_metadata(rp, ps)
+        assert r_o.prefetch_page_ids(ro, ps) == r_p.prefetch_page_ids(rp, ps)
+
+
+def test_precision_policy_matches_oracle_on_grid():
+    pols = ["ALWAYS", "GLOBAL", "RECENT", "ATTEND", "SKIP"]
+    scores = [None, 0.0, 0.39, 0.4, 0.41, 0.74, 0.75, 0.9, 1.0]
+    mps = [0.0, 0.3, 0.31, 0.5, 0.51, 0.6, 0.61, 0.7, 0.71, 0.8, 0.81, 0.9, 0.91, 1.0]
+    for pol, sc, mp, pr, pg in itertools.product(pols, scores, mps, (True, False), (True, False)):
+        o = P.IntentQuantizer(mp, pr, pg).assign_block_precision(P.SemanticBlock("x", 0, 1, pol, sc))
+        p = ia.IntentQuantizer(mp, pr, pg).assign_block_precision(
+            ia.SemanticBlock("x", 0, 1, ia.BlockPolicy(pol), sc))
+        assert (o.precision, o.reason) == (p.precision.value, p.reason), (pol, sc, mp, pr, pg)
+
+
+@pytest.fixture(scope="module")
+def g1(golden_dir):
+    return dict(np.load(os.path.join(golden_dir, "g1_fake_quantize.npz")))
+
+
+@pytest.mark.parametrize("dt", ["f16", "f32"])
+@pytest.mark.parametrize("prec", ["FP8", "INT8", "INT4", "INT4_RESIDUAL"])
+def test_product_fake_quantize_matches_golden(g1, dt, prec):
+    x = torch.from_numpy(g1[f"x_{dt}"]).reshape(-1, 1)
+    recon, meta = ia.fake_quantize_tensor(x, ia.KVPrecision(prec))
+    ref = g1[f"recon_{dt}_page_{prec}"]
+    r = recon.float().numpy()
+    assert np.array_equal(r, ref) or np.array_equal(np.isnan(r), np.isnan(ref)) and \
+        np.array_equal(r[~np.isnan(r)], ref[~np.isnan(ref)])
+    assert np.array_equal(meta["scale"].float().numpy(), g1[f"scale_{dt}_page_{prec}"])
+
+
+def test_product_fake_int8_variants_match_golden(golden_dir):
+    g3 = dict(np.load(os.path.join(golden_dir, "g3_fused_decode.npz")))
+    q, s = fsq_mod.fake_int8_pages_from_fp16(torch.from_numpy(g3["k16"]))
+    assert np.array_equal(q.numpy(), g3["k8"]) and np.array_equal(s.numpy(), g3["ks"])
+    q, s = iqd.fake_int8_pages_from_fp16(torch.from_numpy(g3["edge_pages"]))
+    assert np.array_equal(q.numpy(), g3["edge_tq"]) and np.array_equal(s.numpy(), g3["edge_ts"])
+    q, s = ia.fake_int8_pages_from_fp16(torch.from_numpy(g3["v16"]))   # package export = fp32 variant
+    assert s.dtype == torch.float32 and np.array_equal(q.numpy(), g3["tv8"])
+
+
+def test_page_table_and_precision_helpers():
+    ids, cnt = ia.make_page_tables_from_selected_pages(torch.tensor([0, 2, 5], dtype=torch.int32), 2, 3, 8)
+    o_ids, o_cnt = P.make_page_tables_from_selected_pages(np.array([0, 2, 5]), 2, 3, 8)
+    assert ids.tolist() == o_ids.tolist() and cnt.tolist() == o_cnt.tolist()
+    with pytest.raises(ValueError, match="exceeds max_selected_pages"):
+        ia.make_page_tables_from_selected_pages(torch.arange(10), 1, 1, 5)
+    with pytest.raises(ValueError, match="must match batch and heads"):
+        ia.make_page_tables_from_selected_pages(torch.arange(6).reshape(1, 3, 2), 2, 3)
+    with pytest.raises(ValueError, match="must have shape"):
+        ia.make_page_tables_from_selected_pages(torch.arange(24).reshape(2, 3, 2, 2), 2, 3)
+    prec = ia.make_precision_tensor(10, fp16_pages=torch.tensor([0, 1, 2]), int8_pages=torch.tensor([3, 4]))
+    assert prec.tolist() == P.make_precision_tensor(10, [0, 1, 2], [3, 4]).tolist()
+    assert [int(t) for t in ia.TritonKVPrecision] == [0, 1, 2, 3, 4, 5]
+    assert [int(t) for t in ia.FusedKVPrecision][:3] == [0, 1, 2]
+
+
+def test_decode_entry_points_refuse_host_tensors():
+    x = torch.zeros(1, 1, 1, 64, dtype=torch.float16)
+    p = torch.zeros(2, 16, 64, dtype=torch.float16)
+    i8 = torch.zeros(2, 16, 64, dtype=torch.int8)
+    s = torch.ones(2, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        ia.fused_selected_quant_decode(x, p, p, i8, i8, s, s, torch.zeros(1, 1, 1, dtype=torch.int32),
+                                       torch.zeros(2, dtype=torch.int32), torch.ones(1, 1, dtype=torch.int32),
+                                       ia.FusedDecodeConfig())
+    with pytest.raises(ValueError, match="head_dim"):
+        ia.fused_selected_quant_decode(x, p, p, i8, i8, s, s, torch.zeros(1, 1, 1, dtype=torch.int32),
+                                       torch.zeros(2, dtype=torch.int32), torch.ones(1, 1, dtype=torch.int32),
+                                       ia.FusedDecodeConfig(head_dim=128))
+    if not torch.cuda.is_available():
+        with pytest.raises(RuntimeError, match="CUDA is not available"):
+            ia.intent_quant_decode_attention_triton(
+                x[:, :, 0], p, p, i8, i8, s, s, torch.zeros(1, 1, 64, dtype=torch.int32),
+                torch.ones(1, 1, dtype=torch.int32), torch.zeros(2, dtype=torch.int32))
