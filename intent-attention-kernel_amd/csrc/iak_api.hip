@@ -64,6 +64,10 @@ iak_status validate(const iak_paged_decode_args* a, Plan* plan) {
   const long long rows = (long long)a->batch * a->num_kv_heads;
   if (rows > 0) {
     if (!a->q || !a->out) return fail(IAK_EINVAL, "q/out is NULL");
+    // q rows are read as 16-byte vectors
+    const int qvec = a->q_dtype == IAK_DTYPE_F32 ? 4 : 8;
+    if (!aligned16(a->q) || a->q_stride_b % qvec != 0 || a->q_stride_h % qvec != 0)
+      return fail(IAK_EINVAL, "q must be 16-byte aligned with strides that are multiples of %d elements", qvec);
     if (!a->page_table || !a->page_counts) return fail(IAK_EINVAL, "page_table/page_counts is NULL");
     if (a->num_pages > 0 && !a->page_tags) return fail(IAK_EINVAL, "page_tags is NULL");
   }
@@ -97,8 +101,10 @@ iak_status validate(const iak_paged_decode_args* a, Plan* plan) {
   int chunk = a->pages_per_split;
   const int W = a->table_width;
   if (chunk == 0) {
+    // long splits amortise the per-split prologue and merge traffic; shorter
+    // ones only when the grid would otherwise not fill the 256 CUs
     chunk = 64;
-    while (chunk > 16 && rows * ((W + chunk - 1) / chunk) < 8192) chunk /= 2;
+    while (chunk > 16 && rows * ((W + chunk - 1) / chunk) < 2048) chunk /= 2;
   }
   int splits = W > 0 ? (W + chunk - 1) / chunk : 1;
   if (splits < 1) splits = 1;

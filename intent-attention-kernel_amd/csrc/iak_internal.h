@@ -7,6 +7,17 @@
 #include <stdint.h>
 
 #define IAK_WAVES_PER_BLOCK 4
+#define IAK_MIN_WAVES_PER_SIMD 3
+// pages per ring in each precision class loop (one computed, the rest in flight)
+#ifndef IAK_RING_FP16
+#define IAK_RING_FP16 2
+#endif
+#ifndef IAK_RING_BYTE
+#define IAK_RING_BYTE 3
+#endif
+#ifndef IAK_RING_INT4
+#define IAK_RING_INT4 5
+#endif
 
 namespace iak {
 

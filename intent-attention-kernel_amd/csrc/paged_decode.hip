@@ -51,7 +51,6 @@ typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 
 constexpr int PS = 16;
-constexpr float LOG2E = 1.4426950408889634f;
 constexpr float RESCALE_SLACK = 8.0f;      // p <= 2^8 between rescales
 constexpr uint32_t MAGIC_I8 = 0x64646464u;  // f16 0x64xx = 1024 + xx
 constexpr uint32_t MAGIC_I4 = 0x64006400u;
@@ -119,14 +118,44 @@ __device__ __forceinline__ void i4r_x4_to_f16(uint32_t x, h2 s0, h2 s1, uint32_t
   hi = pack_hi(bits(v02), bits(v13));
 }
 
+// Cross-lane reductions over the lanes {l, l^16, l^32, l^48} with the gfx950
+// lane-swap instructions (VALU, no LDS round trip): v_permlane32_swap v, t
+// with t = v leaves (v[0:32] | v[0:32]) in v and (v[32:64] | v[32:64]) in t,
+// so max(v, t) in every lane is the max over lanes l and l^32;
+// v_permlane16_swap does the same for l and l^16. Written as one asm block:
+// the compiler's own folding drops a float op on the two swap results (it
+// treats the second output as an unmodified copy of the input). s_nop 1 is
+// the wait the compiler inserts between a VALU write and a lane swap.
 __device__ __forceinline__ float xmax16_32(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16));
-  return fmaxf(v, __shfl_xor(v, 32));
+  float t;
+  asm volatile(
+      "v_mov_b32 %1, %0\n\t"
+      "s_nop 1\n\t"
+      "v_permlane32_swap_b32 %0, %1\n\t"
+      "v_max_f32 %0, %0, %1\n\t"
+      "v_mov_b32 %1, %0\n\t"
+      "s_nop 1\n\t"
+      "v_permlane16_swap_b32 %0, %1\n\t"
+      "v_max_f32 %0, %0, %1"
+      : "+v"(v), "=&v"(t));
+  return v;
 }
 __device__ __forceinline__ float xsum16_32(float v) {
-  v += __shfl_xor(v, 16);
-  return v + __shfl_xor(v, 32);
+  float t;
+  asm volatile(
+      "v_mov_b32 %1, %0\n\t"
+      "s_nop 1\n\t"
+      "v_permlane32_swap_b32 %0, %1\n\t"
+      "v_add_f32 %0, %0, %1\n\t"
+      "v_mov_b32 %1, %0\n\t"
+      "s_nop 1\n\t"
+      "v_permlane16_swap_b32 %0, %1\n\t"
+      "v_add_f32 %0, %0, %1"
+      : "+v"(v), "=&v"(t));
+  return v;
 }
+
+template <typename T> __device__ __forceinline__ T ld(const T* p) { return *p; }
 
 __device__ __forceinline__ float load_scale(const void* p, int64_t idx, int dtype) {
   if (dtype == IAK_DTYPE_F32) return reinterpret_cast<const float*>(p)[idx];
@@ -154,15 +183,15 @@ template <int D> __device__ __forceinline__ void load16(Raw16<D>& r, const _Floa
                                                        int c, int g) {
   const u4* kr = reinterpret_cast<const u4*>(kp + c * D + (D / 4) * g);
 #pragma unroll
-  for (int i = 0; i < D / 32; ++i) r.k[i] = __builtin_nontemporal_load(kr + i);
+  for (int i = 0; i < D / 32; ++i) r.k[i] = ld(kr + i);
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     const _Float16* row = vp + (4 * g + t) * D + (D / 16) * c;
     if constexpr (D == 128) {
-      u4 x = __builtin_nontemporal_load(reinterpret_cast<const u4*>(row));
+      u4 x = ld(reinterpret_cast<const u4*>(row));
       r.v[t][0] = x[0]; r.v[t][1] = x[1]; r.v[t][2] = x[2]; r.v[t][3] = x[3];
     } else {
-      u2 x = __builtin_nontemporal_load(reinterpret_cast<const u2*>(row));
+      u2 x = ld(reinterpret_cast<const u2*>(row));
       r.v[t][0] = x[0]; r.v[t][1] = x[1];
     }
   }
@@ -173,17 +202,17 @@ template <int D> __device__ __forceinline__ void load8(Raw8<D>& r, const uint8_t
   const u4* kr = reinterpret_cast<const u4*>(kp + c * D + (D / 4) * g);
 #pragma unroll
   for (int i = 0; i < D / 64; ++i) {
-    u4 x = __builtin_nontemporal_load(kr + i);
+    u4 x = ld(kr + i);
     r.k[4 * i + 0] = x[0]; r.k[4 * i + 1] = x[1]; r.k[4 * i + 2] = x[2]; r.k[4 * i + 3] = x[3];
   }
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     const uint8_t* row = vp + (4 * g + t) * D + (D / 16) * c;
     if constexpr (D == 128) {
-      u2 x = __builtin_nontemporal_load(reinterpret_cast<const u2*>(row));
+      u2 x = ld(reinterpret_cast<const u2*>(row));
       r.v[t][0] = x[0]; r.v[t][1] = x[1];
     } else {
-      r.v[t][0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(row));
+      r.v[t][0] = ld(reinterpret_cast<const uint32_t*>(row));
     }
   }
 }
@@ -192,19 +221,19 @@ template <int D> __device__ __forceinline__ void load4(Raw4<D>& r, const uint8_t
                                                       int c, int g) {
   const uint8_t* krow = kp + c * (D / 2) + (D / 8) * g;
   if constexpr (D == 128) {
-    u4 x = __builtin_nontemporal_load(reinterpret_cast<const u4*>(krow));
+    u4 x = ld(reinterpret_cast<const u4*>(krow));
     r.k[0] = x[0]; r.k[1] = x[1]; r.k[2] = x[2]; r.k[3] = x[3];
   } else {
-    u2 x = __builtin_nontemporal_load(reinterpret_cast<const u2*>(krow));
+    u2 x = ld(reinterpret_cast<const u2*>(krow));
     r.k[0] = x[0]; r.k[1] = x[1];
   }
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     const uint8_t* row = vp + (4 * g + t) * (D / 2) + (D / 32) * c;
     if constexpr (D == 128) {
-      r.v[t] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(row));
+      r.v[t] = ld(reinterpret_cast<const uint32_t*>(row));
     } else {
-      r.v[t] = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(row));
+      r.v[t] = ld(reinterpret_cast<const uint16_t*>(row));
     }
   }
 }
@@ -373,12 +402,74 @@ __device__ __forceinline__ int take(uint64_t& mask) {
   return idx;
 }
 
-template <int D, bool QF32>
-__device__ void write_result(const KArgs& a, const Split& sp, Wave<D, QF32>& w, int c, int g) {
+__device__ __forceinline__ float u2f(uint32_t x) { return __builtin_bit_cast(float, x); }
+__device__ __forceinline__ uint32_t f2u(float x) { return __builtin_bit_cast(uint32_t, x); }
+
+// Uniform scale slots of the page held by lane `idx` (see load_page_scales).
+struct Scales {
+  uint32_t s[4];
+};
+__device__ __forceinline__ Scales read_scales(const uint32_t (&slot)[4], int idx) {
+  Scales r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r.s[i] = __builtin_amdgcn_readlane(slot[i], idx);
+  return r;
+}
+
+// f16 group scale `grp` (0..3) out of two f16x2 dwords, splatted to both halves.
+__device__ __forceinline__ h2 group_scale(uint32_t lo, uint32_t hi, int grp) {
+  const uint32_t w = (grp & 2) ? hi : lo;
+  const uint32_t h = (grp & 1) ? (w >> 16) : (w & 0xFFFFu);
+  return as_h2(h | (h << 16));
+}
+
+__device__ __forceinline__ uint32_t scale_bits_f32(const void* p, int64_t idx, int dtype) {
+  return f2u(load_scale(p, idx, dtype));
+}
+__device__ __forceinline__ uint32_t scale_bits_f16(const void* p, int64_t idx, int dtype) {
+  const _Float16 h = (_Float16)load_scale(p, idx, dtype);
+  return (uint32_t)__builtin_bit_cast(uint16_t, h);
+}
+
+// Per-lane scale slots of the lane's own page, loaded once per split:
+//   FP8 / INT8      s0 = K scale, s1 = V scale (f32 bits)
+//   INT4_RESIDUAL   s0, s1 = K base / residual scale, s2, s3 = V base / residual (f32 bits)
+//   INT4            s0, s1 = K group scales as f16 pairs (g0,g1), (g2,g3); s2, s3 = V
+template <int D>
+__device__ __forceinline__ void load_page_scales(const KArgs& a, int pid, int tag, uint32_t (&slot)[4]) {
+  slot[0] = slot[1] = slot[2] = slot[3] = 0u;
+  if (pid < 0) return;
+  const int64_t p = pid;
+  if (tag == IAK_TAG_FP8) {
+    slot[0] = scale_bits_f32(a.k_fp8_scale, p, a.fp8_sd);
+    slot[1] = scale_bits_f32(a.v_fp8_scale, p, a.fp8_sd);
+  } else if (tag == IAK_TAG_INT8) {
+    slot[0] = scale_bits_f32(a.k_int8_scale, p, a.int8_sd);
+    slot[1] = scale_bits_f32(a.v_int8_scale, p, a.int8_sd);
+  } else if (tag == IAK_TAG_INT4_RESIDUAL) {
+    slot[0] = f2u(a.k_int4r_scale[2 * p]);
+    slot[1] = f2u(a.k_int4r_scale[2 * p + 1]);
+    slot[2] = f2u(a.v_int4r_scale[2 * p]);
+    slot[3] = f2u(a.v_int4r_scale[2 * p + 1]);
+  } else if (tag == IAK_TAG_INT4) {
+    const int ng = D / a.int4_group;   // 1, 2 or 4
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi) {
+      const int src = gi < ng ? gi : ng - 1;
+      const uint32_t kh = scale_bits_f16(a.k_int4_scale, p * ng + src, a.int4_sd);
+      const uint32_t vh = scale_bits_f16(a.v_int4_scale, p * ng + src, a.int4_sd);
+      slot[gi >> 1] |= kh << (16 * (gi & 1));
+      slot[2 + (gi >> 1)] |= vh << (16 * (gi & 1));
+    }
+  }
+}
+
+template <int D, int QT>
+__device__ void write_result(const KArgs& a, const Split& sp, Wave<D, QT != IAK_DTYPE_F16>& w, int c, int g) {
   const float l = xsum16_32(w.l);
+  if (c >= a.G) return;
   const int h = sp.hk * a.G + c;
   if (a.splits == 1) {
-    if (c >= a.G) return;
     const float inv = l > 0.f ? 1.0f / l : 0.0f;
     const int64_t base = (int64_t)sp.b * a.osb + (int64_t)h * a.osh + (D / 4) * g;
 #pragma unroll
@@ -403,7 +494,6 @@ __device__ void write_result(const KArgs& a, const Split& sp, Wave<D, QF32>& w, 
     }
     return;
   }
-  if (c >= a.G) return;
   const int64_t slot = (((int64_t)sp.b * a.Hkv + sp.hk) * a.splits + sp.split) * a.G + c;
   if (g == 0) { a.ws_m[slot] = w.m; a.ws_l[slot] = l; }
   float* op = a.ws_acc + slot * D + (D / 4) * g;
@@ -414,8 +504,83 @@ __device__ void write_result(const KArgs& a, const Split& sp, Wave<D, QF32>& w, 
   }
 }
 
-template <int D, bool QF32>
-__global__ __launch_bounds__(64 * IAK_WAVES_PER_BLOCK) void paged_decode_kernel(const KArgs a) {
+// Q operand of head c (zero for padding columns): dims (D/4)g + 8i .. +7 of step i,
+// loaded as 16-byte vectors (the C ABI checks 16-byte alignment of q rows).
+template <int D, int QT>
+__device__ __forceinline__ void load_q(const KArgs& a, const Split& sp, Wave<D, QT != IAK_DTYPE_F16>& w, int c,
+                                       int g) {
+  const bool live = c < a.G;
+  const int h = sp.hk * a.G + (live ? c : 0);
+  const int64_t off = (int64_t)sp.b * a.qsb + (int64_t)h * a.qsh + (D / 4) * g;
+#pragma unroll
+  for (int i = 0; i < D / 32; ++i) {
+    float qv[8];
+    if constexpr (QT == IAK_DTYPE_F32) {
+      const f4* p = reinterpret_cast<const f4*>(reinterpret_cast<const float*>(a.q) + off + 8 * i);
+      const f4 x0 = p[0], x1 = p[1];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) { qv[e] = x0[e]; qv[4 + e] = x1[e]; }
+    } else {
+      const u4 x = *reinterpret_cast<const u4*>(reinterpret_cast<const uint16_t*>(a.q) + off + 8 * i);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t lo = x[e] & 0xFFFFu, hi = x[e] >> 16;
+        if constexpr (QT == IAK_DTYPE_F16) {
+          qv[2 * e] = (float)__builtin_bit_cast(_Float16, (uint16_t)lo);
+          qv[2 * e + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)hi);
+        } else {   // bf16: the high half of an f32
+          qv[2 * e] = u2f(lo << 16);
+          qv[2 * e + 1] = u2f(hi << 16);
+        }
+      }
+    }
+    h8 vhi, vlo;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float v = live ? qv[e] : 0.f;
+      vhi[e] = (_Float16)v;
+      vlo[e] = (_Float16)(v - (float)vhi[e]);
+    }
+    w.qhi[i] = vhi;
+    if constexpr (QT != IAK_DTYPE_F16) w.qlo[i] = vlo;
+  }
+}
+
+// Walks the pages of one precision class (lanes set in `mask`) through a ring
+// of R register buffers: while one page is computed the next R-1 are in
+// flight. Every step issues exactly one page load -- once the class runs out
+// of pages the last page is loaded again (a cache hit) -- and the loop exits
+// only at its latch, so each buffer stays in its registers and the wait
+// before each compute is a fixed vmcnt: loads are never drained early.
+template <int R, typename Raw, typename LoadF, typename ComputeF>
+__device__ __forceinline__ void class_loop(uint64_t mask, int pid, LoadF load, ComputeF compute) {
+  if (!mask) return;
+  const int n = __builtin_popcountll(mask);
+  Raw buf[R];
+  int idx[R];
+  int last = 0;
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    if (mask) last = take(mask);
+    idx[j] = last;
+    load(buf[j], __builtin_amdgcn_readlane(pid, last));
+  }
+  // one exit, at the latch: the R steps of the body always issue their loads
+  for (int base = 0; base < n; base += R) {
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      if (base + j < n) compute(buf[j], idx[j]);
+      if (mask) last = take(mask);
+      idx[j] = last;
+      load(buf[j], __builtin_amdgcn_readlane(pid, last));
+    }
+  }
+}
+
+template <int D, int QT>
+__global__ __launch_bounds__(64 * IAK_WAVES_PER_BLOCK, IAK_MIN_WAVES_PER_SIMD)
+void paged_decode_kernel(const KArgs a) {
+  constexpr bool QF32 = QT != IAK_DTYPE_F16;
   const int lane = threadIdx.x & 63;
   const int wid = blockIdx.x * IAK_WAVES_PER_BLOCK + (threadIdx.x >> 6);
   if (wid >= a.items) return;
@@ -434,7 +599,7 @@ __global__ __launch_bounds__(64 * IAK_WAVES_PER_BLOCK) void paged_decode_kernel(
     if (sp.n < 0) sp.n = 0;
   }
 
-  // Page ids and native tags: lane i holds entry i of the split.
+  // Page id, native tag and scales: lane i holds entry i of the split.
   int pid = -1, tag = IAK_TAG_SKIP;
   if (lane < sp.n) {
     const int64_t unit = (int64_t)sp.b * a.Hkv + sp.hk;
@@ -447,141 +612,82 @@ __global__ __launch_bounds__(64 * IAK_WAVES_PER_BLOCK) void paged_decode_kernel(
       pid = -1;
     }
   }
+  uint32_t slot[4];
+  load_page_scales<D>(a, pid, tag, slot);
 
   Wave<D, QF32> w;
   w.m = -__builtin_inff();
   w.l = 0.f;
 #pragma unroll
   for (int mb = 0; mb < D / 16; ++mb) w.acc[mb] = f4{0.f, 0.f, 0.f, 0.f};
-  {
-    // Q operand: head c (zero for padding columns), dims (D/4)g + 8i .. +7.
-    const int h = sp.hk * a.G + c;
-    const bool live = c < a.G;
-#pragma unroll
-    for (int i = 0; i < D / 32; ++i) {
-      float qv[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qv[e] = 0.f;
-      if (live) {
-        const int64_t off = (int64_t)sp.b * a.qsb + (int64_t)h * a.qsh + (D / 4) * g + 8 * i;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          if (a.q_dtype == IAK_DTYPE_F16) qv[e] = (float)reinterpret_cast<const _Float16*>(a.q)[off + e];
-          else if (a.q_dtype == IAK_DTYPE_F32) qv[e] = reinterpret_cast<const float*>(a.q)[off + e];
-          else qv[e] = (float)reinterpret_cast<const __bf16*>(a.q)[off + e];
-        }
-      }
-      h8 hi, lo;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        hi[e] = (_Float16)qv[e];
-        lo[e] = (_Float16)(qv[e] - (float)hi[e]);
-      }
-      w.qhi[i] = hi;
-      if constexpr (QF32) w.qlo[i] = lo;
-    }
-  }
+  load_q<D, QT>(a, sp, w, c, g);
 
-  const float smul0 = a.score_mult;
+  const float smul = a.score_mult;
+  const h2 one = splat2((_Float16)1.0f);
 
   // ---- FP16 pages ----
-  uint64_t mask = __builtin_amdgcn_ballot_w64(tag == IAK_TAG_FP16);
-  if (mask) {
-    const _Float16* kpool = reinterpret_cast<const _Float16*>(a.k_fp16);
-    const _Float16* vpool = reinterpret_cast<const _Float16*>(a.v_fp16);
-    Raw16<D> cur, nxt;
-    int p = __builtin_amdgcn_readlane(pid, take(mask));
-    load16<D>(cur, kpool + (int64_t)p * PS * D, vpool + (int64_t)p * PS * D, c, g);
-    while (true) {
-      const bool more = mask != 0;
-      if (more) {
-        p = __builtin_amdgcn_readlane(pid, take(mask));
-        load16<D>(nxt, kpool + (int64_t)p * PS * D, vpool + (int64_t)p * PS * D, c, g);
-      }
-      page_fp16(w, cur, smul0);
-      if (!more) break;
-      cur = nxt;
-    }
+  {
+    const _Float16* kp = reinterpret_cast<const _Float16*>(a.k_fp16);
+    const _Float16* vp = reinterpret_cast<const _Float16*>(a.v_fp16);
+    class_loop<IAK_RING_FP16, Raw16<D>>(
+        __builtin_amdgcn_ballot_w64(tag == IAK_TAG_FP16), pid,
+        [&](Raw16<D>& r, int p) { load16<D>(r, kp + (int64_t)p * PS * D, vp + (int64_t)p * PS * D, c, g); },
+        [&](const Raw16<D>& r, int) { page_fp16(w, r, smul); });
+  }
+  // ---- one-byte precisions ----
+  {
+    const uint8_t* kp = reinterpret_cast<const uint8_t*>(a.k_fp8);
+    const uint8_t* vp = reinterpret_cast<const uint8_t*>(a.v_fp8);
+    class_loop<IAK_RING_BYTE, Raw8<D>>(
+        __builtin_amdgcn_ballot_w64(tag == IAK_TAG_FP8), pid,
+        [&](Raw8<D>& r, int p) { load8<D>(r, kp + (int64_t)p * PS * D, vp + (int64_t)p * PS * D, c, g); },
+        [&](const Raw8<D>& r, int idx) {
+          const Scales s = read_scales(slot, idx);
+          page_byte<D, QF32, IAK_TAG_FP8>(w, r, smul * u2f(s.s[0]), u2f(s.s[1]), one, one, one, one);
+        });
+  }
+  {
+    const uint8_t* kp = reinterpret_cast<const uint8_t*>(a.k_int8);
+    const uint8_t* vp = reinterpret_cast<const uint8_t*>(a.v_int8);
+    class_loop<IAK_RING_BYTE, Raw8<D>>(
+        __builtin_amdgcn_ballot_w64(tag == IAK_TAG_INT8), pid,
+        [&](Raw8<D>& r, int p) { load8<D>(r, kp + (int64_t)p * PS * D, vp + (int64_t)p * PS * D, c, g); },
+        [&](const Raw8<D>& r, int idx) {
+          const Scales s = read_scales(slot, idx);
+          page_byte<D, QF32, IAK_TAG_INT8>(w, r, smul * u2f(s.s[0]), u2f(s.s[1]), one, one, one, one);
+        });
+  }
+  {
+    const uint8_t* kp = reinterpret_cast<const uint8_t*>(a.k_int4r);
+    const uint8_t* vp = reinterpret_cast<const uint8_t*>(a.v_int4r);
+    class_loop<IAK_RING_BYTE, Raw8<D>>(
+        __builtin_amdgcn_ballot_w64(tag == IAK_TAG_INT4_RESIDUAL), pid,
+        [&](Raw8<D>& r, int p) { load8<D>(r, kp + (int64_t)p * PS * D, vp + (int64_t)p * PS * D, c, g); },
+        [&](const Raw8<D>& r, int idx) {
+          const Scales s = read_scales(slot, idx);
+          page_byte<D, QF32, IAK_TAG_INT4_RESIDUAL>(
+              w, r, smul, 1.0f, splat2((_Float16)u2f(s.s[0])), splat2((_Float16)u2f(s.s[1])),
+              splat2((_Float16)u2f(s.s[2])), splat2((_Float16)u2f(s.s[3])));
+        });
+  }
+  // ---- INT4 pages: lane K dims (D/4)g.. lie in group kg, V dims (D/16)c.. in group vg ----
+  {
+    const uint8_t* kp = reinterpret_cast<const uint8_t*>(a.k_int4);
+    const uint8_t* vp = reinterpret_cast<const uint8_t*>(a.v_int4);
+    const int kg = ((D / 4) * g) / a.int4_group;
+    const int vg = ((D / 16) * c) / a.int4_group;
+    class_loop<IAK_RING_INT4, Raw4<D>>(
+        __builtin_amdgcn_ballot_w64(tag == IAK_TAG_INT4), pid,
+        [&](Raw4<D>& r, int p) {
+          load4<D>(r, kp + (int64_t)p * PS * (D / 2), vp + (int64_t)p * PS * (D / 2), c, g);
+        },
+        [&](const Raw4<D>& r, int idx) {
+          const Scales s = read_scales(slot, idx);
+          page_int4(w, r, smul, group_scale(s.s[0], s.s[1], kg), group_scale(s.s[2], s.s[3], vg));
+        });
   }
 
-  // ---- FP8 / INT8 / INT4_RESIDUAL pages (one byte per element) ----
-#define IAK_BYTE_CLASS(TAGV, KPOOL, VPOOL)                                                        \
-  mask = __builtin_amdgcn_ballot_w64(tag == TAGV);                                                 \
-  if (mask) {                                                                                      \
-    const uint8_t* kpool = reinterpret_cast<const uint8_t*>(KPOOL);                                \
-    const uint8_t* vpool = reinterpret_cast<const uint8_t*>(VPOOL);                                \
-    Raw8<D> cur, nxt;                                                                              \
-    float ksc, vsc, ksn = 0.f, vsn = 0.f, ks1 = 0.f, vs1 = 0.f, ks1n = 0.f, vs1n = 0.f;             \
-    int p = __builtin_amdgcn_readlane(pid, take(mask));                                            \
-    load8<D>(cur, kpool + (int64_t)p * PS * D, vpool + (int64_t)p * PS * D, c, g);                \
-    if constexpr (TAGV == IAK_TAG_FP8) {                                                           \
-      ksc = load_scale(a.k_fp8_scale, p, a.fp8_sd); vsc = load_scale(a.v_fp8_scale, p, a.fp8_sd);  \
-    } else if constexpr (TAGV == IAK_TAG_INT8) {                                                   \
-      ksc = load_scale(a.k_int8_scale, p, a.int8_sd); vsc = load_scale(a.v_int8_scale, p, a.int8_sd); \
-    } else {                                                                                       \
-      ksc = a.k_int4r_scale[2 * (int64_t)p]; ks1 = a.k_int4r_scale[2 * (int64_t)p + 1];            \
-      vsc = a.v_int4r_scale[2 * (int64_t)p]; vs1 = a.v_int4r_scale[2 * (int64_t)p + 1];            \
-    }                                                                                              \
-    while (true) {                                                                                 \
-      const bool more = mask != 0;                                                                 \
-      if (more) {                                                                                  \
-        p = __builtin_amdgcn_readlane(pid, take(mask));                                            \
-        load8<D>(nxt, kpool + (int64_t)p * PS * D, vpool + (int64_t)p * PS * D, c, g);            \
-        if constexpr (TAGV == IAK_TAG_FP8) {                                                       \
-          ksn = load_scale(a.k_fp8_scale, p, a.fp8_sd); vsn = load_scale(a.v_fp8_scale, p, a.fp8_sd); \
-        } else if constexpr (TAGV == IAK_TAG_INT8) {                                               \
-          ksn = load_scale(a.k_int8_scale, p, a.int8_sd); vsn = load_scale(a.v_int8_scale, p, a.int8_sd); \
-        } else {                                                                                   \
-          ksn = a.k_int4r_scale[2 * (int64_t)p]; ks1n = a.k_int4r_scale[2 * (int64_t)p + 1];       \
-          vsn = a.v_int4r_scale[2 * (int64_t)p]; vs1n = a.v_int4r_scale[2 * (int64_t)p + 1];       \
-        }                                                                                          \
-      }                                                                                            \
-      if constexpr (TAGV == IAK_TAG_INT4_RESIDUAL) {                                               \
-        page_byte<D, QF32, TAGV>(w, cur, smul0, 1.0f, splat2((_Float16)ksc), splat2((_Float16)ks1), \
-                                 splat2((_Float16)vsc), splat2((_Float16)vs1));                    \
-      } else {                                                                                     \
-        const h2 one = splat2((_Float16)1.0f);                                                     \
-        page_byte<D, QF32, TAGV>(w, cur, smul0 * ksc, vsc, one, one, one, one);                    \
-      }                                                                                            \
-      if (!more) break;                                                                            \
-      cur = nxt; ksc = ksn; vsc = vsn; ks1 = ks1n; vs1 = vs1n;                                     \
-    }                                                                                              \
-  }
-
-  IAK_BYTE_CLASS(IAK_TAG_FP8, a.k_fp8, a.v_fp8)
-  IAK_BYTE_CLASS(IAK_TAG_INT8, a.k_int8, a.v_int8)
-  IAK_BYTE_CLASS(IAK_TAG_INT4_RESIDUAL, a.k_int4r, a.v_int4r)
-#undef IAK_BYTE_CLASS
-
-  // ---- INT4 pages (group scales: lane's K dims are group (D/4)g / grp, V dims (D/16)c / grp) ----
-  mask = __builtin_amdgcn_ballot_w64(tag == IAK_TAG_INT4);
-  if (mask) {
-    const uint8_t* kpool = reinterpret_cast<const uint8_t*>(a.k_int4);
-    const uint8_t* vpool = reinterpret_cast<const uint8_t*>(a.v_int4);
-    const int ngroups = D / a.int4_group;
-    const int kgrp = ((D / 4) * g) / a.int4_group;
-    const int vgrp = ((D / 16) * c) / a.int4_group;
-    Raw4<D> cur, nxt;
-    int p = __builtin_amdgcn_readlane(pid, take(mask));
-    load4<D>(cur, kpool + (int64_t)p * PS * (D / 2), vpool + (int64_t)p * PS * (D / 2), c, g);
-    float ksc = load_scale(a.k_int4_scale, (int64_t)p * ngroups + kgrp, a.int4_sd);
-    float vsc = load_scale(a.v_int4_scale, (int64_t)p * ngroups + vgrp, a.int4_sd);
-    float ksn = 0.f, vsn = 0.f;
-    while (true) {
-      const bool more = mask != 0;
-      if (more) {
-        p = __builtin_amdgcn_readlane(pid, take(mask));
-        load4<D>(nxt, kpool + (int64_t)p * PS * (D / 2), vpool + (int64_t)p * PS * (D / 2), c, g);
-        ksn = load_scale(a.k_int4_scale, (int64_t)p * ngroups + kgrp, a.int4_sd);
-        vsn = load_scale(a.v_int4_scale, (int64_t)p * ngroups + vgrp, a.int4_sd);
-      }
-      page_int4(w, cur, smul0, splat2((_Float16)ksc), splat2((_Float16)vsc));
-      if (!more) break;
-      cur = nxt; ksc = ksn; vsc = vsn;
-    }
-  }
-
-  write_result(a, sp, w, c, g);
+  write_result<D, QT>(a, sp, w, c, g);
 }
 
 // --------------------------------------------------------------------------- //
@@ -625,10 +731,10 @@ __global__ __launch_bounds__(256) void splitk_merge_kernel(const KArgs a) {
   }
 }
 
-template <int D, bool QF32>
+template <int D, int QT>
 hipError_t launch_decode(const KArgs& k, hipStream_t stream) {
   const int blocks = (k.items + IAK_WAVES_PER_BLOCK - 1) / IAK_WAVES_PER_BLOCK;
-  hipLaunchKernelGGL((paged_decode_kernel<D, QF32>), dim3(blocks), dim3(64 * IAK_WAVES_PER_BLOCK), 0,
+  hipLaunchKernelGGL((paged_decode_kernel<D, QT>), dim3(blocks), dim3(64 * IAK_WAVES_PER_BLOCK), 0,
                      stream, k);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || k.splits == 1) return e;
@@ -637,9 +743,17 @@ hipError_t launch_decode(const KArgs& k, hipStream_t stream) {
   return hipGetLastError();
 }
 
+template <int D>
+hipError_t launch_d(const KArgs& k, hipStream_t stream) {
+  switch (k.q_dtype) {
+    case IAK_DTYPE_F32: return launch_decode<D, IAK_DTYPE_F32>(k, stream);
+    case IAK_DTYPE_BF16: return launch_decode<D, IAK_DTYPE_BF16>(k, stream);
+    default: return launch_decode<D, IAK_DTYPE_F16>(k, stream);
+  }
+}
+
 hipError_t launch_paged_decode(const KArgs& k, hipStream_t stream) {
-  if (k.D == 128) return k.q_f32 ? launch_decode<128, true>(k, stream) : launch_decode<128, false>(k, stream);
-  return k.q_f32 ? launch_decode<64, true>(k, stream) : launch_decode<64, false>(k, stream);
+  return k.D == 128 ? launch_d<128>(k, stream) : launch_d<64>(k, stream);
 }
 
 }  // namespace iak

@@ -158,8 +158,9 @@ def make_plan(q: torch.Tensor, pools: PagePools, page_table: torch.Tensor, page_
     page_table, page_counts, page_tags = (t.contiguous() for t in (page_table, page_counts, page_tags))
     if q.dtype not in _DT:
         raise ValueError(f"q dtype {q.dtype} not supported")
-    if q.stride(-1) != 1:
-        q = q.contiguous()
+    qvec = 4 if q.dtype == torch.float32 else 8
+    if q.stride(-1) != 1 or q.data_ptr() % 16 or q.stride(0) % qvec or q.stride(1) % qvec:
+        q = q.contiguous()   # the kernel reads q rows as 16-byte vectors
 
     f16, u8, i8 = (torch.float16,), (torch.uint8,), (torch.int8,)
     _check_pool("k_fp16", pools.k_fp16, NP, (PAGE_SIZE, D), f16)
