@@ -97,21 +97,22 @@ iak_status validate(const iak_paged_decode_args* a, Plan* plan) {
     }
   }
 
-  // split plan: enough waves to fill 256 CUs several times over
-  int chunk = a->pages_per_split;
+  // split plan: one wave per split of up to `chunk` table entries
   const int W = a->table_width;
+  int chunk = a->pages_per_split;
   if (chunk == 0) {
-    // long splits amortise the per-split prologue and merge traffic; shorter
+    // long splits amortise the per-split prologue and partial traffic; shorter
     // ones only when the grid would otherwise not fill the 256 CUs
     chunk = 64;
     while (chunk > 16 && rows * ((W + chunk - 1) / chunk) < 2048) chunk /= 2;
   }
-  int splits = W > 0 ? (W + chunk - 1) / chunk : 1;
+  int splits = (W + chunk - 1) / chunk;
   if (splits < 1) splits = 1;
   if (rows * (long long)splits > 0x7FFFFFFFLL) return fail(IAK_EINVAL, "too many splits");
   plan->G = G;
   plan->splits = splits;
   plan->chunk = chunk;
+  // workspace: the split partials (m, l, acc); none when one split covers a row
   if (splits == 1) {
     plan->ws_m = plan->ws_l = plan->ws_acc = plan->total = 0;
   } else {
@@ -160,12 +161,14 @@ iak_status iak_paged_decode(const iak_paged_decode_args* a, void* workspace, siz
   if (rows == 0) return IAK_OK;
   if (plan.total > 0 && (!workspace || workspace_bytes < plan.total))
     return fail(IAK_EINVAL, "workspace of %zu bytes is smaller than the %zu bytes required", workspace_bytes, plan.total);
+  if (plan.total > 0 && !aligned16(workspace)) return fail(IAK_EINVAL, "workspace must be 16-byte aligned");
 
   iak::KArgs k;
   std::memset(&k, 0, sizeof(k));
   k.B = a->batch; k.Hq = a->num_q_heads; k.Hkv = a->num_kv_heads; k.G = plan.G; k.D = a->head_dim;
   k.W = a->table_width; k.NP = a->num_pages;
-  k.splits = plan.splits; k.chunk = plan.chunk; k.items = (int)(rows * plan.splits);
+  k.splits = plan.splits; k.chunk = plan.chunk;
+  k.items = (int)(rows * plan.splits);
   k.q = a->q; k.q_dtype = a->q_dtype; k.q_f32 = a->q_dtype != IAK_DTYPE_F16;
   k.qsb = a->q_stride_b; k.qsh = a->q_stride_h;
   k.out = a->out; k.out_dtype = a->out_dtype; k.osb = a->out_stride_b; k.osh = a->out_stride_h;

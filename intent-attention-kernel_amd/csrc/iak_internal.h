@@ -25,7 +25,7 @@ struct KArgs {
   int B, Hq, Hkv, G, D, W;
   int64_t NP;
   int splits;   // splits per (batch, kv head) row
-  int chunk;    // pages per split (<= 64)
+  int chunk;    // table entries per split (<= 64)
   int items;    // B * Hkv * splits waves
 
   const void* q; int q_dtype; int q_f32; int64_t qsb, qsh;

@@ -577,43 +577,71 @@ __device__ __forceinline__ void class_loop(uint64_t mask, int pid, LoadF load, C
   }
 }
 
+// Position of work item `item`: split `item % splits` of row
+// `unit` = b * Hkv + hk, table entries [start, start + chunk).
+__device__ __forceinline__ void locate(const KArgs& a, int item, Split& sp, int& start, int& unit) {
+  unit = item / a.splits;
+  sp.split = item - unit * a.splits;
+  start = sp.split * a.chunk;
+  sp.b = unit / a.Hkv;
+  sp.hk = unit - sp.b * a.Hkv;
+}
+
+// First metadata stage of an item: lane i loads table entry start + i (bounded
+// by the table width, so it needs no count) and the row's page count.
+__device__ __forceinline__ void load_entry(const KArgs& a, int unit, int start, int len, int lane, int& raw,
+                                           int& cnt) {
+  raw = -1;
+  if (lane < len && start + lane < a.W) raw = a.table[(int64_t)unit * a.W + start + lane];
+  cnt = a.counts[unit];
+}
+
+// Second stage: drop entries at or past the row's count, validate the page id
+// (wrapping negative ids when asked) and load its tag through the tag map.
+__device__ __forceinline__ void load_tag(const KArgs& a, int raw, int cnt, int start, int len, int lane,
+                                         int& pid, int& tag, int& n) {
+  cnt = cnt < 0 ? 0 : (cnt > a.W ? a.W : cnt);
+  n = cnt - start < len ? cnt - start : len;
+  if (n < 0) n = 0;
+  pid = -1;
+  tag = IAK_TAG_SKIP;
+  if (lane < n) {
+    int p = raw;
+    if (a.neg_wrap && p < 0 && (int64_t)p >= -a.NP) p = (int)((int64_t)p + a.NP);
+    if (p >= 0 && (int64_t)p < a.NP) {
+      const int t = a.tags[p];
+      tag = (t >= 0 && t < 8) ? (int)((a.tagmap >> (8 * t)) & 0xFFu) : IAK_TAG_SKIP;
+      pid = p;
+    }
+  }
+}
+
+// Waves per SIMD the kernel is compiled for: f32 / bf16 queries carry a second
+// (low-half) Q operand and get the register budget of two waves per SIMD.
+template <int QT> constexpr int waves_per_simd() { return QT == IAK_DTYPE_F16 ? IAK_MIN_WAVES_PER_SIMD : 2; }
+
+// One wave per work item. The dependent metadata loads (table entry and count
+// -> tag -> scales) are the wave's prologue; the waves the hardware starts as
+// others finish run their prologue while the rest of the CU streams pages.
 template <int D, int QT>
-__global__ __launch_bounds__(64 * IAK_WAVES_PER_BLOCK, IAK_MIN_WAVES_PER_SIMD)
+__global__ __launch_bounds__(64 * IAK_WAVES_PER_BLOCK, waves_per_simd<QT>())
 void paged_decode_kernel(const KArgs a) {
   constexpr bool QF32 = QT != IAK_DTYPE_F16;
   const int lane = threadIdx.x & 63;
-  const int wid = blockIdx.x * IAK_WAVES_PER_BLOCK + (threadIdx.x >> 6);
-  if (wid >= a.items) return;
   const int c = lane & 15, g = lane >> 4;
+  const int item = blockIdx.x * IAK_WAVES_PER_BLOCK + (threadIdx.x >> 6);
+  if (item >= a.items) return;
 
   Split sp;
-  {
-    const int unit = wid / a.splits;
-    sp.split = wid - unit * a.splits;
-    sp.b = unit / a.Hkv;
-    sp.hk = unit - sp.b * a.Hkv;
-    int cnt = a.counts[unit];
-    cnt = cnt < 0 ? 0 : (cnt > a.W ? a.W : cnt);
-    const int start = sp.split * a.chunk;
-    sp.n = cnt - start < a.chunk ? cnt - start : a.chunk;
-    if (sp.n < 0) sp.n = 0;
-  }
-
-  // Page id, native tag and scales: lane i holds entry i of the split.
-  int pid = -1, tag = IAK_TAG_SKIP;
-  if (lane < sp.n) {
-    const int64_t unit = (int64_t)sp.b * a.Hkv + sp.hk;
-    pid = a.table[unit * a.W + (int64_t)sp.split * a.chunk + lane];
-    if (a.neg_wrap && pid < 0 && (int64_t)pid >= -a.NP) pid = (int)((int64_t)pid + a.NP);
-    if (pid >= 0 && (int64_t)pid < a.NP) {
-      const int t = a.tags[pid];
-      tag = (t >= 0 && t < 8) ? (int)((a.tagmap >> (8 * t)) & 0xFFu) : IAK_TAG_SKIP;
-    } else {
-      pid = -1;
-    }
-  }
+  int pid, tag;
   uint32_t slot[4];
-  load_page_scales<D>(a, pid, tag, slot);
+  {
+    int start, unit, raw, cnt;
+    locate(a, item, sp, start, unit);
+    load_entry(a, unit, start, a.chunk, lane, raw, cnt);
+    load_tag(a, raw, cnt, start, a.chunk, lane, pid, tag, sp.n);
+    load_page_scales<D>(a, pid, tag, slot);
+  }
 
   Wave<D, QF32> w;
   w.m = -__builtin_inff();
@@ -701,23 +729,41 @@ __global__ __launch_bounds__(256) void splitk_merge_kernel(const KArgs a) {
   if (bh >= a.B * a.Hq) return;
   const int b = bh / a.Hq, h = bh - b * a.Hq;
   const int hk = h / a.G, c = h - hk * a.G;
-  const int64_t first = (((int64_t)b * a.Hkv + hk) * a.splits) * a.G + c;   // slot of split 0
+  const int S = a.splits;
+  const int64_t first = (((int64_t)b * a.Hkv + hk) * S) * a.G + c;   // slot of split 0
+  // global max over the splits: lanes read splits in parallel, then reduce
   float M = -__builtin_inff();
-  for (int s = 0; s < a.splits; ++s) M = fmaxf(M, a.ws_m[first + (int64_t)s * a.G]);
+  for (int s = lane; s < S; s += 64) M = fmaxf(M, a.ws_m[first + (int64_t)s * a.G]);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
   constexpr int PER = D / 64;   // dims per lane
   float o[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) o[j] = 0.f;
   float L = 0.f;
   if (M > -__builtin_inff()) {
-    for (int s = 0; s < a.splits; ++s) {
-      const int64_t slot = first + (int64_t)s * a.G;
-      const float ms = a.ws_m[slot];
-      const float wgt = __builtin_amdgcn_exp2f(ms - M);   // 0 for empty splits (m = -inf)
-      L += wgt * a.ws_l[slot];
-      const float* ap = a.ws_acc + slot * D + PER * lane;
+    // eight splits per step with their loads issued together
+    constexpr int U = 8;
+    int s = 0;
+    for (; s < S; s += U) {
+      float ms[U], ls[U], av[U][PER];
 #pragma unroll
-      for (int j = 0; j < PER; ++j) o[j] += wgt * ap[j];
+      for (int k = 0; k < U; ++k) {
+        const int64_t slot = first + (int64_t)(s + k < S ? s + k : S - 1) * a.G;
+        ms[k] = a.ws_m[slot];
+        ls[k] = a.ws_l[slot];
+        const float* ap = a.ws_acc + slot * D + PER * lane;
+#pragma unroll
+        for (int j = 0; j < PER; ++j) av[k][j] = ap[j];
+      }
+#pragma unroll
+      for (int k = 0; k < U; ++k) {
+        // 0 for empty splits (m = -inf) and for the clamped reloads past S
+        const float wgt = s + k < S ? __builtin_amdgcn_exp2f(ms[k] - M) : 0.f;
+        L += wgt * ls[k];
+#pragma unroll
+        for (int j = 0; j < PER; ++j) o[j] += wgt * av[k][j];
+      }
     }
   }
   const float inv = L > 0.f ? 1.0f / L : 0.f;

@@ -80,6 +80,27 @@ def test_paged_decode_matches_oracle(dev, name, seed, B, Hq, Hkv, D, NP, W, mix,
                 assert np.all(got[b, hk * G:(hk + 1) * G] == 0)
 
 
+@pytest.mark.parametrize("W", [448, 1000])
+def test_many_rows(dev, W):
+    """256 (batch, kv head) rows with ragged counts: the automatic plan (64-entry
+    splits, partials merged per row) against the oracle on rows sampled from
+    the batch and, for the whole output, against a uniform 16-entry plan."""
+    _say("many rows", f"W={W}")
+    B, Hq, Hkv, D = 32, 32, 8, 128
+    q, pools, table, counts, tags = random_case(
+        51 + W, B, Hq, Hkv, D, 2048, W,
+        {"FP16": .25, "FP8": .25, "INT8": .3, "INT4": .15, "INT4_RESIDUAL": .05}, outliers=0.01,
+        q_scale=1 / np.sqrt(D))
+    counts[1] = W                    # full rows next to the random counts
+    got = _run(dev, q, pools, table, counts, tags)
+    uni = _run(dev, q, pools, table, counts, tags, pages_per_split=16)
+    assert np.abs(got - uni).max() <= 1e-3
+    for b in (0, 1, 17, 31):
+        ref = Dm.paged_decode_oracle(q[b:b + 1], pools, table[b:b + 1], counts[b:b + 1], tags)
+        err = np.abs(got[b:b + 1] - ref).max()
+        assert err <= TOL_QUANT, f"batch {b}: max abs err {err:.3e}"
+
+
 @pytest.mark.parametrize("qdt,odt", [("f32", "f32"), ("f16", "f32"), ("f32", "f16"), ("bf16", "bf16")])
 def test_q_and_out_dtypes(dev, qdt, odt):
     import torch
