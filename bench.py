@@ -185,6 +185,13 @@ def build_workload(name: str, device: torch.device, seed: int = 1234, chunk_page
     return dict(cfg=cfg, name=name, q=q, pools=pools, table=table, counts=counts, tags=tags, NP=NP, W=W)
 
 
+# HBM bytes per decode-kernel launch (reads + writes) from rocprofv3 FETCH_SIZE /
+# WRITE_SIZE runs of this bench, each scaled by what the counter reads for a
+# 1 GiB device copy (--calibrate-copy): profiles/paged_decode_cfg3_hbm_traffic.txt.
+MEASURED_TRAFFIC = {
+    "cfg3": {"bytes": 2_120_189_338 + 13_974_938, "source": "profiles/paged_decode_cfg3_hbm_traffic.txt"},
+}
+
 PAGE_BYTES = {  # K+V code bytes and scale bytes per page (D = 128, fp16 scales, INT4 groups of 32)
     TAG_FP16: (2 * PS * 128 * 2, 0), TAG_FP8: (2 * PS * 128, 2 * 2), TAG_INT8: (2 * PS * 128, 2 * 2),
     TAG_INT4: (2 * PS * 64, 2 * 4 * 2), TAG_INT4R: (2 * PS * 128, 2 * 2 * 4), TAG_SKIP: (0, 0),
@@ -331,8 +338,11 @@ def main() -> None:
                    "pages_per_tag": ab["per_tag"], "pages_per_split": plan.args.pages_per_split,
                    "gflop": round(flops(wl) / 1e9, 3)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None},
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": MEASURED_TRAFFIC.get(args.config, {}).get("bytes")},
     }
+    if args.config in MEASURED_TRAFFIC:
+        res["roofline"]["traffic_source"] = MEASURED_TRAFFIC[args.config]["source"]
     if args.calibrate_copy:
         n = args.calibrate_copy * (1 << 20)
         src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
