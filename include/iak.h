@@ -13,6 +13,10 @@
  *                               and intent_quant_decode_attention_triton()
  *                                                                      triton_intent_quant_attention.py:342-457
  *   iak_paged_decode_workspace  (no counterpart: sizes the split-K partial buffer the caller allocates)
+ *   iak_mla_decode              mla_decode_triton() / _mla_decode_cpu()    triton_mla_decode.py:110-186
+ *                               (the latent context; mla_sparse_decode_reference mla.py:61-92,
+ *                               mla_triton_decode mla.py:95-136)
+ *   iak_mla_decode_workspace    (no counterpart: sizes the split-K partial buffer)
  *   iak_status_string           (no counterpart: the reference raises ValueError/RuntimeError in Python)
  */
 #ifndef IAK_H
@@ -126,6 +130,50 @@ iak_status iak_paged_decode_workspace(const iak_paged_decode_args* args, size_t*
  * NULL when that is 0). `stream` is a hipStream_t (NULL = default stream). */
 iak_status iak_paged_decode(const iak_paged_decode_args* args, void* workspace,
                             size_t workspace_bytes, void* stream);
+
+/*
+ * MLA latent decode: every query head attends to one shared compressed KV
+ * (latent rows of qk_dim values; dims v_offset .. v_offset + v_dim - 1 of a
+ * row are also its values). Per sequence b and head h:
+ *   s_t = sm_scale * q[b,h,:] . C_t   over the latent rows C_t of the pages
+ *         page_table[b, 0 .. page_counts[b]-1] (SKIP pages contribute nothing)
+ *   out[b,h,:] = sum_t softmax(s)_t * C_t[v_offset : v_offset + v_dim]   (0 when nothing is visited)
+ * Latent pools are [num_pages, page_size, qk_dim]: FP16 values, or FP8-e4m3 / INT8
+ * codes with one scale per page (dequantised value = code * scale). Page tags go
+ * through tag_map as in iak_paged_decode; INT4 tags are not supported here.
+ * Computed with f16 MFMA operands (q rounded to f16) and f32 accumulation.
+ * Supported (qk_dim, v_dim): (64,64) (128,128) (256,256) (512,512) (576,512) (576,64).
+ */
+typedef struct {
+  int32_t batch, num_heads, qk_dim, v_dim, v_offset, page_size, table_width;
+  int64_t num_pages;
+
+  const void* q; int32_t q_dtype; int64_t q_stride_b, q_stride_h;
+  void* out; int32_t out_dtype; int64_t out_stride_b, out_stride_h;
+
+  const int32_t* page_table;   /* [batch, table_width] */
+  const int32_t* page_counts;  /* [batch] */
+  const int32_t* page_tags;    /* [num_pages]; NULL = every page FP16 */
+  uint8_t tag_map[8];
+  int32_t negative_ids;
+  const int32_t* valid_tokens; /* [batch] or NULL: token t of table entry e exists only if
+                                  e * page_size + t < valid_tokens[b] (a ragged last page) */
+
+  const void* c_fp16;          /* [num_pages, page_size, qk_dim] f16 */
+  const void* c_fp8;           /* e4m3fn codes */
+  const void* c_int8;          /* int8 codes */
+  const void* c_fp8_scale; const void* c_int8_scale; int32_t scale_dtype;   /* [num_pages] */
+
+  float sm_scale;
+  int32_t pages_per_split;     /* 0 = automatic, else 1 .. 64 */
+} iak_mla_decode_args;
+
+/* Bytes of device workspace iak_mla_decode needs (0 when one split covers a sequence). */
+iak_status iak_mla_decode_workspace(const iak_mla_decode_args* args, size_t* bytes);
+
+/* MLA latent decode on MFMA, split-K over pages with an LSE merge; async on `stream`. */
+iak_status iak_mla_decode(const iak_mla_decode_args* args, void* workspace, size_t workspace_bytes,
+                          void* stream);
 
 #ifdef __cplusplus
 }

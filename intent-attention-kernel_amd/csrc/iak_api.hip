@@ -125,6 +125,88 @@ iak_status validate(const iak_paged_decode_args* a, Plan* plan) {
   return IAK_OK;
 }
 
+struct MPlan {
+  int splits, chunk, HG;
+  size_t ws_m, ws_l, ws_acc, total;
+};
+
+bool mla_shape_supported(int dqk, int dv) {
+  return (dqk == 64 && dv == 64) || (dqk == 128 && dv == 128) || (dqk == 256 && dv == 256) ||
+         (dqk == 512 && dv == 512) || (dqk == 576 && dv == 512) || (dqk == 576 && dv == 64);
+}
+
+iak_status validate_mla(const iak_mla_decode_args* a, MPlan* plan) {
+  if (!a) return fail(IAK_EINVAL, "args is NULL");
+  if (a->batch < 0 || a->num_heads <= 0 || a->table_width < 0 || a->num_pages < 0)
+    return fail(IAK_EINVAL, "negative or zero size (batch=%d, num_heads=%d, table_width=%d, num_pages=%lld)",
+                a->batch, a->num_heads, a->table_width, (long long)a->num_pages);
+  if (!mla_shape_supported(a->qk_dim, a->v_dim))
+    return fail(IAK_ENOTSUP, "MLA (qk_dim, v_dim) = (%d, %d) is not supported", a->qk_dim, a->v_dim);
+  if (a->v_offset < 0 || a->v_offset % 4 != 0 || a->v_offset + a->v_dim > a->qk_dim)
+    return fail(IAK_EINVAL, "v_offset %d must be a multiple of 4 with v_offset + v_dim <= qk_dim", a->v_offset);
+  if (a->page_size != 16) return fail(IAK_ENOTSUP, "page_size %d is not supported (16)", a->page_size);
+  if (a->num_pages > 0x7FFFFFFFLL) return fail(IAK_EINVAL, "num_pages %lld exceeds int32 page ids", (long long)a->num_pages);
+  if (a->q_dtype < 0 || a->q_dtype > 2 || a->out_dtype < 0 || a->out_dtype > 2)
+    return fail(IAK_EINVAL, "bad q/out dtype (%d, %d)", a->q_dtype, a->out_dtype);
+  if (!std::isfinite(a->sm_scale)) return fail(IAK_EINVAL, "sm_scale is not finite");
+  if (a->pages_per_split < 0 || a->pages_per_split > 64)
+    return fail(IAK_EINVAL, "pages_per_split %d outside [0, 64]", a->pages_per_split);
+  if (a->scale_dtype != IAK_DTYPE_F16 && a->scale_dtype != IAK_DTYPE_F32)
+    return fail(IAK_EINVAL, "scale dtype %d must be f16 or f32", a->scale_dtype);
+  if (a->batch > 0) {
+    if (!a->q || !a->out) return fail(IAK_EINVAL, "q/out is NULL");
+    const int qvec = a->q_dtype == IAK_DTYPE_F32 ? 4 : 8;
+    if (!aligned16(a->q) || a->q_stride_b % qvec != 0 || a->q_stride_h % qvec != 0)
+      return fail(IAK_EINVAL, "q must be 16-byte aligned with strides that are multiples of %d elements", qvec);
+    if (!a->page_table || !a->page_counts) return fail(IAK_EINVAL, "page_table/page_counts is NULL");
+  }
+  // latent pools reachable through the tag map (no tags: every page FP16)
+  for (int t = 0; t < 8; ++t) {
+    const int n = a->page_tags ? a->tag_map[t] : (t == 0 ? IAK_TAG_FP16 : IAK_TAG_SKIP);
+    const void *pool = nullptr, *sc = nullptr;
+    switch (n) {
+      case IAK_TAG_FP16: pool = a->c_fp16; sc = pool; break;
+      case IAK_TAG_FP8: pool = a->c_fp8; sc = a->c_fp8_scale; break;
+      case IAK_TAG_INT8: pool = a->c_int8; sc = a->c_int8_scale; break;
+      case IAK_TAG_INT4:
+      case IAK_TAG_INT4_RESIDUAL:
+        return fail(IAK_ENOTSUP, "tag %d maps to %s, which MLA latent pages do not support", t, tag_name(n));
+      default: continue;
+    }
+    if (!pool || !sc) return fail(IAK_EINVAL, "tag %d maps to %s but its latent pool or scales are NULL", t, tag_name(n));
+    if (!aligned16(pool)) return fail(IAK_EINVAL, "%s latent pool must be 16-byte aligned", tag_name(n));
+  }
+
+  // split plan: one workgroup per (sequence, split, 64 heads); enough
+  // workgroups for every CU when the table is long enough
+  const int W = a->table_width;
+  const int HG = (a->num_heads + 63) / 64;
+  int chunk = a->pages_per_split;
+  if (chunk == 0) {
+    const long long units = (long long)a->batch * HG;
+    const long long want = units > 0 ? (256 + units - 1) / units : 1;
+    chunk = (int)((W + want - 1) / (want > 0 ? want : 1));
+    if (chunk > 64) chunk = 64;
+    if (chunk < 1) chunk = 1;
+  }
+  int splits = (W + chunk - 1) / chunk;
+  if (splits < 1) splits = 1;
+  if ((long long)a->batch * splits > 0x7FFFFFFFLL || HG > 65535) return fail(IAK_EINVAL, "too many splits");
+  plan->splits = splits;
+  plan->chunk = chunk;
+  plan->HG = HG;
+  if (splits == 1) {
+    plan->ws_m = plan->ws_l = plan->ws_acc = plan->total = 0;
+  } else {
+    const size_t slots = (size_t)a->batch * splits * a->num_heads;
+    plan->ws_m = 0;
+    plan->ws_l = round_up(slots * sizeof(float));
+    plan->ws_acc = plan->ws_l + round_up(slots * sizeof(float));
+    plan->total = plan->ws_acc + round_up(slots * a->v_dim * sizeof(float));
+  }
+  return IAK_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -198,6 +280,55 @@ iak_status iak_paged_decode(const iak_paged_decode_args* a, void* workspace, siz
     k.ws_acc = reinterpret_cast<float*>(ws + plan.ws_acc);
   }
   const hipError_t e = iak::launch_paged_decode(k, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(IAK_EHIP, "kernel launch failed: %s", hipGetErrorString(e));
+  return IAK_OK;
+}
+
+iak_status iak_mla_decode_workspace(const iak_mla_decode_args* args, size_t* bytes) {
+  if (!bytes) return fail(IAK_EINVAL, "bytes is NULL");
+  MPlan plan;
+  const iak_status st = validate_mla(args, &plan);
+  if (st != IAK_OK) return st;
+  *bytes = plan.total;
+  return IAK_OK;
+}
+
+iak_status iak_mla_decode(const iak_mla_decode_args* a, void* workspace, size_t workspace_bytes, void* stream) {
+  MPlan plan;
+  iak_status st = validate_mla(a, &plan);
+  if (st != IAK_OK) return st;
+  if (a->batch == 0) return IAK_OK;
+  if (plan.total > 0 && (!workspace || workspace_bytes < plan.total))
+    return fail(IAK_EINVAL, "workspace of %zu bytes is smaller than the %zu bytes required", workspace_bytes, plan.total);
+  if (plan.total > 0 && !aligned16(workspace)) return fail(IAK_EINVAL, "workspace must be 16-byte aligned");
+
+  iak::MArgs m;
+  std::memset(&m, 0, sizeof(m));
+  m.B = a->batch; m.H = a->num_heads; m.DQK = a->qk_dim; m.DV = a->v_dim; m.VOFF = a->v_offset;
+  m.W = a->table_width; m.NP = a->num_pages;
+  m.splits = plan.splits; m.chunk = plan.chunk; m.HG = plan.HG;
+  m.q = a->q; m.q_dtype = a->q_dtype; m.qsb = a->q_stride_b; m.qsh = a->q_stride_h;
+  m.out = a->out; m.out_dtype = a->out_dtype; m.osb = a->out_stride_b; m.osh = a->out_stride_h;
+  m.table = a->page_table; m.counts = a->page_counts; m.tags = a->page_tags;
+  uint64_t map = 0;
+  for (int t = 0; t < 8; ++t) {
+    int n = a->tag_map[t];
+    if (n != IAK_TAG_FP16 && n != IAK_TAG_INT8 && n != IAK_TAG_FP8) n = IAK_TAG_SKIP;
+    map |= (uint64_t)n << (8 * t);
+  }
+  m.tagmap = map;
+  m.neg_wrap = a->negative_ids != 0;
+  m.valid = a->valid_tokens;
+  m.c16 = a->c_fp16; m.c8f = a->c_fp8; m.c8i = a->c_int8;
+  m.s8f = a->c_fp8_scale; m.s8i = a->c_int8_scale; m.sd = a->scale_dtype;
+  m.score_mult = a->sm_scale * 1.4426950408889634f;
+  if (plan.total > 0) {
+    char* ws = static_cast<char*>(workspace);
+    m.ws_m = reinterpret_cast<float*>(ws + plan.ws_m);
+    m.ws_l = reinterpret_cast<float*>(ws + plan.ws_l);
+    m.ws_acc = reinterpret_cast<float*>(ws + plan.ws_acc);
+  }
+  const hipError_t e = iak::launch_mla_decode(m, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(IAK_EHIP, "kernel launch failed: %s", hipGetErrorString(e));
   return IAK_OK;
 }

@@ -1,0 +1,206 @@
+// Device helpers shared by the libiak kernels (selected-page decode and MLA
+// latent decode): packed f16 conversions of quantised codes, lane-swap
+// reductions and the split-K log-sum-exp merge.
+#ifndef IAK_DEVICE_H
+#define IAK_DEVICE_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "iak.h"
+#include "iak_internal.h"
+
+namespace iak {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+
+constexpr int PS = 16;
+constexpr float RESCALE_SLACK = 8.0f;      // p <= 2^8 between rescales
+constexpr uint32_t MAGIC_I8 = 0x64646464u;  // f16 0x64xx = 1024 + xx
+constexpr uint32_t MAGIC_I4 = 0x64006400u;
+
+__device__ __forceinline__ uint32_t bits(h2 v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
+__device__ __forceinline__ h2 splat2(_Float16 x) { return h2{x, x}; }
+
+__device__ __forceinline__ h8 make_h8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  u4 v = {a, b, c, d};
+  return __builtin_bit_cast(h8, v);
+}
+__device__ __forceinline__ h4 make_h4(uint32_t a, uint32_t b) {
+  u2 v = {a, b};
+  return __builtin_bit_cast(h4, v);
+}
+
+// (lo16(x), lo16(y)) and (hi16(x), hi16(y)) as one dword
+__device__ __forceinline__ uint32_t pack_lo(uint32_t x, uint32_t y) {
+  return __builtin_amdgcn_perm(y, x, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t pack_hi(uint32_t x, uint32_t y) {
+  return __builtin_amdgcn_perm(y, x, 0x07060302u);
+}
+
+// Four signed int8 -> two f16 pairs (b0,b1), (b2,b3), exactly.
+__device__ __forceinline__ void i8x4_to_f16(uint32_t x, uint32_t& lo, uint32_t& hi) {
+  const uint32_t u = x ^ 0x80808080u;                          // b + 128
+  const h2 off = splat2((_Float16)-1152.0f);                   // 1024 + 128
+  lo = bits(as_h2(__builtin_amdgcn_perm(MAGIC_I8, u, 0x04010400u)) + off);
+  hi = bits(as_h2(__builtin_amdgcn_perm(MAGIC_I8, u, 0x04030402u)) + off);
+}
+
+// Four e4m3fn bytes -> two f16 pairs (b0,b1), (b2,b3), exactly.
+__device__ __forceinline__ void fp8x4_to_f16(uint32_t x, uint32_t& lo, uint32_t& hi) {
+  lo = bits(__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x, 1.0f, false));
+  hi = bits(__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x, 1.0f, true));
+}
+
+// Nibbles at bits 0-3 and 16-19 of y (code + 8) -> f16 pair of codes, exactly.
+__device__ __forceinline__ h2 nib_pair(uint32_t y) {
+  return as_h2((y & 0x000F000Fu) | MAGIC_I4) + splat2((_Float16)-1032.0f);
+}
+
+// Eight packed INT4 codes (element j = nibble j) -> four f16 pairs in element
+// order, multiplied by scale s.
+__device__ __forceinline__ void i4x8_to_f16(uint32_t x, h2 s, uint32_t o[4]) {
+  const h2 p04 = nib_pair(x) * s;         // (e0, e4)
+  const h2 p15 = nib_pair(x >> 4) * s;    // (e1, e5)
+  const h2 p26 = nib_pair(x >> 8) * s;    // (e2, e6)
+  const h2 p37 = nib_pair(x >> 12) * s;   // (e3, e7)
+  o[0] = pack_lo(bits(p04), bits(p15));
+  o[1] = pack_lo(bits(p26), bits(p37));
+  o[2] = pack_hi(bits(p04), bits(p15));
+  o[3] = pack_hi(bits(p26), bits(p37));
+}
+
+// Four INT4_RESIDUAL bytes (base | resid<<4) -> two f16 pairs of base*s0 + resid*s1.
+__device__ __forceinline__ void i4r_x4_to_f16(uint32_t x, h2 s0, h2 s1, uint32_t& lo, uint32_t& hi) {
+  const h2 b02 = nib_pair(x), r02 = nib_pair(x >> 4);
+  const h2 b13 = nib_pair(x >> 8), r13 = nib_pair(x >> 12);
+  const h2 v02 = __builtin_elementwise_fma(r02, s1, b02 * s0);
+  const h2 v13 = __builtin_elementwise_fma(r13, s1, b13 * s0);
+  lo = pack_lo(bits(v02), bits(v13));
+  hi = pack_hi(bits(v02), bits(v13));
+}
+
+// Cross-lane reductions over the lanes {l, l^16, l^32, l^48} with the gfx950
+// lane-swap instructions (VALU, no LDS round trip): v_permlane32_swap v, t
+// with t = v leaves (v[0:32] | v[0:32]) in v and (v[32:64] | v[32:64]) in t,
+// so max(v, t) in every lane is the max over lanes l and l^32;
+// v_permlane16_swap does the same for l and l^16. Written as one asm block:
+// the compiler's own folding drops a float op on the two swap results (it
+// treats the second output as an unmodified copy of the input). s_nop 1 is
+// the wait the compiler inserts between a VALU write and a lane swap.
+__device__ __forceinline__ float xmax16_32(float v) {
+  float t;
+  asm volatile(
+      "v_mov_b32 %1, %0\n\t"
+      "s_nop 1\n\t"
+      "v_permlane32_swap_b32 %0, %1\n\t"
+      "v_max_f32 %0, %0, %1\n\t"
+      "v_mov_b32 %1, %0\n\t"
+      "s_nop 1\n\t"
+      "v_permlane16_swap_b32 %0, %1\n\t"
+      "v_max_f32 %0, %0, %1"
+      : "+v"(v), "=&v"(t));
+  return v;
+}
+__device__ __forceinline__ float xsum16_32(float v) {
+  float t;
+  asm volatile(
+      "v_mov_b32 %1, %0\n\t"
+      "s_nop 1\n\t"
+      "v_permlane32_swap_b32 %0, %1\n\t"
+      "v_add_f32 %0, %0, %1\n\t"
+      "v_mov_b32 %1, %0\n\t"
+      "s_nop 1\n\t"
+      "v_permlane16_swap_b32 %0, %1\n\t"
+      "v_add_f32 %0, %0, %1"
+      : "+v"(v), "=&v"(t));
+  return v;
+}
+
+template <typename T> __device__ __forceinline__ T ld(const T* p) { return *p; }
+
+__device__ __forceinline__ float load_scale(const void* p, int64_t idx, int dtype) {
+  if (dtype == IAK_DTYPE_F32) return reinterpret_cast<const float*>(p)[idx];
+  return (float)reinterpret_cast<const _Float16*>(p)[idx];
+}
+
+// Index of the lowest set bit of `mask`, which is then cleared.
+__device__ __forceinline__ int take(uint64_t& mask) {
+  const int idx = __builtin_ctzll(mask);
+  mask &= mask - 1;
+  return idx;
+}
+
+__device__ __forceinline__ float u2f(uint32_t x) { return __builtin_bit_cast(float, x); }
+__device__ __forceinline__ uint32_t f2u(float x) { return __builtin_bit_cast(uint32_t, x); }
+
+// --------------------------------------------------------------------------- //
+// Cross-split merge: one wave per (batch, query head). Partial slot of split s
+// of head c in row (b, hk): ((b * Hkv + hk) * splits + s) * G + c.
+// --------------------------------------------------------------------------- //
+
+template <int D>
+__global__ __launch_bounds__(256) void splitk_merge_kernel(const KArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int bh = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (bh >= a.B * a.Hq) return;
+  const int b = bh / a.Hq, h = bh - b * a.Hq;
+  const int hk = h / a.G, c = h - hk * a.G;
+  const int S = a.splits;
+  const int64_t first = (((int64_t)b * a.Hkv + hk) * S) * a.G + c;   // slot of split 0
+  // global max over the splits: lanes read splits in parallel, then reduce
+  float M = -__builtin_inff();
+  for (int s = lane; s < S; s += 64) M = fmaxf(M, a.ws_m[first + (int64_t)s * a.G]);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+  constexpr int PER = D / 64;   // dims per lane
+  float o[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) o[j] = 0.f;
+  float L = 0.f;
+  if (M > -__builtin_inff()) {
+    // eight splits per step with their loads issued together
+    constexpr int U = 8;
+    int s = 0;
+    for (; s < S; s += U) {
+      float ms[U], ls[U], av[U][PER];
+#pragma unroll
+      for (int k = 0; k < U; ++k) {
+        const int64_t slot = first + (int64_t)(s + k < S ? s + k : S - 1) * a.G;
+        ms[k] = a.ws_m[slot];
+        ls[k] = a.ws_l[slot];
+        const float* ap = a.ws_acc + slot * D + PER * lane;
+#pragma unroll
+        for (int j = 0; j < PER; ++j) av[k][j] = ap[j];
+      }
+#pragma unroll
+      for (int k = 0; k < U; ++k) {
+        // 0 for empty splits (m = -inf) and for the clamped reloads past S
+        const float wgt = s + k < S ? __builtin_amdgcn_exp2f(ms[k] - M) : 0.f;
+        L += wgt * ls[k];
+#pragma unroll
+        for (int j = 0; j < PER; ++j) o[j] += wgt * av[k][j];
+      }
+    }
+  }
+  const float inv = L > 0.f ? 1.0f / L : 0.f;
+  const int64_t base = (int64_t)b * a.osb + (int64_t)h * a.osh + PER * lane;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const float v = o[j] * inv;
+    if (a.out_dtype == IAK_DTYPE_F32) reinterpret_cast<float*>(a.out)[base + j] = v;
+    else if (a.out_dtype == IAK_DTYPE_F16) reinterpret_cast<_Float16*>(a.out)[base + j] = (_Float16)v;
+    else reinterpret_cast<__bf16*>(a.out)[base + j] = (__bf16)v;
+  }
+}
+
+}  // namespace iak
+
+#endif

@@ -56,6 +56,36 @@ struct KArgs {
 
 hipError_t launch_paged_decode(const KArgs& k, hipStream_t stream);
 
+// Kernel-side arguments of the MLA latent decode (built from iak_mla_decode_args).
+struct MArgs {
+  int B, H, DQK, DV, VOFF, W;
+  int64_t NP;
+  int splits;   // splits per sequence
+  int chunk;    // table entries per split (<= 64)
+  int HG;       // groups of 128 heads
+
+  const void* q; int q_dtype; int64_t qsb, qsh;
+  void* out; int out_dtype; int64_t osb, osh;
+
+  const int32_t* table;
+  const int32_t* counts;
+  const int32_t* tags;     // may be null: every page FP16
+  uint64_t tagmap;
+  int neg_wrap;
+  const int32_t* valid;    // [B] token bound per sequence, may be null
+
+  const void* c16; const void* c8f; const void* c8i;
+  const void* s8f; const void* s8i; int sd;
+
+  float score_mult;   // sm_scale * log2(e)
+
+  float* ws_m;        // [B, splits, H]
+  float* ws_l;        // [B, splits, H]
+  float* ws_acc;      // [B, splits, H, DV]
+};
+
+hipError_t launch_mla_decode(const MArgs& m, hipStream_t stream);
+
 }  // namespace iak
 
 #endif

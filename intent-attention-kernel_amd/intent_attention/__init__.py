@@ -38,6 +38,9 @@ from .intent_quant_decode import (
     make_precision_tensor,
 )
 from .decode_core import PagePools, paged_decode
+from .mla import MLABlockTable, MLAConfig, absorb_weights, mla_sparse_decode_reference, mla_triton_decode
+from .mla_core import LatentPools, mla_paged_decode
+from .triton_mla_decode import mla_decode_triton
 
 __all__ = [
     "SELECTED_POLICIES", "BlockLayout", "BlockPolicy", "SemanticBlock",
@@ -50,4 +53,6 @@ __all__ = [
     "IntentQuantKernelConfig", "TritonKVPrecision", "fake_int8_pages_from_fp16",
     "intent_quant_decode_attention_triton", "make_page_tables_from_selected_pages", "make_precision_tensor",
     "PagePools", "paged_decode",
+    "MLABlockTable", "MLAConfig", "absorb_weights", "mla_sparse_decode_reference", "mla_triton_decode",
+    "LatentPools", "mla_paged_decode", "mla_decode_triton",
 ]

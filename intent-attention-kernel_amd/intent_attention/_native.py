@@ -51,8 +51,29 @@ class PagedDecodeArgs(ctypes.Structure):
     ]
 
 
+class MlaDecodeArgs(ctypes.Structure):
+    """Mirror of ``iak_mla_decode_args`` (include/iak.h)."""
+
+    _fields_ = [
+        ("batch", c_i32), ("num_heads", c_i32), ("qk_dim", c_i32), ("v_dim", c_i32), ("v_offset", c_i32),
+        ("page_size", c_i32), ("table_width", c_i32),
+        ("num_pages", c_i64),
+        ("q", c_void_p), ("q_dtype", c_i32), ("q_stride_b", c_i64), ("q_stride_h", c_i64),
+        ("out", c_void_p), ("out_dtype", c_i32), ("out_stride_b", c_i64), ("out_stride_h", c_i64),
+        ("page_table", c_void_p), ("page_counts", c_void_p), ("page_tags", c_void_p),
+        ("tag_map", ctypes.c_uint8 * 8),
+        ("negative_ids", c_i32),
+        ("valid_tokens", c_void_p),
+        ("c_fp16", c_void_p), ("c_fp8", c_void_p), ("c_int8", c_void_p),
+        ("c_fp8_scale", c_void_p), ("c_int8_scale", c_void_p), ("scale_dtype", c_i32),
+        ("sm_scale", c_float),
+        ("pages_per_split", c_i32),
+    ]
+
+
 EXPORTED = ("iak_abi_version", "iak_status_string", "iak_last_error",
-            "iak_paged_decode_workspace", "iak_paged_decode")
+            "iak_paged_decode_workspace", "iak_paged_decode",
+            "iak_mla_decode_workspace", "iak_mla_decode")
 
 _lib: Optional[ctypes.CDLL] = None
 _load_error: Optional[str] = None
@@ -82,6 +103,10 @@ def load() -> ctypes.CDLL:
     lib.iak_paged_decode_workspace.argtypes = [ctypes.POINTER(PagedDecodeArgs), ctypes.POINTER(ctypes.c_size_t)]
     lib.iak_paged_decode.restype = ctypes.c_int
     lib.iak_paged_decode.argtypes = [ctypes.POINTER(PagedDecodeArgs), c_void_p, ctypes.c_size_t, c_void_p]
+    lib.iak_mla_decode_workspace.restype = ctypes.c_int
+    lib.iak_mla_decode_workspace.argtypes = [ctypes.POINTER(MlaDecodeArgs), ctypes.POINTER(ctypes.c_size_t)]
+    lib.iak_mla_decode.restype = ctypes.c_int
+    lib.iak_mla_decode.argtypes = [ctypes.POINTER(MlaDecodeArgs), c_void_p, ctypes.c_size_t, c_void_p]
     ver = lib.iak_abi_version()
     if ver != ABI_VERSION:
         _load_error = f"libiak.so ABI version {ver} != expected {ABI_VERSION}; rebuild the library"
@@ -110,3 +135,13 @@ def workspace_bytes(args: PagedDecodeArgs) -> int:
 
 def paged_decode(args: PagedDecodeArgs, workspace_ptr: int, workspace_size: int, stream: int) -> None:
     check(load().iak_paged_decode(ctypes.byref(args), workspace_ptr or None, workspace_size, stream or None))
+
+
+def mla_workspace_bytes(args: MlaDecodeArgs) -> int:
+    n = ctypes.c_size_t(0)
+    check(load().iak_mla_decode_workspace(ctypes.byref(args), ctypes.byref(n)))
+    return int(n.value)
+
+
+def mla_decode(args: MlaDecodeArgs, workspace_ptr: int, workspace_size: int, stream: int) -> None:
+    check(load().iak_mla_decode(ctypes.byref(args), workspace_ptr or None, workspace_size, stream or None))

@@ -31,12 +31,15 @@ def test_library_exports_every_declared_symbol():
     assert lib.iak_status_string(0) == b"ok"
 
 
-def test_ctypes_struct_matches_c_layout():
+@pytest.mark.parametrize("cname,pyname", [("iak_paged_decode_args", "PagedDecodeArgs"),
+                                          ("iak_mla_decode_args", "MlaDecodeArgs")])
+def test_ctypes_struct_matches_c_layout(cname, pyname):
     from intent_attention import _native as N
-    fields = [f[0] for f in N.PagedDecodeArgs._fields_]
+    S = getattr(N, pyname)
+    fields = [f[0] for f in S._fields_]
     prog = ['#include <stdio.h>', '#include <stddef.h>', '#include "iak.h"', 'int main(void){',
-            'printf("size %zu\\n", sizeof(iak_paged_decode_args));']
-    prog += [f'printf("{f} %zu\\n", offsetof(iak_paged_decode_args, {f}));' for f in fields]
+            f'printf("size %zu\\n", sizeof({cname}));']
+    prog += [f'printf("{f} %zu\\n", offsetof({cname}, {f}));' for f in fields]
     prog += ["return 0;}"]
     with tempfile.TemporaryDirectory() as d:
         c = os.path.join(d, "probe.c")
@@ -45,9 +48,9 @@ def test_ctypes_struct_matches_c_layout():
         subprocess.run(["gcc", "-std=c11", "-I", os.path.join(ROOT, "include"), c, "-o", exe], check=True)
         got = dict(line.split() for line in subprocess.run([exe], capture_output=True, text=True,
                                                            check=True).stdout.splitlines())
-    assert int(got["size"]) == ctypes.sizeof(N.PagedDecodeArgs)
+    assert int(got["size"]) == ctypes.sizeof(S)
     for f in fields:
-        assert int(got[f]) == getattr(N.PagedDecodeArgs, f).offset, f
+        assert int(got[f]) == getattr(S, f).offset, f
 
 
 def test_validation_errors_without_gpu():
@@ -74,4 +77,32 @@ def test_validation_errors_without_gpu():
     a.tag_map[3] = N.TAG_SKIP
     a.sm_scale = 0.1
     n = N.workspace_bytes(a)     # 2 rows x 100 pages: split into several chunks -> workspace
+    assert n > 0 and n % 256 == 0
+
+
+def test_mla_validation_errors_without_gpu():
+    from intent_attention import _native as N
+    a = N.MlaDecodeArgs()
+    a.batch, a.num_heads, a.qk_dim, a.v_dim, a.page_size = 2, 128, 576, 576, 16
+    with pytest.raises(ValueError, match="not supported"):
+        N.mla_workspace_bytes(a)
+    a.v_dim, a.v_offset = 512, 128
+    with pytest.raises(ValueError, match="v_offset"):
+        N.mla_workspace_bytes(a)
+    a.v_offset, a.page_size = 0, 64
+    with pytest.raises(ValueError, match="page_size 64"):
+        N.mla_workspace_bytes(a)
+    a.page_size, a.table_width, a.num_pages = 16, 512, 1024
+    a.q = a.out = a.page_table = a.page_counts = a.page_tags = 16
+    for i in range(8):
+        a.tag_map[i] = N.TAG_SKIP
+    a.tag_map[1] = N.TAG_INT4
+    with pytest.raises(ValueError, match="INT4"):
+        N.mla_workspace_bytes(a)
+    a.tag_map[1] = N.TAG_INT8     # INT8 reachable but no latent pool
+    with pytest.raises(ValueError, match="INT8"):
+        N.mla_workspace_bytes(a)
+    a.tag_map[1] = N.TAG_SKIP
+    a.sm_scale = 0.04
+    n = N.mla_workspace_bytes(a)  # 2 sequences x 512 pages: 64-page splits -> partials
     assert n > 0 and n % 256 == 0

@@ -165,3 +165,30 @@ def test_mla_decode_golden(g5):
     assert np.abs(cf - g5["out"]).max() < 1e-4
     empty = M.mla_decode_cpu_loop(g5["q_absorb"], g5["C"], g5["W_VO"], [], ps)
     assert np.all(empty == 0) and np.all(g5["out_empty"] == 0)
+
+
+def test_mla_paged_oracle_equals_reference_loop():
+    """The paged form (per-sequence tables, tags, token bound) reduces to the
+    restated reference loop on an FP16 pool with full pages, and a token bound
+    equals truncating the gathered rows."""
+    rng = np.random.default_rng(7)
+    B, H, d, NP = 2, 5, 32, 12
+    pool = rng.standard_normal((NP, 16, d)).astype(np.float16)
+    q = rng.standard_normal((B, H, d))
+    ids = np.array([3, 0, 7, 7, 11], np.int32)
+    table = np.stack([ids, ids])
+    counts = np.array([5, 5])
+    got = M.mla_paged_decode_oracle(q, {"c_fp16": pool}, table, counts)
+    ref = M.mla_decode_cpu_loop(q, pool.reshape(-1, d), np.eye(d), ids, page_size=16)
+    assert np.abs(got - ref).max() < 1e-12
+    # token bound of 70 = 4 full pages + 6 tokens of the fifth
+    got = M.mla_paged_decode_oracle(q, {"c_fp16": pool}, table, counts, valid_tokens=np.array([70, 70]))
+    rows = np.concatenate([pool[p].astype(np.float64) for p in ids], 0)[:70]
+    assert np.abs(got - M.mla_decode_closed_form(q, rows)).max() < 1e-12
+    # SKIP pages and a zero count contribute nothing
+    tags = np.zeros(NP, np.int32)
+    tags[7] = Dm.SKIP
+    got = M.mla_paged_decode_oracle(q, {"c_fp16": pool}, table, np.array([5, 0]), tags)
+    rows = np.concatenate([pool[p].astype(np.float64) for p in (3, 0, 11)], 0)
+    assert np.abs(got[0] - M.mla_decode_closed_form(q[:1], rows)[0]).max() < 1e-12
+    assert np.all(got[1] == 0)
