@@ -265,13 +265,158 @@ def cpu_baseline(wl, rows: int, budget_s: float = 20.0) -> dict:
 
 
 # --------------------------------------------------------------------------- #
+# MLA latent decode (cfg5)
+# --------------------------------------------------------------------------- #
+
+MLA_CONFIGS = {
+    # DeepSeek-V3-style latent decode: 512 latent + 64 RoPE dims shared by 128 heads,
+    # 16,384-token context in 16-token pages, half the pages selected, latent pages
+    # half FP8-e4m3 / half INT8 with one scale per page.
+    "cfg5": dict(B=32, H=128, DQK=576, DV=512, T=16384, sel=0.5, mix={TAG_FP8: .5, TAG_INT8: .5}),
+}
+MLA_SETS = 4          # independent page sets rotated per step (4 x 151 MB > 256 MB MALL)
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def build_mla_workload(name: str, device: torch.device, seed: int = 4321):
+    from intent_attention import LatentPools
+    cfg = MLA_CONFIGS[name]
+    B, H, DQK, T = cfg["B"], cfg["H"], cfg["DQK"], cfg["T"]
+    P = T // PS
+    NP = MLA_SETS * B * P
+    g = torch.Generator(device=device).manual_seed(seed)
+    gc = torch.Generator().manual_seed(seed)
+    tags_list = list(cfg["mix"])
+    probs = torch.tensor([cfg["mix"][t] for t in tags_list])
+    tags = torch.tensor(tags_list, dtype=torch.int32)[torch.multinomial(probs, NP, replacement=True, generator=gc)]
+    tags = tags.to(device)
+    pools = LatentPools(c_fp8=torch.zeros((NP, PS, DQK), dtype=torch.uint8, device=device),
+                        c_fp8_scale=torch.zeros(NP, dtype=torch.float16, device=device),
+                        c_int8=torch.zeros((NP, PS, DQK), dtype=torch.int8, device=device),
+                        c_int8_scale=torch.zeros(NP, dtype=torch.float16, device=device))
+    for lo in range(0, NP, 16384):
+        hi = min(NP, lo + 16384)
+        x = torch.randn((hi - lo, PS, DQK), generator=g, device=device, dtype=torch.float32).half()
+        t = tags[lo:hi]
+        for tag, (pool, sc) in ((TAG_FP8, ("c_fp8", "c_fp8_scale")), (TAG_INT8, ("c_int8", "c_int8_scale"))):
+            idx = torch.nonzero(t == tag).flatten()
+            if idx.numel():
+                codes, scales = quantize_pages(x[idx], tag)
+                getattr(pools, pool)[lo + idx] = codes
+                getattr(pools, sc)[lo + idx] = scales.to(torch.float16)
+    nsel = int(cfg["sel"] * P)
+    tables = []
+    for s in range(MLA_SETS):
+        base = s * B * P
+        perm = (torch.randperm(B * P, generator=gc) + base).to(torch.int32).reshape(B, P)
+        logical = torch.stack([torch.randperm(P, generator=gc)[:nsel].sort().values for _ in range(B)])
+        tables.append(torch.gather(perm, 1, logical).contiguous().to(device))
+    counts = torch.full((B,), nsel, dtype=torch.int32, device=device)
+    q = torch.randn((B, H, DQK), generator=g, device=device).half()
+    return dict(cfg=cfg, name=name, q=q, pools=pools, tables=tables, counts=counts, tags=tags, NP=NP, W=nsel)
+
+
+def mla_step_cost(wl) -> dict:
+    cfg = wl["cfg"]
+    B, H, DQK, DV = cfg["B"], cfg["H"], cfg["DQK"], cfg["DV"]
+    toks = B * wl["W"] * PS
+    flop = 2.0 * H * toks * (DQK + DV)
+    codes = B * wl["W"] * PS * DQK                    # one byte per latent element
+    scales = B * wl["W"] * 2 + B * wl["W"] * (4 + 4)  # fp16 scale + page id + tag per page
+    qo = wl["q"].numel() * 2 + B * H * DV * 2
+    return dict(flop=flop, bytes=codes + scales + qo, tokens=toks)
+
+
+def mla_cpu_baseline(wl, seqs: int = 4, budget_s: float = 20.0) -> dict:
+    from threadpoolctl import threadpool_limits
+
+    from oracle.mla import mla_paged_decode_oracle
+    cfg = wl["cfg"]
+    p = wl["pools"]
+    table = wl["tables"][0]
+    done, t0 = 0, time.perf_counter()
+    with threadpool_limits(limits=1):
+        for b in range(min(seqs, cfg["B"])):
+            ids = table[b].long()
+            uniq, inv = torch.unique(ids, return_inverse=True)
+            pools = {"c_fp8": p.c_fp8[uniq].cpu().numpy(), "c_fp8_scale": p.c_fp8_scale[uniq].cpu().numpy(),
+                     "c_i8": p.c_int8[uniq].cpu().numpy(), "c_i8_scale": p.c_int8_scale[uniq].cpu().numpy()}
+            tags = wl["tags"][uniq].cpu().numpy()
+            mla_paged_decode_oracle(wl["q"][b:b + 1].cpu().numpy(), pools, inv[None].cpu().numpy().astype(np.int32),
+                                    np.array([wl["W"]]), tags, v_dim=cfg["DV"])
+            done += 1
+            if time.perf_counter() - t0 > budget_s:
+                break
+    dt = time.perf_counter() - t0
+    step_s = dt * cfg["B"] / done
+    return {"value": mla_step_cost(wl)["flop"] / step_s / 1e12, "unit": "TFLOP/s", "us_per_step": step_s * 1e6,
+            "cores": 1, "kind": "port",
+            "sample": f"oracle.mla.mla_paged_decode_oracle (numpy float64, 1 thread) on {done} of {cfg['B']} "
+                      f"sequences of {wl['name']}, {dt:.1f} s, scaled to the full step"}
+
+
+def run_mla(args) -> None:
+    from intent_attention.mla_core import make_mla_plan
+    dev = torch.device("cuda:0")
+    t_build = time.perf_counter()
+    wl = build_mla_workload(args.config, dev)
+    torch.cuda.synchronize()
+    print(f"[bench] built {args.config}: NP={wl['NP']} W={wl['W']} in {time.perf_counter() - t_build:.1f}s",
+          file=sys.stderr, flush=True)
+    cfg = wl["cfg"]
+    out = torch.empty((cfg["B"], cfg["H"], cfg["DV"]), dtype=torch.float16, device=dev)
+    plans = [make_mla_plan(wl["q"], wl["pools"], t, wl["counts"], wl["tags"], v_dim=cfg["DV"], out=out,
+                           pages_per_split=args.pages_per_split) for t in wl["tables"]]
+    stream = torch.cuda.current_stream(dev)
+    for i in range(args.warmup):
+        plans[i % MLA_SETS].run()
+    torch.cuda.synchronize()
+    t_start, t_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t_start.record(stream)
+    for i in range(args.steps):
+        plans[i % MLA_SETS].run()
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    ms = t_start.elapsed_time(t_end) / args.steps
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    for i, (s, e) in enumerate(ev):
+        s.record(stream)
+        plans[i % MLA_SETS].run()
+        e.record(stream)
+    torch.cuda.synchronize()
+    per = sorted(s.elapsed_time(e) for s, e in ev)
+    cost = mla_step_cost(wl)
+    tflops = cost["flop"] / (ms * 1e-3) / 1e12
+    res = {
+        "metric": "MLA latent decode µs/step + MFMA TFLOP/s (cfg5, DeepSeek-V3-style)", "value": round(tflops, 1),
+        "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+        "us_per_step": round(ms * 1e3, 2),
+        "us_per_step_p10_p50_p90": [round(per[len(per) // 10] * 1e3, 2), round(per[len(per) // 2] * 1e3, 2),
+                                    round(per[(9 * len(per)) // 10] * 1e3, 2)],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+        "data": "synthetic (seeded; latent N(0,1) fp16 pages quantised with the reference's fake-quant arithmetic)",
+        "config": {"workload": f"{args.config}: MLA decode B={cfg['B']} heads={cfg['H']} latent {cfg['DV']}+"
+                               f"{cfg['DQK'] - cfg['DV']} ctx={cfg['T']} page=16 sel={wl['W']} pages/seq "
+                               f"mix=FP8/INT8 50/50, {MLA_SETS} page sets rotated",
+                   "selected_tokens": cost["tokens"], "algorithmic_bytes": cost["bytes"],
+                   "gflop": round(cost["flop"] / 1e9, 3), "pages_per_split": plans[0].args.pages_per_split},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None,
+                     "hbm_gbps": round(cost["bytes"] / (ms * 1e-3) / 1e9, 1)},
+    }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = mla_cpu_baseline(wl)
+    print(json.dumps(res), flush=True)
+
+
+# --------------------------------------------------------------------------- #
 
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS) + sorted(MLA_CONFIGS))
     ap.add_argument("--pages-per-split", type=int, default=0)
     ap.add_argument("--cpu-rows", type=int, default=192, help="rows of the step the CPU baseline times")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -285,6 +430,9 @@ def main() -> None:
               file=sys.stderr)
         sys.exit(2)
 
+    if args.config in MLA_CONFIGS:
+        run_mla(args)
+        return
     from intent_attention.decode_core import make_plan
     dev = torch.device("cuda:0")
     t_build = time.perf_counter()

@@ -317,6 +317,10 @@ iak_status iak_mla_decode(const iak_mla_decode_args* a, void* workspace, size_t 
     map |= (uint64_t)n << (8 * t);
   }
   m.tagmap = map;
+  m.wide = 0;
+  for (int t = 0; t < 8; ++t)
+    if (((map >> (8 * t)) & 0xFFu) == IAK_TAG_FP16) m.wide = 1;
+  if (!a->page_tags) m.wide = 1;
   m.neg_wrap = a->negative_ids != 0;
   m.valid = a->valid_tokens;
   m.c16 = a->c_fp16; m.c8f = a->c_fp8; m.c8i = a->c_int8;

@@ -76,6 +76,7 @@ struct MArgs {
 
   const void* c16; const void* c8f; const void* c8i;
   const void* s8f; const void* s8i; int sd;
+  int wide;           // FP16 latent pages are reachable
 
   float score_mult;   // sm_scale * log2(e)
 

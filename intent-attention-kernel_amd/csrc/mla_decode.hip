@@ -39,7 +39,7 @@
 
 namespace iak {
 
-template <int DQK, int DV> struct Mla {
+template <int DQK, int DV, bool WIDE> struct Mla {
   static constexpr int WAVES = 4;
   static constexpr int THREADS = 64 * WAVES;
   static constexpr int QB = 1;                 // score head blocks (of 16) per wave
@@ -50,27 +50,24 @@ template <int DQK, int DV> struct Mla {
   static constexpr int NDB = DVW / 16;         // 16-dim blocks per wave
   static constexpr int T1 = DQK + 8;           // [token][dim] row stride (halves)
   static constexpr int T2 = 20;                // [dim][token] row stride (halves)
-  static constexpr int UNITS16 = PS * DQK * 2 / 16;   // 16-byte units of an FP16 page
-  static constexpr int UNITS8 = PS * DQK / 16;         // of a one-byte page
-  static constexpr int U = (UNITS16 + THREADS - 1) / THREADS;   // loads per thread per page
+  static constexpr int PAGE8 = PS * DQK;       // bytes of a one-byte page (a multiple of 1 KB)
+  static constexpr int SLOT = WIDE ? 2 * PAGE8 : PAGE8;   // raw ring slot: the widest page
+  static constexpr int NDMA = (SLOT / 1024 + WAVES - 1) / WAVES;   // 1 KB copies per wave per page
+  static constexpr int RING = 4;               // raw slots: pages stream in two steps ahead
   static constexpr int TASKS = DQK;            // 4 tokens x 4 dims per staging task
-  static_assert(DQK % 32 == 0 && DV % 64 == 0 && DV <= DQK, "unsupported MLA shape");
+  static_assert(DQK % 32 == 0 && DV % 64 == 0 && DV <= DQK && PAGE8 % 1024 == 0, "unsupported MLA shape");
 };
 
-template <int DQK, int DV> struct MlaShared {
-  _Float16 t1[2][PS][Mla<DQK, DV>::T1];   // [buffer][token][dim]
-  _Float16 t2[2][DV][Mla<DQK, DV>::T2];   // [buffer][value dim][token]
-  u4 raw[Mla<DQK, DV>::UNITS8];           // one-byte codes of the page being staged
-  u2 pbuf[Mla<DQK, DV>::HB][64];          // P of every head block, A-operand layout
-  alignas(16) float alpha[Mla<DQK, DV>::HEADS];   // rescale factor of every head this page
-  float lsum[Mla<DQK, DV>::HEADS];        // final denominators
-  float mmax[Mla<DQK, DV>::HEADS];        // final maxima
-  int grow[Mla<DQK, DV>::WAVES];
-};
-
-// Registers of one page being staged by this thread.
-template <int DQK, int DV> struct MlaRegs {
-  u4 r[Mla<DQK, DV>::U];
+template <int DQK, int DV, bool WIDE> struct MlaShared {
+  using C = Mla<DQK, DV, WIDE>;
+  _Float16 t1[2][PS][C::T1];              // [buffer][token][dim]
+  _Float16 t2[2][DV][C::T2];              // [buffer][value dim][token]
+  alignas(16) uint8_t ring[C::RING][C::SLOT];   // raw pages as copied from HBM
+  u2 pbuf[C::HB][64];                     // P of every head block, A-operand layout
+  alignas(16) float alpha[C::HEADS];      // rescale factor of every head this page
+  float lsum[C::HEADS];                   // final denominators
+  float mmax[C::HEADS];                   // final maxima
+  int grow[C::WAVES];
 };
 
 // Page metadata of one split: lane i holds entry i.
@@ -108,71 +105,62 @@ __device__ __forceinline__ MlaPages mla_page_meta(const MArgs& a, int b, int sta
   return m;
 }
 
-// Global -> registers: the U 16-byte units of page `pid` this thread stages
-// (unit tid + THREADS*k; past the page's last unit the last unit is loaded
-// again, so every page issues the same loads).
-template <int DQK, int DV>
-__device__ __forceinline__ void mla_stage_load(MlaRegs<DQK, DV>& rg, const MArgs& a, int pid, int tag, int tid) {
-  using C = Mla<DQK, DV>;
-  const bool wide = tag == IAK_TAG_FP16;
-  const int units = wide ? C::UNITS16 : C::UNITS8;
-  const uint8_t* base = wide ? reinterpret_cast<const uint8_t*>(a.c16) + (int64_t)pid * PS * DQK * 2
+// HBM -> LDS ring slot: the page's 1 KB chunks are copied straight into LDS
+// (global_load_lds_dwordx4: lane i's 16 bytes land at the slot offset + 16 i),
+// chunk w + WAVES*k by wave w. Every wave issues NDMA copies per page -- past
+// the page's last chunk the last chunk is copied again -- so the number of
+// copies in flight per wave is fixed and each wait is a constant vmcnt. The
+// copies bypass the registers; the compiler does not see them, so the waits
+// for them are written out (mla_wait_pages) and no compiler-issued load runs
+// inside the page loop.
+template <int DQK, int DV, bool WIDE>
+__device__ __forceinline__ void mla_dma_page(MlaShared<DQK, DV, WIDE>& sh, int slot, const MArgs& a, int pid,
+                                             int tag, int w, int lane) {
+  using C = Mla<DQK, DV, WIDE>;
+  const bool wide = WIDE && tag == IAK_TAG_FP16;
+  const int nch = (wide ? 2 * C::PAGE8 : C::PAGE8) / 1024;
+  const uint8_t* base = wide ? reinterpret_cast<const uint8_t*>(a.c16) + (int64_t)pid * C::PAGE8 * 2
                              : reinterpret_cast<const uint8_t*>(tag == IAK_TAG_FP8 ? a.c8f : a.c8i) +
-                                   (int64_t)pid * PS * DQK;
+                                   (int64_t)pid * C::PAGE8;
+  typedef __attribute__((address_space(3))) uint8_t lds_u8;
 #pragma unroll
-  for (int k = 0; k < C::U; ++k) {
-    int u = tid + C::THREADS * k;
-    u = u < units ? u : units - 1;
-    rg.r[k] = *reinterpret_cast<const u4*>(base + (int64_t)u * 16);
+  for (int k = 0; k < C::NDMA; ++k) {
+    int ch = w + C::WAVES * k;
+    ch = ch < nch ? ch : nch - 1;
+    const uint8_t* src = base + (int64_t)ch * 1024 + 16 * lane;
+    const uint32_t dst = (uint32_t)(uintptr_t)(lds_u8*)&sh.ring[slot][ch * 1024];
+    asm volatile("global_load_lds_dwordx4 %0, off" : : "v"(src), "{m0}"(dst) : "memory");
   }
 }
 
-// Registers -> LDS: FP16 units straight into the [token][dim] tile, one-byte
-// codes into the raw buffer.
-template <int DQK, int DV>
-__device__ __forceinline__ void mla_stage_store(MlaShared<DQK, DV>& sh, const MlaRegs<DQK, DV>& rg, int buf,
-                                                int tag, int tid) {
-  using C = Mla<DQK, DV>;
-  if (tag == IAK_TAG_FP16) {
-#pragma unroll
-    for (int k = 0; k < C::U; ++k) {
-      const int u = tid + C::THREADS * k;
-      if (u < C::UNITS16) {
-        const int t = u / (DQK / 8), d = 8 * (u % (DQK / 8));
-        *reinterpret_cast<u4*>(&sh.t1[buf][t][d]) = rg.r[k];
-      }
-    }
-  } else {
-#pragma unroll
-    for (int k = 0; k < C::U; ++k) {
-      const int u = tid + C::THREADS * k;
-      if (u < C::UNITS8) sh.raw[u] = rg.r[k];
-    }
-  }
+// Wait until at most `pages` pages of this wave's ring copies are in flight.
+template <int NDMA, int PAGES> __device__ __forceinline__ void mla_wait_pages() {
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(NDMA * PAGES) : "memory");
 }
 
 // LDS -> tiles: each task takes 4 tokens x 4 dims, converts one-byte codes to
 // f16 (exact) into the [token][dim] tile and writes the value dims transposed
 // into the [dim][token] tile.
-template <int DQK, int DV>
-__device__ __forceinline__ void mla_stage_tiles(MlaShared<DQK, DV>& sh, int buf, int tag, int voff, int tid) {
-  using C = Mla<DQK, DV>;
+template <int DQK, int DV, bool WIDE>
+__device__ __forceinline__ void mla_stage_tiles(MlaShared<DQK, DV, WIDE>& sh, int slot, int buf, int tag, int voff,
+                                                int tid) {
+  using C = Mla<DQK, DV, WIDE>;
   for (int task = tid; task < C::TASKS; task += C::THREADS) {
     const int tg = task / (DQK / 4), d = 4 * (task % (DQK / 4));
     uint32_t lo[4], hi[4];   // token 4tg+t: f16 pairs (d, d+1), (d+2, d+3)
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const int tok = 4 * tg + t;
-      if (tag == IAK_TAG_FP16) {
-        const u2 x = *reinterpret_cast<const u2*>(&sh.t1[buf][tok][d]);
+      if (WIDE && tag == IAK_TAG_FP16) {
+        const u2 x = *reinterpret_cast<const u2*>(&sh.ring[slot][(tok * DQK + d) * 2]);
         lo[t] = x[0];
         hi[t] = x[1];
       } else {
-        const uint32_t x = reinterpret_cast<const uint32_t*>(sh.raw)[(tok * DQK + d) / 4];
+        const uint32_t x = *reinterpret_cast<const uint32_t*>(&sh.ring[slot][tok * DQK + d]);
         if (tag == IAK_TAG_FP8) fp8x4_to_f16(x, lo[t], hi[t]);
         else i8x4_to_f16(x, lo[t], hi[t]);
-        *reinterpret_cast<u2*>(&sh.t1[buf][tok][d]) = u2{lo[t], hi[t]};
       }
+      *reinterpret_cast<u2*>(&sh.t1[buf][tok][d]) = u2{lo[t], hi[t]};
     }
     const int vd = d - voff;
     if (vd >= 0 && vd < DV) {
@@ -184,10 +172,10 @@ __device__ __forceinline__ void mla_stage_tiles(MlaShared<DQK, DV>& sh, int buf,
   }
 }
 
-template <int DQK, int DV>
+template <int DQK, int DV, bool WIDE>
 __global__ __launch_bounds__(256, 1) void mla_decode_kernel(const MArgs a) {
-  using C = Mla<DQK, DV>;
-  __shared__ MlaShared<DQK, DV> sh;
+  using C = Mla<DQK, DV, WIDE>;
+  __shared__ MlaShared<DQK, DV, WIDE> sh;
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
   const int c = lane & 15, g = lane >> 4;
@@ -250,47 +238,65 @@ __global__ __launch_bounds__(256, 1) void mla_decode_kernel(const MArgs a) {
       if (rem) last = take(rem);
       return last;
     };
-    MlaRegs<DQK, DV> regs[2];
-    int idx0 = next_page();
-    int idx1 = next_page();
-    mla_stage_load<DQK, DV>(regs[0], a, __builtin_amdgcn_readlane(meta.pid, idx0),
-                            __builtin_amdgcn_readlane(meta.tag, idx0), tid);
-    mla_stage_load<DQK, DV>(regs[1], a, __builtin_amdgcn_readlane(meta.pid, idx1),
-                            __builtin_amdgcn_readlane(meta.tag, idx1), tid);
-    {
-      const int tag0 = __builtin_amdgcn_readlane(meta.tag, idx0);
-      mla_stage_store<DQK, DV>(sh, regs[0], 0, tag0, tid);
-      __syncthreads();
-      mla_stage_tiles<DQK, DV>(sh, 0, tag0, a.VOFF, tid);
-      __syncthreads();
+    auto page_pid = [&](int idx) { return __builtin_amdgcn_readlane(meta.pid, idx); };
+    auto page_tag = [&](int idx) { return __builtin_amdgcn_readlane(meta.tag, idx); };
+    // pages 0 .. RING-2 start streaming into ring slots 0 .. RING-2; page 0 is
+    // staged into tile buffer 0. qi[k] = lane of page j+k.
+    int qi[C::RING - 1];
+#pragma unroll
+    for (int k = 0; k < C::RING - 1; ++k) {
+      qi[k] = next_page();
+      mla_dma_page<DQK, DV, WIDE>(sh, k, a, page_pid(qi[k]), page_tag(qi[k]), w, lane);
     }
-    int cur = idx0, nxt = idx1;
+    mla_wait_pages<C::NDMA, C::RING - 2>();
+    __syncthreads();
+    mla_stage_tiles<DQK, DV, WIDE>(sh, 0, 0, page_tag(qi[0]), a.VOFF, tid);
+    __syncthreads();
 
-    // One page: stage page j+1 into the other buffer, then scores and values
-    // of page j. `R` is the buffer (and register set) of page j.
+    // One page: page j+RING-1 starts streaming, page j+1 (landed) is staged into
+    // the other tile buffer, then scores and values of page j. `R` is the tile
+    // buffer of page j; page p streams into ring slot p % RING.
     auto step = [&](auto RC, int j) {
       constexpr int R = decltype(RC)::value;
-      const int idx2 = next_page();
-      mla_stage_load<DQK, DV>(regs[R], a, __builtin_amdgcn_readlane(meta.pid, idx2),
-                              __builtin_amdgcn_readlane(meta.tag, idx2), tid);
-      const bool have_next = j + 1 < np;
-      const int tagn = __builtin_amdgcn_readlane(meta.tag, nxt);
-      if (have_next) mla_stage_store<DQK, DV>(sh, regs[1 - R], 1 - R, tagn, tid);
-      __syncthreads();
-      if (have_next) mla_stage_tiles<DQK, DV>(sh, 1 - R, tagn, a.VOFF, tid);
+      const int cur = qi[0], nxt = qi[1];
+      const int inew = next_page();
+      mla_dma_page<DQK, DV, WIDE>(sh, (j + C::RING - 1) % C::RING, a, page_pid(inew), page_tag(inew), w, lane);
 
-      if (j >= np) return;
-      // ---- scores of page j (buffer R) for the wave's head blocks ----
+      // ---- scores of page j (buffer R) for the wave's head blocks, issued
+      // first so the MFMAs run while the wave stages page j+1; in a step past
+      // the end they see stale data and their result is dropped ----
       const float pscale = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, meta.scale), cur));
       const float smul = a.score_mult * pscale;
-      f4 s[C::QB];
+      // NCH independent accumulation chains keep the MFMA pipe busy; summed after
+      constexpr int NCH = C::KSTEPS >= 4 ? 4 : C::KSTEPS;
+      f4 s[C::QB], sc[C::QB][NCH];
 #pragma unroll
-      for (int k = 0; k < C::QB; ++k) s[k] = f4{0.f, 0.f, 0.f, 0.f};
+      for (int k = 0; k < C::QB; ++k)
+#pragma unroll
+        for (int ch = 0; ch < NCH; ++ch) sc[k][ch] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int i = 0; i < C::KSTEPS; ++i) {
         const h8 av = *reinterpret_cast<const h8*>(&sh.t1[R][c][32 * i + 8 * g]);
 #pragma unroll
-        for (int k = 0; k < C::QB; ++k) s[k] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, q[k][i], s[k], 0, 0, 0);
+        for (int k = 0; k < C::QB; ++k)
+          sc[k][i % NCH] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, q[k][i], sc[k][i % NCH], 0, 0, 0);
+      }
+
+      // ---- stage page j+1 (landed: this wave's copies, then every wave's) ----
+      const bool have_next = j + 1 < np;
+      mla_wait_pages<C::NDMA, C::RING - 2>();
+      __syncthreads();
+      if (have_next) mla_stage_tiles<DQK, DV, WIDE>(sh, (j + 1) % C::RING, 1 - R, page_tag(nxt), a.VOFF, tid);
+#pragma unroll
+      for (int k = 0; k < C::RING - 2; ++k) qi[k] = qi[k + 1];
+      qi[C::RING - 2] = inew;
+
+      if (j >= np) return;
+#pragma unroll
+      for (int k = 0; k < C::QB; ++k) {
+        s[k] = sc[k][0];
+#pragma unroll
+        for (int ch = 1; ch < NCH; ++ch) s[k] += sc[k][ch];
       }
       float pm[C::QB];
       bool grow[C::QB];
@@ -354,11 +360,9 @@ __global__ __launch_bounds__(256, 1) void mla_decode_kernel(const MArgs a) {
         for (int db = 0; db < C::NDB; ++db)
           acc[hb][db] = __builtin_amdgcn_mfma_f32_16x16x16f16(aop, bop[db], acc[hb][db], 0, 0, 0);
       }
-      cur = nxt;
-      nxt = idx2;
     };
 
-    // pages in pairs so the buffer and register-set indices are static
+    // pages in pairs so the tile-buffer indices are static
     // (both steps of a pair always run -- an exit between them makes the
     // compiler keep two copies of the accumulators -- and a step past the end
     // issues its loads but skips its compute)
@@ -366,6 +370,8 @@ __global__ __launch_bounds__(256, 1) void mla_decode_kernel(const MArgs a) {
       step(std::integral_constant<int, 0>{}, j);
       step(std::integral_constant<int, 1>{}, j + 1);
     }
+    // the copies of the pages past the end land before the LDS is reused or released
+    mla_wait_pages<C::NDMA, 0>();
   }
 
   // ---- denominators and maxima of every head, then the output or the partials ----
@@ -410,10 +416,10 @@ __global__ __launch_bounds__(256, 1) void mla_decode_kernel(const MArgs a) {
   }
 }
 
-template <int DQK, int DV>
-hipError_t launch_mla(const MArgs& m, hipStream_t stream) {
-  hipLaunchKernelGGL((mla_decode_kernel<DQK, DV>), dim3(m.B * m.splits, m.HG), dim3(Mla<DQK, DV>::THREADS), 0,
-                     stream, m);
+template <int DQK, int DV, bool WIDE>
+hipError_t launch_mla_w(const MArgs& m, hipStream_t stream) {
+  hipLaunchKernelGGL((mla_decode_kernel<DQK, DV, WIDE>), dim3(m.B * m.splits, m.HG),
+                     dim3(Mla<DQK, DV, WIDE>::THREADS), 0, stream, m);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || m.splits == 1) return e;
   // the paged-decode merge over rows (b, 0) of H heads
@@ -424,6 +430,12 @@ hipError_t launch_mla(const MArgs& m, hipStream_t stream) {
   const int mblocks = (m.B * m.H + 3) / 4;
   hipLaunchKernelGGL((splitk_merge_kernel<DV>), dim3(mblocks), dim3(256), 0, stream, k);
   return hipGetLastError();
+}
+
+// WIDE: FP16 latent pages are reachable (ring slots sized for two bytes per value)
+template <int DQK, int DV>
+hipError_t launch_mla(const MArgs& m, hipStream_t stream) {
+  return m.wide ? launch_mla_w<DQK, DV, true>(m, stream) : launch_mla_w<DQK, DV, false>(m, stream);
 }
 
 hipError_t launch_mla_decode(const MArgs& m, hipStream_t stream) {
