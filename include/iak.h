@@ -17,6 +17,9 @@
  *                               (the latent context; mla_sparse_decode_reference mla.py:61-92,
  *                               mla_triton_decode mla.py:95-136)
  *   iak_mla_decode_workspace    (no counterpart: sizes the split-K partial buffer)
+ *   iak_quantize_pages          fake_quantize_tensor() intent_quant.py:221-312 at page granules, and
+ *                               fake_int8_pages_from_fp16() fused_selected_quant_decode.py:521-542 /
+ *                               triton_intent_quant_attention.py:460-496
  *   iak_status_string           (no counterpart: the reference raises ValueError/RuntimeError in Python)
  */
 #ifndef IAK_H
@@ -174,6 +177,39 @@ iak_status iak_mla_decode_workspace(const iak_mla_decode_args* args, size_t* byt
 /* MLA latent decode on MFMA, split-K over pages with an LSE merge; async on `stream`. */
 iak_status iak_mla_decode(const iak_mla_decode_args* args, void* workspace, size_t workspace_bytes,
                           void* stream);
+
+/*
+ * Quantise-on-write: float16 pages [num_pages, page_size, head_dim] -> codes and
+ * scales of one pool, page p written to pool page dst_pages[p] (or p when
+ * dst_pages is NULL); pages whose destination lies outside [0, pool_pages)
+ * are not written. Layouts are those of iak_paged_decode_args.
+ *   mode IAK_QUANT_FAKE_QUANTIZE: fake_quantize_tensor (intent_quant.py:221-312) at the
+ *        page granule (INT4: page x int4_group channels); precision FP8, INT8, INT4 or
+ *        INT4_RESIDUAL; arithmetic in float16 (INT4_RESIDUAL residual in float32).
+ *   mode IAK_QUANT_FUSED_INT8:  fake_int8_pages_from_fp16, fused_selected_quant_decode.py:521-542
+ *        (float16; clamp(round(x/s), -128, 127)); precision INT8.
+ *   mode IAK_QUANT_TRITON_INT8: fake_int8_pages_from_fp16, triton_intent_quant_attention.py:460-496
+ *        (float32; clamp(round(x/s), -127, 127)); precision INT8.
+ * scale_dtype: F16 or F32 for one scale per page or group; INT4_RESIDUAL writes
+ * [pool_pages, 2] f32 (base, residual) pairs.
+ */
+enum { IAK_QUANT_FAKE_QUANTIZE = 0, IAK_QUANT_FUSED_INT8 = 1, IAK_QUANT_TRITON_INT8 = 2 };
+
+typedef struct {
+  int32_t num_pages, page_size, head_dim;
+  const void* src;              /* f16 [num_pages, page_size, head_dim] */
+  const int32_t* dst_pages;     /* [num_pages] or NULL */
+  int64_t pool_pages;
+  int32_t precision;            /* IAK_TAG_FP8 / INT8 / INT4 / INT4_RESIDUAL */
+  int32_t mode;
+  int32_t int4_group;
+  void* codes;                  /* pool codes (INT4: head_dim/2 bytes per token) */
+  void* scales;                 /* pool scales */
+  int32_t scale_dtype;
+} iak_quantize_args;
+
+/* Quantise pages into a pool; async on `stream`. */
+iak_status iak_quantize_pages(const iak_quantize_args* args, void* stream);
 
 #ifdef __cplusplus
 }

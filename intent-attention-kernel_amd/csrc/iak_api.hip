@@ -337,4 +337,34 @@ iak_status iak_mla_decode(const iak_mla_decode_args* a, void* workspace, size_t 
   return IAK_OK;
 }
 
+iak_status iak_quantize_pages(const iak_quantize_args* a, void* stream) {
+  if (!a) return fail(IAK_EINVAL, "args is NULL");
+  if (a->num_pages < 0 || a->pool_pages < 0) return fail(IAK_EINVAL, "negative page count");
+  if (a->head_dim != 64 && a->head_dim != 128)
+    return fail(IAK_ENOTSUP, "head_dim %d is not supported (64 or 128)", a->head_dim);
+  if (a->page_size != 16) return fail(IAK_ENOTSUP, "page_size %d is not supported (16)", a->page_size);
+  const int p = a->precision, m = a->mode;
+  if (m == IAK_QUANT_FAKE_QUANTIZE) {
+    if (p != IAK_TAG_FP8 && p != IAK_TAG_INT8 && p != IAK_TAG_INT4 && p != IAK_TAG_INT4_RESIDUAL)
+      return fail(IAK_EINVAL, "precision %d cannot be quantised (FP8, INT8, INT4 or INT4_RESIDUAL)", p);
+  } else if (m == IAK_QUANT_FUSED_INT8 || m == IAK_QUANT_TRITON_INT8) {
+    if (p != IAK_TAG_INT8) return fail(IAK_EINVAL, "mode %d writes INT8 pages only", m);
+  } else {
+    return fail(IAK_EINVAL, "unknown quantisation mode %d", m);
+  }
+  if (p == IAK_TAG_INT4) {
+    const int grp = a->int4_group, D = a->head_dim;
+    if (grp <= 0 || D % grp != 0 || grp % (D / 4) != 0)
+      return fail(IAK_ENOTSUP, "int4_group %d must divide head_dim %d and be a multiple of %d", grp, D, D / 4);
+  }
+  if (a->scale_dtype != IAK_DTYPE_F16 && a->scale_dtype != IAK_DTYPE_F32)
+    return fail(IAK_EINVAL, "scale dtype %d must be f16 or f32", a->scale_dtype);
+  if (a->num_pages == 0) return IAK_OK;
+  if (!a->src || !a->codes || !a->scales) return fail(IAK_EINVAL, "src/codes/scales is NULL");
+  if (!aligned16(a->src) || !aligned16(a->codes)) return fail(IAK_EINVAL, "src and codes must be 16-byte aligned");
+  const hipError_t e = iak::launch_quantize_pages(*a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(IAK_EHIP, "kernel launch failed: %s", hipGetErrorString(e));
+  return IAK_OK;
+}
+
 }  // extern "C"

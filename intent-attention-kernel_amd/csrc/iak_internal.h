@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "iak.h"
+
 #define IAK_WAVES_PER_BLOCK 4
 #define IAK_MIN_WAVES_PER_SIMD 3
 // pages per ring in each precision class loop (one computed, the rest in flight)
@@ -86,6 +88,8 @@ struct MArgs {
 };
 
 hipError_t launch_mla_decode(const MArgs& m, hipStream_t stream);
+
+hipError_t launch_quantize_pages(const iak_quantize_args& a, hipStream_t stream);
 
 }  // namespace iak
 

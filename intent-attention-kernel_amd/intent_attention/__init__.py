@@ -41,6 +41,7 @@ from .decode_core import PagePools, paged_decode
 from .mla import MLABlockTable, MLAConfig, absorb_weights, mla_sparse_decode_reference, mla_triton_decode
 from .mla_core import LatentPools, mla_paged_decode
 from .triton_mla_decode import mla_decode_triton
+from .quantize import fake_int8_pages_device, quantize_pages
 
 __all__ = [
     "SELECTED_POLICIES", "BlockLayout", "BlockPolicy", "SemanticBlock",
@@ -55,4 +56,5 @@ __all__ = [
     "PagePools", "paged_decode",
     "MLABlockTable", "MLAConfig", "absorb_weights", "mla_sparse_decode_reference", "mla_triton_decode",
     "LatentPools", "mla_paged_decode", "mla_decode_triton",
+    "quantize_pages", "fake_int8_pages_device",
 ]

@@ -71,9 +71,23 @@ class MlaDecodeArgs(ctypes.Structure):
     ]
 
 
+QUANT_FAKE_QUANTIZE, QUANT_FUSED_INT8, QUANT_TRITON_INT8 = 0, 1, 2
+
+
+class QuantizeArgs(ctypes.Structure):
+    """Mirror of ``iak_quantize_args`` (include/iak.h)."""
+
+    _fields_ = [
+        ("num_pages", c_i32), ("page_size", c_i32), ("head_dim", c_i32),
+        ("src", c_void_p), ("dst_pages", c_void_p), ("pool_pages", c_i64),
+        ("precision", c_i32), ("mode", c_i32), ("int4_group", c_i32),
+        ("codes", c_void_p), ("scales", c_void_p), ("scale_dtype", c_i32),
+    ]
+
+
 EXPORTED = ("iak_abi_version", "iak_status_string", "iak_last_error",
             "iak_paged_decode_workspace", "iak_paged_decode",
-            "iak_mla_decode_workspace", "iak_mla_decode")
+            "iak_mla_decode_workspace", "iak_mla_decode", "iak_quantize_pages")
 
 _lib: Optional[ctypes.CDLL] = None
 _load_error: Optional[str] = None
@@ -107,6 +121,8 @@ def load() -> ctypes.CDLL:
     lib.iak_mla_decode_workspace.argtypes = [ctypes.POINTER(MlaDecodeArgs), ctypes.POINTER(ctypes.c_size_t)]
     lib.iak_mla_decode.restype = ctypes.c_int
     lib.iak_mla_decode.argtypes = [ctypes.POINTER(MlaDecodeArgs), c_void_p, ctypes.c_size_t, c_void_p]
+    lib.iak_quantize_pages.restype = ctypes.c_int
+    lib.iak_quantize_pages.argtypes = [ctypes.POINTER(QuantizeArgs), c_void_p]
     ver = lib.iak_abi_version()
     if ver != ABI_VERSION:
         _load_error = f"libiak.so ABI version {ver} != expected {ABI_VERSION}; rebuild the library"
@@ -145,3 +161,7 @@ def mla_workspace_bytes(args: MlaDecodeArgs) -> int:
 
 def mla_decode(args: MlaDecodeArgs, workspace_ptr: int, workspace_size: int, stream: int) -> None:
     check(load().iak_mla_decode(ctypes.byref(args), workspace_ptr or None, workspace_size, stream or None))
+
+
+def quantize_pages(args: QuantizeArgs, stream: int) -> None:
+    check(load().iak_quantize_pages(ctypes.byref(args), stream or None))

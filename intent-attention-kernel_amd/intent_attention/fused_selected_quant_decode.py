@@ -175,6 +175,10 @@ def fake_int8_pages_from_fp16(pages: torch.Tensor, eps: float = 1e-6) -> Tuple[t
     the same name in this module (:521-542); the division is a true division
     on every device.
     """
+    if (pages.is_cuda and eps == 1e-6 and pages.dtype == torch.float16 and pages.dim() == 3
+            and pages.shape[1] == 16 and pages.shape[2] in (64, 128)):
+        from .quantize import fake_int8_pages_device
+        return fake_int8_pages_device(pages, "fused")        # the same arithmetic on the HIP quantiser
     n = pages.shape[0]
     flat = pages.view(n, -1)
     absmax = flat.abs().amax(dim=1, keepdim=True).clamp(min=eps)

@@ -168,6 +168,10 @@ def fake_int8_pages_from_fp16(pages: torch.Tensor, *, eps: float = 1e-6) -> Tupl
     arithmetic, clamp_min(eps), /127, round half even, clamp(-127, 127)."""
     if pages.ndim != 3:
         raise ValueError("pages must have shape [num_pages, page_size, D]")
+    if (pages.is_cuda and eps == 1e-6 and pages.dtype == torch.float16 and pages.shape[1] == 16
+            and pages.shape[2] in (64, 128)):
+        from .quantize import fake_int8_pages_device
+        return fake_int8_pages_device(pages, "triton")       # the same arithmetic on the HIP quantiser
     n = pages.shape[0]
     flat = pages.float().reshape(n, -1)
     scales = flat.abs().amax(dim=1).clamp_min(eps) / torch.full((1,), 127.0, device=flat.device)

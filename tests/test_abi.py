@@ -32,7 +32,8 @@ def test_library_exports_every_declared_symbol():
 
 
 @pytest.mark.parametrize("cname,pyname", [("iak_paged_decode_args", "PagedDecodeArgs"),
-                                          ("iak_mla_decode_args", "MlaDecodeArgs")])
+                                          ("iak_mla_decode_args", "MlaDecodeArgs"),
+                                          ("iak_quantize_args", "QuantizeArgs")])
 def test_ctypes_struct_matches_c_layout(cname, pyname):
     from intent_attention import _native as N
     S = getattr(N, pyname)
@@ -106,3 +107,23 @@ def test_mla_validation_errors_without_gpu():
     a.sm_scale = 0.04
     n = N.mla_workspace_bytes(a)  # 2 sequences x 512 pages: 64-page splits -> partials
     assert n > 0 and n % 256 == 0
+
+
+def test_quantize_validation_errors_without_gpu():
+    from intent_attention import _native as N
+    a = N.QuantizeArgs()
+    a.num_pages, a.page_size, a.head_dim, a.pool_pages = 4, 16, 96, 4
+    with pytest.raises(ValueError, match="head_dim 96"):
+        N.quantize_pages(a, 0)
+    a.head_dim, a.precision, a.mode = 128, N.TAG_FP16, N.QUANT_FAKE_QUANTIZE
+    with pytest.raises(ValueError, match="cannot be quantised"):
+        N.quantize_pages(a, 0)
+    a.precision, a.mode = N.TAG_FP8, N.QUANT_FUSED_INT8
+    with pytest.raises(ValueError, match="INT8 pages only"):
+        N.quantize_pages(a, 0)
+    a.precision, a.mode, a.int4_group = N.TAG_INT4, N.QUANT_FAKE_QUANTIZE, 48
+    with pytest.raises(ValueError, match="int4_group 48"):
+        N.quantize_pages(a, 0)
+    a.int4_group, a.scale_dtype = 32, N.DTYPE_F16
+    with pytest.raises(ValueError, match="NULL"):
+        N.quantize_pages(a, 0)
