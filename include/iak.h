@@ -20,6 +20,9 @@
  *   iak_quantize_pages          fake_quantize_tensor() intent_quant.py:221-312 at page granules, and
  *                               fake_int8_pages_from_fp16() fused_selected_quant_decode.py:521-542 /
  *                               triton_intent_quant_attention.py:460-496
+ *   iak_build_page_tables       routing_to_kernel_metadata() block_router.py:383-421 (page ids: selected_page_ids
+ *                               :283-296) followed by metadata_to_kernel_tensors()
+ *                               fused_selected_quant_decode.py:344-400 (the loop :394-398)
  *   iak_status_string           (no counterpart: the reference raises ValueError/RuntimeError in Python)
  */
 #ifndef IAK_H
@@ -210,6 +213,51 @@ typedef struct {
 
 /* Quantise pages into a pool; async on `stream`. */
 iak_status iak_quantize_pages(const iak_quantize_args* args, void* stream);
+
+/*
+ * Page tables from routed spans (the selected blocks of a routing decision,
+ * in routed order), built on the device.
+ *
+ * Row r (of num_rows = batch * kv_heads; row b * kv_heads + h) reads span list
+ * r / rows_per_list and block-table row r / rows_per_seq. Its logical pages
+ * are t / page_size for the tokens start <= t < end of each span, span by
+ * span, each page once at its first occurrence (dedupe = 1,
+ * block_router.py:283-296) or once per span (dedupe = 0). A logical page l
+ * maps to block_table[seq * block_table_width + l] (l >= block_table_width or
+ * a negative entry: not resident) or to l without a block table; pages whose
+ * physical id is outside [0, num_pages) are dropped. Outputs:
+ *   page_table [num_rows, table_width]: the first table_width ids, zeros after;
+ *   page_counts [num_rows]: min(ids, table_width);
+ *   page_precision [num_pages] (optional): the tag of the span that emitted the
+ *     page in the lowest row emitting it (the smallest tag if that row emits it
+ *     twice), default_tag elsewhere; pages past table_width count.
+ * With one list for all rows, no block table and dedupe = 1 the three outputs
+ * equal metadata_to_kernel_tensors(routing_to_kernel_metadata(blocks,
+ * page_size), num_pages, B, H) whenever every selected page is below
+ * num_pages (the reference raises IndexError otherwise).
+ * span_offsets has ceil(num_rows / rows_per_list) + 1 entries (CSR into the
+ * span arrays); span_tag holds IAK_TAG_* values. Work is proportional to the
+ * pages the lists name; a list whose pages span more than 16384 ids tests
+ * first occurrence against its earlier spans (quadratic in spans).
+ */
+typedef struct {
+  int32_t num_rows, rows_per_seq, rows_per_list;
+  int32_t table_width, page_size, num_pages;
+  int32_t dedupe;
+  int32_t default_tag;
+  int32_t block_table_width;
+  const int32_t* span_offsets;
+  const int32_t* span_begin;
+  const int32_t* span_end;
+  const int32_t* span_tag;
+  const int32_t* block_table;   /* [num_seqs, block_table_width] or NULL */
+  int32_t* page_table;
+  int32_t* page_counts;
+  int32_t* page_precision;      /* or NULL */
+} iak_page_table_args;
+
+/* Build page tables; async on `stream`. */
+iak_status iak_build_page_tables(const iak_page_table_args* args, void* stream);
 
 #ifdef __cplusplus
 }

@@ -367,4 +367,29 @@ iak_status iak_quantize_pages(const iak_quantize_args* a, void* stream) {
   return IAK_OK;
 }
 
+iak_status iak_build_page_tables(const iak_page_table_args* a, void* stream) {
+  if (!a) return fail(IAK_EINVAL, "args is NULL");
+  if (a->num_rows < 0 || a->table_width < 0 || a->num_pages < 0)
+    return fail(IAK_EINVAL, "negative num_rows / table_width / num_pages");
+  if (a->rows_per_seq <= 0 || a->rows_per_list <= 0)
+    return fail(IAK_EINVAL, "rows_per_seq and rows_per_list must be positive");
+  if (a->page_size <= 0) return fail(IAK_EINVAL, "page_size must be positive, got %d", a->page_size);
+  if (a->dedupe != 0 && a->dedupe != 1) return fail(IAK_EINVAL, "dedupe must be 0 or 1");
+  if (a->default_tag < IAK_TAG_FP16 || a->default_tag > IAK_TAG_INT4_RESIDUAL)
+    return fail(IAK_EINVAL, "default_tag %d is not a page tag", a->default_tag);
+  if (a->block_table && a->block_table_width <= 0)
+    return fail(IAK_EINVAL, "block_table_width must be positive with a block table");
+  if (a->page_precision && a->num_rows >= (1 << 28))
+    return fail(IAK_ENOTSUP, "num_rows %d too large for the precision reduction (< 2^28)", a->num_rows);
+  if (a->num_rows > 0) {
+    if (!a->span_offsets || !a->span_begin || !a->span_end || !a->span_tag)
+      return fail(IAK_EINVAL, "span arrays must not be NULL");
+    if (!a->page_counts || (a->table_width > 0 && !a->page_table))
+      return fail(IAK_EINVAL, "page_table / page_counts is NULL");
+  }
+  const hipError_t e = iak::launch_page_tables(*a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(IAK_EHIP, "kernel launch failed: %s", hipGetErrorString(e));
+  return IAK_OK;
+}
+
 }  // extern "C"

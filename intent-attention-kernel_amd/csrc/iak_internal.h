@@ -91,6 +91,8 @@ hipError_t launch_mla_decode(const MArgs& m, hipStream_t stream);
 
 hipError_t launch_quantize_pages(const iak_quantize_args& a, hipStream_t stream);
 
+hipError_t launch_page_tables(const iak_page_table_args& a, hipStream_t stream);
+
 }  // namespace iak
 
 #endif

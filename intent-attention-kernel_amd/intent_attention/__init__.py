@@ -42,6 +42,7 @@ from .mla import MLABlockTable, MLAConfig, absorb_weights, mla_sparse_decode_ref
 from .mla_core import LatentPools, mla_paged_decode
 from .triton_mla_decode import mla_decode_triton
 from .quantize import fake_int8_pages_device, quantize_pages
+from .page_tables import build_page_tables, routing_to_kernel_tensors
 
 __all__ = [
     "SELECTED_POLICIES", "BlockLayout", "BlockPolicy", "SemanticBlock",
@@ -57,4 +58,5 @@ __all__ = [
     "MLABlockTable", "MLAConfig", "absorb_weights", "mla_sparse_decode_reference", "mla_triton_decode",
     "LatentPools", "mla_paged_decode", "mla_decode_triton",
     "quantize_pages", "fake_int8_pages_device",
+    "build_page_tables", "routing_to_kernel_tensors",
 ]

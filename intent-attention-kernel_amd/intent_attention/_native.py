@@ -85,9 +85,23 @@ class QuantizeArgs(ctypes.Structure):
     ]
 
 
+class PageTableArgs(ctypes.Structure):
+    """Mirror of ``iak_page_table_args`` (include/iak.h)."""
+
+    _fields_ = [
+        ("num_rows", c_i32), ("rows_per_seq", c_i32), ("rows_per_list", c_i32),
+        ("table_width", c_i32), ("page_size", c_i32), ("num_pages", c_i32),
+        ("dedupe", c_i32), ("default_tag", c_i32), ("block_table_width", c_i32),
+        ("span_offsets", c_void_p), ("span_begin", c_void_p), ("span_end", c_void_p), ("span_tag", c_void_p),
+        ("block_table", c_void_p),
+        ("page_table", c_void_p), ("page_counts", c_void_p), ("page_precision", c_void_p),
+    ]
+
+
 EXPORTED = ("iak_abi_version", "iak_status_string", "iak_last_error",
             "iak_paged_decode_workspace", "iak_paged_decode",
-            "iak_mla_decode_workspace", "iak_mla_decode", "iak_quantize_pages")
+            "iak_mla_decode_workspace", "iak_mla_decode", "iak_quantize_pages",
+            "iak_build_page_tables")
 
 _lib: Optional[ctypes.CDLL] = None
 _load_error: Optional[str] = None
@@ -165,3 +179,7 @@ def mla_decode(args: MlaDecodeArgs, workspace_ptr: int, workspace_size: int, str
 
 def quantize_pages(args: QuantizeArgs, stream: int) -> None:
     check(load().iak_quantize_pages(ctypes.byref(args), stream or None))
+
+
+def build_page_tables(args: PageTableArgs, stream: int) -> None:
+    check(load().iak_build_page_tables(ctypes.byref(args), stream or None))

@@ -79,6 +79,11 @@ def compute_block_scores(query_vector: torch.Tensor,
 
 
 def _pages(start: int, end: int, ps: int) -> range:
+    """The distinct ``t // ps`` of tokens ``start <= t < end`` in increasing
+    order (the reference walks the tokens, block_router.py:291-295): empty
+    when ``end <= start``."""
+    if end <= start:
+        return range(0)
     return range(start // ps, (end - 1) // ps + 1)
 
 

@@ -80,6 +80,19 @@ _NATIVE_NAME_TO_TAG = {"FP8": FusedKVPrecision.FP8, "INT4": FusedKVPrecision.INT
                        "INT4_RESIDUAL": FusedKVPrecision.INT4_RESIDUAL}
 
 
+def precision_tag(name: str, native_precisions: bool = False) -> int:
+    """Precision name -> page tag as metadata_to_kernel_tensors maps it
+    (fused_selected_quant_decode.py:379-389): "SKIP" -> SKIP, "INT8" / "INT4" /
+    "INT4_RESIDUAL" -> INT8, anything else (FP8 included) -> FP16; with
+    ``native_precisions`` FP8 / INT4 / INT4_RESIDUAL keep their native tags."""
+    name = getattr(name, "value", name)          # KVPrecision members or their names
+    tag = _NAME_TO_TAG.get(name, FusedKVPrecision.FP16)
+    if name in _NATIVE_NAME_TO_TAG:
+        tag = _NATIVE_NAME_TO_TAG[name] if native_precisions else (
+            FusedKVPrecision.INT8 if name != "FP8" else FusedKVPrecision.FP16)
+    return int(tag)
+
+
 def metadata_to_kernel_tensors(meta: Dict, num_pages: int, B: int = 1, H: int = 1,
                                config: Optional[FusedDecodeConfig] = None,
                                device: Optional[torch.device] = None, *,
@@ -101,11 +114,7 @@ def metadata_to_kernel_tensors(meta: Dict, num_pages: int, B: int = 1, H: int = 
             pid = int(key)
         except ValueError:
             continue
-        tag = _NAME_TO_TAG.get(name, FusedKVPrecision.FP16)
-        if name in _NATIVE_NAME_TO_TAG:
-            tag = _NATIVE_NAME_TO_TAG[name] if native_precisions else (
-                FusedKVPrecision.INT8 if name != "FP8" else FusedKVPrecision.FP16)
-        prec[pid] = int(tag)
+        prec[pid] = precision_tag(name, native_precisions)
     ids = np.asarray(meta.get("selected_page_ids", []), dtype=np.int64)[:width].astype(np.int32)
     table = np.zeros((B, H, width), dtype=np.int32)
     table[:, :, : ids.size] = ids

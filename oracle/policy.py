@@ -438,3 +438,98 @@ def make_precision_tensor(num_pages: int, fp16_pages=None, int8_pages=None):
     if int8_pages is not None:
         prec[np.asarray(int8_pages, dtype=np.int64)] = TRITON_TAG["INT8"]
     return prec
+
+
+# --------------------------------------------------------------------------- #
+# Page tables from routed spans: routing_to_kernel_metadata followed by
+# metadata_to_kernel_tensors, generalised to one span list per group of rows,
+# a logical -> physical block table and residency. Test infrastructure: the
+# product computes this on the GPU (iak_build_page_tables).
+# --------------------------------------------------------------------------- #
+
+def reference_tag(name: str, native_precisions: bool = False) -> int:
+    """The precision string -> fused tag mapping of metadata_to_kernel_tensors
+    (fused_selected_quant_decode.py:379-389; native tags as above)."""
+    if name == "SKIP":
+        return 2
+    if name == "INT8":
+        return 1
+    if name in ("INT4", "INT4_RESIDUAL"):
+        return (4 if name == "INT4" else 5) if native_precisions else 1
+    if name == "FP8" and native_precisions:
+        return 3
+    return 0
+
+
+def routed_spans(routed: List[RoutedBlock], native_precisions: bool = False) -> List[Tuple[int, int, int]]:
+    """(start, end, tag) of the selected blocks in routed order (the blocks
+    whose tokens routing_to_kernel_metadata pages, block_router.py:400-410)."""
+    return [(b.start, b.end, reference_tag(b.precision, native_precisions))
+            for b in BlockRouter.selected_blocks(routed)]
+
+
+def build_page_tables_oracle(lists, num_rows: int, table_width: int, page_size: int, num_pages: int, *,
+                             rows_per_seq: int = 1, rows_per_list: Optional[int] = None, block_table=None,
+                             dedupe: bool = True, default_tag: int = 0):
+    """Loops over rows, spans and tokens; numpy int32 (page_table [R, W],
+    page_precision [num_pages], page_counts [R]).
+
+    ``lists[l]`` is a list of ``(start, end, tag)`` spans in routed order. Row
+    ``r`` reads list ``r // rows_per_list`` (default: one list for every row,
+    the reference's broadcast) and block-table row ``r // rows_per_seq``.
+    Per row:
+      * logical pages ``t // page_size`` of tokens ``start <= t < end``, span by
+        span, first seen only (block_router.py:283-296, :405-410); with
+        ``dedupe=False`` every page of every span, in order;
+      * physical id ``block_table[seq][l]`` (``l`` outside the row or a negative
+        entry: not resident, dropped), or ``l`` without a block table; ids
+        outside ``[0, num_pages)`` are dropped;
+      * ``page_table[r, :n]`` = the first ``min(n, W)`` ids, zeros after, and
+        ``page_counts[r] = min(n, W)`` (fused_selected_quant_decode.py:394-400);
+      * ``page_precision[q]`` = the tag of the span that emitted ``q``, taken
+        from the lowest row that emits ``q`` (the smallest tag if that row
+        emits ``q`` twice); pages no row emits keep ``default_tag``. Every page
+        a row emits counts, also those past ``W`` (the reference tags every key
+        of block_precision_by_page).
+    """
+    rpl = num_rows if rows_per_list is None else rows_per_list
+    table = np.zeros((num_rows, table_width), dtype=np.int32)
+    counts = np.zeros((num_rows,), dtype=np.int32)
+    prec = np.full((num_pages,), default_tag, dtype=np.int32)
+    owner_row = {}
+    memo = {}
+    for r in range(num_rows):
+        key = (r // max(rpl, 1), r // rows_per_seq)
+        if key in memo:                       # rows sharing list and block-table row
+            ids, tags = memo[key]
+            n = min(len(ids), table_width)
+            table[r, :n] = ids[:n]
+            counts[r] = n
+            continue
+        spans = lists[key[0]]
+        seq = key[1]
+        ids, tags, seen = [], [], set()
+        for start, end, tag in spans:
+            for t in range(start, end):
+                lp = t // page_size
+                if dedupe:
+                    if lp in seen:
+                        continue
+                    seen.add(lp)
+                if block_table is not None:
+                    row = block_table[seq]
+                    q = int(row[lp]) if 0 <= lp < len(row) else -1
+                else:
+                    q = lp
+                if 0 <= q < num_pages and (dedupe or t == start or (t - 1) // page_size != lp):
+                    ids.append(q)
+                    tags.append(tag)
+        memo[key] = (ids, tags)
+        n = min(len(ids), table_width)
+        table[r, :n] = ids[:n]
+        counts[r] = n
+        for q, tag in zip(ids, tags):
+            if q not in owner_row or owner_row[q][0] == r and tag < prec[q]:
+                owner_row[q] = (r, tag)
+                prec[q] = tag
+    return table, prec, counts

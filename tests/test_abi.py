@@ -33,7 +33,8 @@ def test_library_exports_every_declared_symbol():
 
 @pytest.mark.parametrize("cname,pyname", [("iak_paged_decode_args", "PagedDecodeArgs"),
                                           ("iak_mla_decode_args", "MlaDecodeArgs"),
-                                          ("iak_quantize_args", "QuantizeArgs")])
+                                          ("iak_quantize_args", "QuantizeArgs"),
+                                          ("iak_page_table_args", "PageTableArgs")])
 def test_ctypes_struct_matches_c_layout(cname, pyname):
     from intent_attention import _native as N
     S = getattr(N, pyname)
@@ -127,3 +128,29 @@ def test_quantize_validation_errors_without_gpu():
     a.int4_group, a.scale_dtype = 32, N.DTYPE_F16
     with pytest.raises(ValueError, match="NULL"):
         N.quantize_pages(a, 0)
+
+
+def test_page_table_validation_errors_without_gpu():
+    from intent_attention import _native as N
+    a = N.PageTableArgs()
+    a.num_rows, a.rows_per_seq, a.rows_per_list, a.table_width, a.page_size, a.num_pages = 4, 0, 4, 8, 16, 10
+    with pytest.raises(ValueError, match="rows_per_seq"):
+        N.build_page_tables(a, 0)
+    a.rows_per_seq, a.page_size = 2, 0
+    with pytest.raises(ValueError, match="page_size"):
+        N.build_page_tables(a, 0)
+    a.page_size, a.default_tag = 16, 7
+    with pytest.raises(ValueError, match="default_tag"):
+        N.build_page_tables(a, 0)
+    a.default_tag, a.block_table = 0, 16
+    with pytest.raises(ValueError, match="block_table_width"):
+        N.build_page_tables(a, 0)
+    a.block_table_width = 4
+    with pytest.raises(ValueError, match="span arrays"):
+        N.build_page_tables(a, 0)
+    a.span_offsets = a.span_begin = a.span_end = a.span_tag = 16
+    with pytest.raises(ValueError, match="page_table / page_counts"):
+        N.build_page_tables(a, 0)
+    a.num_rows, a.page_precision = 1 << 28, 16
+    with pytest.raises(ValueError, match="2\\^28"):
+        N.build_page_tables(a, 0)

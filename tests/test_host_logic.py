@@ -150,3 +150,39 @@ def test_decode_entry_points_refuse_host_tensors():
             ia.intent_quant_decode_attention_triton(
                 x[:, :, 0], p, p, i8, i8, s, s, torch.zeros(1, 1, 64, dtype=torch.int32),
                 torch.ones(1, 1, dtype=torch.int32), torch.zeros(2, dtype=torch.int32))
+
+
+def test_routed_spans_for_the_device_builder(g2):
+    """The span arrays routing_to_kernel_tensors uploads: the selected blocks in
+    routed order with the metadata_to_kernel_tensors tag of their precision
+    (KVPrecision members and names alike), equal to the oracle's spans."""
+    from intent_attention.page_tables import _spans
+    from intent_attention.fused_selected_quant_decode import precision_tag
+    from oracle import policy as P
+    for name in ("FP16", "FP8", "INT8", "INT4", "INT4_RESIDUAL", "SKIP"):
+        for native in (False, True):
+            assert precision_tag(ia.KVPrecision(name), native) == precision_tag(name, native) == \
+                P.reference_tag(name, native)
+    for rec in g2:
+        router = ia.BlockRouter(ia.RouterConfig(**rec["config"]))
+        routed = router.route_layout(_product_layout(rec["blocks"]), rec["total_tokens"])
+        o_router = P.BlockRouter(P.RouterConfig(**rec["config"]))
+        o_routed = o_router.route_layout(P.BlockLayout([P.SemanticBlock(*b) for b in rec["blocks"]]),
+                                         rec["total_tokens"])
+        for native in (False, True):
+            b, e, t = _spans(routed, native)
+            assert list(zip(b, e, t)) == P.routed_spans(o_routed, native)
+
+
+def test_empty_span_has_no_pages():
+    """block_router.py:291-295 walks the tokens: a block with end <= start
+    selects no page, also when its start is not page-aligned."""
+    blocks = [ia.RoutedBlock("a", 17, 17, ia.BlockPolicy.ALWAYS, None, ia.BlockDecision.SELECT,
+                             ia.KVPrecision.FP16, ""),
+              ia.RoutedBlock("b", 40, 20, ia.BlockPolicy.ALWAYS, None, ia.BlockDecision.SELECT,
+                             ia.KVPrecision.INT8, ""),
+              ia.RoutedBlock("c", 33, 34, ia.BlockPolicy.ALWAYS, None, ia.BlockDecision.SELECT,
+                             ia.KVPrecision.INT8, "")]
+    meta = ia.routing_to_kernel_metadata(blocks, 16)
+    assert meta["selected_page_ids"] == [2]
+    assert meta["block_precision_by_page"] == {"2": "INT8"}

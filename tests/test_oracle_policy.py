@@ -131,3 +131,117 @@ def test_page_table_helpers_reference_facts():
     prec = P.make_precision_tensor(10, fp16_pages=[0, 1, 2], int8_pages=[3, 4])
     assert prec.tolist() == [0, 0, 0] + [2] * 7
     assert P.TRITON_TAG == {"FP16": 0, "FP8": 1, "INT8": 2, "INT4": 3, "INT4_RESIDUAL": 4, "SKIP": 5}
+
+
+# --------------------------------------------------------------------------- #
+# build_page_tables_oracle: the device page-table builder's semantics
+# --------------------------------------------------------------------------- #
+
+def _g2_routed(rec):
+    router = P.BlockRouter(P.RouterConfig(**rec["config"]))
+    return router.route_layout(_layout(rec["blocks"]), rec["total_tokens"])
+
+
+def test_page_table_oracle_matches_reference_golden(g2):
+    """One list broadcast to B*H rows, identity pages: the reference's kernel
+    tensors of every G2 record, in both precision mappings."""
+    for rec in g2:
+        routed = _g2_routed(rec)
+        ps = rec["page_size"]
+        num_pages = (rec["total_tokens"] + ps - 1) // ps
+        pt, prec, pc = P.build_page_tables_oracle([P.routed_spans(routed)], 6, 40, ps, num_pages)
+        assert pt.reshape(2, 3, 40).tolist() == rec["kernel"]["page_table"]
+        assert prec.tolist() == rec["kernel"]["page_precision"]
+        assert pc.reshape(2, 3).tolist() == rec["kernel"]["page_counts"]
+        meta = P.routing_to_kernel_metadata(routed, ps)
+        _, prec_n, _ = P.metadata_to_kernel_tensors(meta, num_pages, native_precisions=True)
+        _, prec_o, _ = P.build_page_tables_oracle([P.routed_spans(routed, True)], 1, 40, ps, num_pages)
+        assert prec_o.tolist() == prec_n.tolist()
+
+
+def test_page_table_oracle_detects_plausible_mistakes(g2):
+    """The golden check above fails for a builder that forgets the
+    first-seen dedupe or pages the end token of each span."""
+    no_dedupe = off_by_one = 0
+    for rec in g2:
+        routed = _g2_routed(rec)
+        ps = rec["page_size"]
+        num_pages = (rec["total_tokens"] + ps - 1) // ps + 1
+        spans = P.routed_spans(routed)
+        want = rec["kernel"]["page_table"]
+        pt, _, _ = P.build_page_tables_oracle([spans], 6, 40, ps, num_pages, dedupe=False)
+        no_dedupe += pt.reshape(2, 3, 40).tolist() != want
+        pt, _, _ = P.build_page_tables_oracle([[(s, e + 1, t) for s, e, t in spans]], 6, 40, ps, num_pages)
+        off_by_one += pt.reshape(2, 3, 40).tolist() != want
+    assert no_dedupe > 10 and off_by_one > 10
+
+
+def _random_routing(rng, n_blocks=25, max_len=300):
+    pols = ["ALWAYS", "ATTEND", "ATTEND", "SKIP", "RECENT", "GLOBAL"]
+    blocks, t = [], 0
+    for i in range(int(rng.integers(1, n_blocks))):
+        ln = int(rng.integers(1, max_len))
+        pol = pols[int(rng.integers(0, len(pols)))]
+        sc = float(np.round(rng.random(), 1)) if (pol == "ATTEND" or rng.random() < .4) else None
+        blocks.append(P.SemanticBlock(f"b{i}", t, t + ln, pol, sc))
+        t += ln + int(rng.integers(0, 40))
+    cfg = P.RouterConfig(top_k_blocks=int(rng.integers(0, 12)), score_threshold=float(rng.random()),
+                         memory_pressure=float(np.round(rng.random(), 2)))
+    return P.BlockRouter(cfg).route_layout(P.BlockLayout(blocks), t), t
+
+
+def test_page_table_oracle_matches_reference_composition_on_random_layouts():
+    """metadata_to_kernel_tensors(routing_to_kernel_metadata(...)) on random
+    layouts, page sizes and widths (truncation included)."""
+    rng = np.random.default_rng(7)
+    for trial in range(80):
+        routed, total = _random_routing(rng)
+        ps = int(rng.choice([1, 3, 16, 64]))
+        W = int(rng.integers(1, 80))
+        num_pages = (total + ps - 1) // ps + int(rng.integers(0, 3))
+        meta = P.routing_to_kernel_metadata(routed, ps)
+        native = bool(trial % 2)
+        pt_r, prec_r, pc_r = P.metadata_to_kernel_tensors(meta, num_pages, B=2, H=2, max_selected=W,
+                                                          native_precisions=native)
+        pt, prec, pc = P.build_page_tables_oracle([P.routed_spans(routed, native)], 4, W, ps, num_pages)
+        assert pt.reshape(2, 2, W).tolist() == pt_r.tolist()
+        assert prec.tolist() == prec_r.tolist()
+        assert pc.reshape(2, 2).tolist() == pc_r.tolist()
+
+
+def test_page_table_oracle_block_table_invariants():
+    """Identity block table == no block table; a permutation maps every id;
+    non-resident entries drop out and the rest keep their order."""
+    rng = np.random.default_rng(8)
+    for trial in range(30):
+        lists, totals = [], []
+        for b in range(3):
+            routed, total = _random_routing(rng)
+            lists.append(P.routed_spans(routed, True))
+            totals.append(total)
+        ps = 16
+        L = max((t + ps - 1) // ps for t in totals)
+        W = int(rng.integers(4, 60))
+        R, H = 6, 2
+        base = P.build_page_tables_oracle(lists, R, W, ps, L, rows_per_seq=H, rows_per_list=H)
+        ident = np.tile(np.arange(L, dtype=np.int32), (3, 1))
+        got = P.build_page_tables_oracle(lists, R, W, ps, L, rows_per_seq=H, rows_per_list=H, block_table=ident)
+        for x, y in zip(base, got):
+            assert np.array_equal(x, y)
+        # per-sequence permutations into a pool of 3 * L pages
+        perm = np.stack([rng.permutation(L).astype(np.int32) + s * L for s in range(3)])
+        pt, prec, pc = P.build_page_tables_oracle(lists, R, W, ps, 3 * L, rows_per_seq=H, rows_per_list=H,
+                                                  block_table=perm)
+        assert np.array_equal(pc, base[2])
+        for r in range(R):
+            n = pc[r]
+            assert np.array_equal(pt[r, :n], perm[r // H][base[0][r, :n]])
+        # holes: entries set to -1 vanish, order kept, precision of dropped pages untouched
+        holes = ident.copy()
+        holes[rng.random(holes.shape) < 0.3] = -1
+        pt_h, _, pc_h = P.build_page_tables_oracle(lists, R, 4096, ps, L, rows_per_seq=H, rows_per_list=H,
+                                                   block_table=holes)
+        full, _, pcf = P.build_page_tables_oracle(lists, R, 4096, ps, L, rows_per_seq=H, rows_per_list=H)
+        for r in range(R):
+            keep = [p for p in full[r, :pcf[r]] if holes[r // H][p] >= 0]
+            assert pt_h[r, :pc_h[r]].tolist() == keep
