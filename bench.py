@@ -410,13 +410,270 @@ def run_mla(args) -> None:
 
 
 # --------------------------------------------------------------------------- #
+# Quantise-on-write (cfg3-quantize): every quantised page of the cfg3 pools
+# --------------------------------------------------------------------------- #
+
+QUANT_CONFIGS = {
+    # the cfg3 pools: 32 x 8 x 4096 pages per K and V, 25 % FP16 (stored as is),
+    # 25 % FP8, 30 % INT8, 20 % INT4 (groups of 32 channels); fresh float16 pages
+    # with 1 % of K elements at 8 sigma, quantised into their pool slots
+    "cfg3-quantize": dict(pages=32 * 8 * 4096, D=128, mix={TAG_FP8: .25, TAG_INT8: .30, TAG_INT4: .20},
+                          outliers=0.01),
+}
+QUANT_OUT_BYTES = {TAG_FP8: (PS * 128, 2), TAG_INT8: (PS * 128, 2), TAG_INT4: (PS * 64, 4 * 2)}
+
+
+def build_quantize_workload(name: str, device: torch.device, seed: int = 99):
+    cfg = QUANT_CONFIGS[name]
+    NP, D = cfg["pages"], cfg["D"]
+    g = torch.Generator(device=device).manual_seed(seed)
+    gc = torch.Generator().manual_seed(seed)
+    jobs = []
+    for w in ("k", "v"):
+        slots = torch.randperm(NP, generator=gc)
+        lo = 0
+        for tag, frac in cfg["mix"].items():
+            n = int(frac * NP)
+            dst = slots[lo:lo + n].to(torch.int32).to(device)
+            lo += n
+            src = torch.randn((n, PS, D), generator=g, device=device, dtype=torch.float32)
+            if w == "k" and cfg["outliers"] > 0:
+                m = torch.rand(src.shape, generator=g, device=device) < cfg["outliers"]
+                src = torch.where(m, 8.0 * torch.sign(src), src)
+            src = src.half()
+            width = D // 2 if tag == TAG_INT4 else D
+            codes = torch.zeros((NP, PS, width), dtype=torch.uint8, device=device)
+            scales = torch.zeros((NP, D // 32) if tag == TAG_INT4 else (NP,), dtype=torch.float16, device=device)
+            jobs.append(dict(w=w, tag=tag, src=src, dst=dst, codes=codes, scales=scales))
+    return dict(cfg=cfg, name=name, jobs=jobs)
+
+
+def quantize_step_bytes(wl) -> int:
+    total = 0
+    for j in wl["jobs"]:
+        n = j["src"].shape[0]
+        cb, sb = QUANT_OUT_BYTES[j["tag"]]
+        total += n * (PS * wl["cfg"]["D"] * 2 + 4 + cb + sb)     # f16 page in, slot id, codes + scales out
+    return total
+
+
+def quantize_cpu_baseline(wl, budget_s: float = 12.0) -> dict:
+    from oracle import quant as Q
+    names = {TAG_FP8: "FP8", TAG_INT8: "INT8", TAG_INT4: "INT4"}
+    host = [(j["tag"], j["src"][:512].cpu().numpy()) for j in wl["jobs"]]
+    done_pages, done_bytes, t0 = 0, 0, time.perf_counter()
+    i = 0
+    while time.perf_counter() - t0 < budget_s and i < 512:
+        for tag, x in host:                     # round robin over the K/V x precision jobs
+            cb, sb = QUANT_OUT_BYTES[tag]
+            Q.quantize_page(x[i], names[tag], 32)
+            done_pages += 1
+            done_bytes += PS * wl["cfg"]["D"] * 2 + 4 + cb + sb
+        i += 1
+    dt = time.perf_counter() - t0
+    rate = done_bytes / dt
+    return {"value": round(rate / 1e9, 4), "unit": "GB/s", "us_per_step": round(quantize_step_bytes(wl) / rate * 1e6),
+            "cores": 1, "kind": "port",
+            "sample": f"oracle.quant.quantize_page (numpy, 1 thread) on {done_pages} pages (round robin over the "
+                      f"6 K/V x precision jobs), {dt:.1f} s, scaled to the full step"}
+
+
+def run_quantize(args) -> None:
+    from intent_attention import _native as N
+    dev = torch.device("cuda:0")
+    t_build = time.perf_counter()
+    wl = build_quantize_workload(args.config, dev)
+    torch.cuda.synchronize()
+    print(f"[bench] built {args.config} in {time.perf_counter() - t_build:.1f}s", file=sys.stderr, flush=True)
+    stream = torch.cuda.current_stream(dev)
+    argv = []
+    for j in wl["jobs"]:
+        a = N.QuantizeArgs()
+        a.num_pages, a.page_size, a.head_dim = j["src"].shape[0], PS, wl["cfg"]["D"]
+        a.src, a.dst_pages, a.pool_pages = j["src"].data_ptr(), j["dst"].data_ptr(), j["codes"].shape[0]
+        a.precision, a.mode, a.int4_group = j["tag"], N.QUANT_FAKE_QUANTIZE, 32
+        a.codes, a.scales, a.scale_dtype = j["codes"].data_ptr(), j["scales"].data_ptr(), N.DTYPE_F16
+        argv.append(a)
+
+    def step():
+        for a in argv:
+            N.quantize_pages(a, stream.cuda_stream)
+
+    res = _time_steps(step, args, stream)
+    ab = quantize_step_bytes(wl)
+    ms = res["ms"]
+    gbps = ab / (ms * 1e-3) / 1e9
+    out = {"metric": "quantise-on-write GB/s (cfg3 pools: FP8 / INT8 / INT4 pages from float16)",
+           "value": round(gbps, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": round(ms, 5), "us_per_step": round(ms * 1e3, 2),
+           "us_per_step_p10_p50_p90": res["spread"], "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "f16->u8",
+           "data": "synthetic (seeded float16 N(0,1) pages, 1 % of K at 8 sigma)",
+           "config": {"workload": f"{args.config}: {sum(j['src'].shape[0] for j in wl['jobs'])} pages of 16x128 "
+                                  f"quantised into 1,048,576-slot K and V pools (6 launches per step)",
+                      "algorithmic_bytes": ab},
+           "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                        "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None}}
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = quantize_cpu_baseline(wl)
+    print(json.dumps(out), flush=True)
+
+
+# --------------------------------------------------------------------------- #
+# Page tables from routing (cfg3-tables): iak_build_page_tables at cfg3 shape
+# --------------------------------------------------------------------------- #
+
+TABLE_CONFIGS = {
+    # 32 sequences x 8 KV heads, 65,536 tokens (4096 pages) each; per sequence a
+    # routing of blocks of 16..1024 tokens, 40 % of the tokens selected, in a
+    # shuffled (routed) order with random page precisions; each (sequence, KV
+    # head) row maps its logical pages through its own block-table row into a
+    # 1,048,576-page pool; width 1639, precision over every pool page
+    "cfg3-tables": dict(B=32, Hkv=8, T=65536, sel=0.40, block=(16, 1024), W=1639),
+}
+
+
+def build_table_workload(name: str, device: torch.device, seed: int = 7):
+    cfg = TABLE_CONFIGS[name]
+    B, Hkv, T = cfg["B"], cfg["Hkv"], cfg["T"]
+    P = T // PS
+    rng = np.random.default_rng(seed)
+    lists = []
+    for b in range(B):
+        cuts, t = [], 0
+        while t < T:
+            ln = int(rng.integers(cfg["block"][0], cfg["block"][1] + 1))
+            cuts.append((t, min(T, t + ln)))
+            t += ln
+        order = rng.permutation(len(cuts))
+        spans, got = [], 0
+        for i in order:
+            if got >= cfg["sel"] * T:
+                break
+            s, e = cuts[i]
+            spans.append((s, e, int(rng.choice([TAG_FP16, TAG_FP8, TAG_INT8, TAG_INT4], p=[.25, .25, .30, .20]))))
+            got += e - s
+        lists.append(spans)
+    NP = B * Hkv * P
+    bt = torch.from_numpy(rng.permutation(NP).astype(np.int32).reshape(B * Hkv, P)).to(device)
+    offs, beg, end, tag = [0], [], [], []
+    for spans in lists:
+        for s, e, t in spans:
+            beg.append(s)
+            end.append(e)
+            tag.append(t)
+        offs.append(len(beg))
+    dev_i32 = lambda x: torch.tensor(x, dtype=torch.int32, device=device)  # noqa: E731
+    return dict(cfg=cfg, name=name, lists=lists, NP=NP, P=P, block_table=bt, offs=dev_i32(offs),
+                begin=dev_i32(beg), end=dev_i32(end), tag=dev_i32(tag))
+
+
+def table_step_bytes(wl, pairs: int) -> int:
+    cfg = wl["cfg"]
+    R = cfg["B"] * cfg["Hkv"]
+    spans = wl["begin"].numel()
+    return (spans * 12 * cfg["Hkv"] + wl["offs"].numel() * 4      # span lists, read by each of their rows
+            + pairs * 4                                          # block-table entries of the named pages
+            + R * cfg["W"] * 4 + R * 4 + wl["NP"] * 4)          # page table, counts, precision out
+
+
+def run_tables(args) -> None:
+    from intent_attention import _native as N
+    from oracle import policy as Pol
+    dev = torch.device("cuda:0")
+    wl = build_table_workload(args.config, dev)
+    cfg = wl["cfg"]
+    R = cfg["B"] * cfg["Hkv"]
+    table = torch.empty((R, cfg["W"]), dtype=torch.int32, device=dev)
+    counts = torch.empty(R, dtype=torch.int32, device=dev)
+    prec = torch.empty(wl["NP"], dtype=torch.int32, device=dev)
+    a = N.PageTableArgs()
+    a.num_rows, a.rows_per_seq, a.rows_per_list = R, 1, cfg["Hkv"]
+    a.table_width, a.page_size, a.num_pages, a.dedupe, a.default_tag = cfg["W"], PS, wl["NP"], 1, TAG_FP16
+    a.block_table_width = wl["P"]
+    a.span_offsets, a.span_begin, a.span_end, a.span_tag = (t.data_ptr() for t in
+                                                            (wl["offs"], wl["begin"], wl["end"], wl["tag"]))
+    a.block_table, a.page_table, a.page_counts, a.page_precision = (wl["block_table"].data_ptr(), table.data_ptr(),
+                                                                    counts.data_ptr(), prec.data_ptr())
+    stream = torch.cuda.current_stream(dev)
+    # one step = the three launches (fill, build, tags); replayed as a HIP graph so
+    # the host's launch rate does not set the step time
+    N.build_page_tables(a, stream.cuda_stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        N.build_page_tables(a, torch.cuda.current_stream(dev).cuda_stream)
+    torch.cuda.synchronize()
+    res = _time_steps(graph.replay, args, stream)
+    # every replay must give the CPU restatement's tables (checked on 16 rows)
+    rows = list(range(0, R, R // 16))
+    want = Pol.build_page_tables_oracle(wl["lists"], R, cfg["W"], PS, wl["NP"], rows_per_seq=1,
+                                        rows_per_list=cfg["Hkv"], block_table=wl["block_table"].cpu().numpy())
+    got_t, got_c = table.cpu().numpy(), counts.cpu().numpy()
+    if not (np.array_equal(got_t[rows], want[0][rows]) and np.array_equal(got_c, want[2])
+            and np.array_equal(prec.cpu().numpy(), want[1])):
+        raise SystemExit("page tables differ from the CPU restatement")
+    pairs = int(sum(min(wl["P"] - 1, (e - 1) // PS) - s // PS + 1 for spans in wl["lists"] for s, e, _ in spans))
+    ab = table_step_bytes(wl, pairs * cfg["Hkv"])
+    ms = res["ms"]
+    gbps = ab / (ms * 1e-3) / 1e9
+    out = {"metric": "page-table build µs/step (routing -> page_table / precision / counts, cfg3 shape)",
+           "value": round(ms * 1e3, 2), "unit": "us", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": round(ms, 5), "us_per_step_p10_p50_p90": res["spread"], "higher_is_better": False,
+           "scaling": "weak", "vs_baseline": None, "dtype": "int32",
+           "data": "synthetic (seeded block routings and block tables)",
+           "config": {"workload": f"{args.config}: {R} rows (32 sequences x 8 KV heads), "
+                                  f"{wl['begin'].numel()} routed blocks, {pairs} selected pages per KV head "
+                                  f"summed over sequences, width {cfg['W']}, {wl['NP']}-page precision array",
+                      "algorithmic_bytes": ab},
+           "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                        "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None}}
+    if not args.no_cpu_baseline:
+        bt_host = wl["block_table"].cpu().numpy()
+        reps, t0 = 0, time.perf_counter()
+        while reps < 3 or time.perf_counter() - t0 < 10.0:
+            Pol.build_page_tables_oracle(wl["lists"], R, cfg["W"], PS, wl["NP"], rows_per_seq=1,
+                                         rows_per_list=cfg["Hkv"], block_table=bt_host)
+            reps += 1
+        dt = time.perf_counter() - t0
+        out["cpu_baseline"] = {"value": round(dt / reps * 1e6, 1), "unit": "us", "cores": 1, "kind": "port",
+                               "sample": f"oracle.policy.build_page_tables_oracle (Python loops as the reference's "
+                                         f"routing_to_kernel_metadata + metadata_to_kernel_tensors, 1 thread), the "
+                                         f"full step {reps} times in {dt:.1f} s"}
+    print(json.dumps(out), flush=True)
+
+
+def _time_steps(step, args, stream) -> dict:
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(args.steps):
+        step()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / args.steps
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    for s, e in ev:
+        s.record(stream)
+        step()
+        e.record(stream)
+    torch.cuda.synchronize()
+    per = sorted(s.elapsed_time(e) for s, e in ev)
+    return {"ms": ms, "spread": [round(per[len(per) // 10] * 1e3, 2), round(per[len(per) // 2] * 1e3, 2),
+                                 round(per[(9 * len(per)) // 10] * 1e3, 2)]}
+
+
+# --------------------------------------------------------------------------- #
 
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS) + sorted(MLA_CONFIGS))
+    ap.add_argument("--config", default="cfg3",
+                    choices=sorted(CONFIGS) + sorted(MLA_CONFIGS) + sorted(QUANT_CONFIGS) + sorted(TABLE_CONFIGS))
     ap.add_argument("--pages-per-split", type=int, default=0)
     ap.add_argument("--cpu-rows", type=int, default=192, help="rows of the step the CPU baseline times")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -432,6 +689,12 @@ def main() -> None:
 
     if args.config in MLA_CONFIGS:
         run_mla(args)
+        return
+    if args.config in QUANT_CONFIGS:
+        run_quantize(args)
+        return
+    if args.config in TABLE_CONFIGS:
+        run_tables(args)
         return
     from intent_attention.decode_core import make_plan
     dev = torch.device("cuda:0")

@@ -9,9 +9,11 @@
 // of each span's page interval [start / ps, (end - 1) / ps]; call the k-th page
 // of that concatenation "pair k". Pair k is emitted when its page is seen for
 // the first time (the lowest span covering it is its own span) and resident;
-// its output position is the number of emitted pairs before it, one
-// exclusive scan over k. Spans are taken 256 at a time (a scan of their page
-// counts places each pair), and the first-seen test reads an LDS map
+// its output position is the number of emitted pairs before it: each thread
+// takes PT_PER consecutive pairs (their block-table loads in flight together)
+// and one exclusive scan over the threads' counts places them. Spans are
+// taken 256 at a time (a scan of their page counts locates each pair), and
+// the first-seen test reads an LDS map
 // page -> lowest covering span, built with LDS atomicMin over the same pairs
 // before they are emitted: a later chunk's spans have larger indices, so the
 // map is final for every page of the current chunk. A list whose pages span
@@ -36,6 +38,7 @@ namespace iak {
 
 constexpr int PT_THREADS = 256;
 constexpr int PT_OWNER = 16384;   // page ids one list may span for the LDS first-seen map (64 KB)
+constexpr int PT_PER = 8;         // consecutive pairs per thread in the emit pass
 
 __device__ __forceinline__ int64_t floor_div(int64_t x, int64_t d) {
   return x >= 0 ? x / d : -((-x + d - 1) / d);
@@ -86,6 +89,7 @@ __global__ __launch_bounds__(PT_THREADS) void page_tables_kernel(const iak_page_
   __shared__ uint32_t owner[PT_OWNER];
   __shared__ int64_t pre[PT_THREADS];     // exclusive page-count prefix of the chunk's spans
   __shared__ int64_t first[PT_THREADS];   // first (clamped) page of each span of the chunk
+  __shared__ int32_t tags[PT_THREADS];    // tag of each span of the chunk
   __shared__ int64_t wsum[PT_THREADS / 64];
   __shared__ int64_t rmin[PT_THREADS / 64], rmax[PT_THREADS / 64];
 
@@ -139,15 +143,18 @@ __global__ __launch_bounds__(PT_THREADS) void page_tables_kernel(const iak_page_
   for (int64_t c0 = 0; c0 < S; c0 += PT_THREADS) {
     const int cn = S - c0 < PT_THREADS ? (int)(S - c0) : PT_THREADS;
     int64_t n = 0, lo = 0;
+    int tg = 0;
     if (tid < cn) {
       const SpanPages p = span_pages(a, s0 + c0 + tid, bound);
       lo = p.lo;
       n = p.hi >= p.lo ? p.hi - p.lo + 1 : 0;
+      tg = a.span_tag[s0 + c0 + tid] & 7;
     }
     int64_t tot;
     const int64_t ex = block_scan(n, tot, wsum);
     pre[tid] = ex;
     first[tid] = lo;
+    tags[tid] = tg;
     __syncthreads();
 
     // span of pair k: the largest j < cn with pre[j] <= k (never an empty span for k < tot)
@@ -158,48 +165,70 @@ __global__ __launch_bounds__(PT_THREADS) void page_tables_kernel(const iak_page_
         if (j + step < cn && pre[j + step] <= k) j += step;
       return j;
     };
+    auto advance = [&](int j, int64_t k) {
+      while (j + 1 < cn && pre[j + 1] <= k) ++j;
+      return j;
+    };
 
+    // pairs in batches of PT_THREADS * PT_PER; thread t takes PT_PER consecutive pairs
     if (use_map) {
-      for (int64_t k = tid; k < tot; k += PT_THREADS) {
-        const int j = locate(k);
-        const int64_t pg = first[j] + (k - pre[j]);
-        atomicMin(&owner[pg - amin], (uint32_t)(c0 + j));
+      for (int64_t k0 = (int64_t)tid * PT_PER; k0 < tot; k0 += (int64_t)PT_THREADS * PT_PER) {
+        int j = locate(k0);
+        for (int u = 0; u < PT_PER && k0 + u < tot; ++u) {
+          j = advance(j, k0 + u);
+          atomicMin(&owner[first[j] + (k0 + u - pre[j]) - amin], (uint32_t)(c0 + j));
+        }
       }
       __syncthreads();
     }
 
-    for (int64_t k0 = 0; k0 < tot; k0 += PT_THREADS) {
-      const int64_t k = k0 + tid;
-      int64_t emit = 0;
-      int32_t phys = 0, tag = 0;
-      if (k < tot) {
-        const int j = locate(k);
-        const int64_t i = c0 + j;
-        const int64_t pg = first[j] + (k - pre[j]);
-        bool fresh = true;
-        if (a.dedupe) {
-          if (use_map) {
-            fresh = owner[pg - amin] == (uint32_t)i;
-          } else {
-            for (int64_t e = 0; e < i && fresh; ++e) {
-              const SpanPages p = span_pages(a, s0 + e, bound);
-              fresh = !(p.lo <= pg && pg <= p.hi);
+    for (int64_t b0 = 0; b0 < tot; b0 += (int64_t)PT_THREADS * PT_PER) {
+      const int64_t k0 = b0 + (int64_t)tid * PT_PER;
+      int32_t phys[PT_PER];
+      int8_t fresh[PT_PER], tagv[PT_PER];
+      int j = k0 < tot ? locate(k0) : 0;
+#pragma unroll
+      for (int u = 0; u < PT_PER; ++u) {      // independent loads, issued back to back
+        const int64_t k = k0 + u;
+        fresh[u] = 0;
+        phys[u] = -1;
+        tagv[u] = 0;
+        if (k < tot) {
+          j = advance(j, k);
+          const int64_t i = c0 + j;
+          const int64_t pg = first[j] + (k - pre[j]);
+          bool f = true;
+          if (a.dedupe) {
+            if (use_map) {
+              f = owner[pg - amin] == (uint32_t)i;
+            } else {
+              for (int64_t e = 0; e < i && f; ++e) {
+                const SpanPages p = span_pages(a, s0 + e, bound);
+                f = !(p.lo <= pg && pg <= p.hi);
+              }
             }
           }
+          fresh[u] = f;
+          phys[u] = bt ? bt[pg] : (int32_t)pg;
+          tagv[u] = (int8_t)tags[j];
         }
-        phys = bt ? bt[pg] : (int32_t)pg;
-        emit = fresh && phys >= 0 && phys < a.num_pages;
-        tag = a.span_tag[s0 + i] & 7;
       }
+      int64_t mine = 0;
+#pragma unroll
+      for (int u = 0; u < PT_PER; ++u) mine += (fresh[u] && phys[u] >= 0 && phys[u] < a.num_pages) ? 1 : 0;
       int64_t etot;
-      const int64_t pos = base + block_scan(emit, etot, wsum);
-      if (emit) {
-        if (pos < W) table[pos] = phys;
-        if (write_prec) atomicMin(&a.page_precision[phys], r * 8 + tag);
+      int64_t pos = base + block_scan(mine, etot, wsum);
+#pragma unroll
+      for (int u = 0; u < PT_PER; ++u) {
+        if (fresh[u] && phys[u] >= 0 && phys[u] < a.num_pages) {
+          if (pos < W) table[pos] = phys[u];
+          if (write_prec) atomicMin(&a.page_precision[phys[u]], r * 8 + tagv[u]);
+          ++pos;
+        }
       }
       base += etot;
     }
-    __syncthreads();   // pre / first are rewritten by the next chunk
+    __syncthreads();   // pre / first / tags are rewritten by the next chunk
   }
 
   const int64_t cnt = base < W ? base : W;

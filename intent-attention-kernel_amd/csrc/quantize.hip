@@ -18,10 +18,12 @@
 // A quotient 0/0 (an all-zero page) gives integer code 0 and e4m3fn code 0xFF,
 // as the reference does on the host.
 //
-// One wave per page: lane = 4 * token + j holds channels (D/4) j .. (D/4) j + D/4 - 1
-// of its token, so the page absmax is a wave reduction and a channel group of
-// INT4 is a reduction over the lanes of one j (and its neighbours when a group
-// spans more than D/4 channels).
+// One wave per page, loaded as whole 1 KB runs: load i of lane l is the 16
+// bytes at i * 1024 + 16 * l of the page, i.e. token i * TPL + l / LPT and
+// channels 8 * (l % LPT) .. + 7 (TPL tokens per run, LPT lanes per token).
+// The page absmax is a wave reduction; an INT4 channel group is a reduction
+// over the lanes of one group position across all tokens. Codes go out the same
+// way (8, or 4 for INT4, contiguous bytes per lane and token).
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -32,17 +34,44 @@
 
 namespace iak {
 
-__device__ __forceinline__ float wave_max(float v, int lo_bits) {
-  // over the lanes that differ in bits 2..5 (the token), then in the low bits
-  // 0 .. lo_bits-1 (neighbouring channel blocks of one group)
+// max over the lanes that differ from this one only in the bits of `mask`
+__device__ __forceinline__ float wave_max(float v, int mask) {
 #pragma unroll
-  for (int off = 4; off < 64; off <<= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  if (lo_bits > 0) v = fmaxf(v, __shfl_xor(v, 1, 64));
-  if (lo_bits > 1) v = fmaxf(v, __shfl_xor(v, 2, 64));
+  for (int off = 1; off < 64; off <<= 1)
+    if (mask & off) v = fmaxf(v, __shfl_xor(v, off, 64));
   return v;
 }
 
 __device__ __forceinline__ float f16r(float x) { return (float)(_Float16)x; }   // round to float16
+
+// x / s for a float16 numerator and a float16 scale s > 0, from r = 1 / s: the
+// product and one FMA correction. Its float16 rounding equals that of the IEEE
+// float32 quotient for every finite float16 x and positive finite float16 s
+// (checked exhaustively on the host, tests/native/f16_quotient_check.c);
+// e == 0 means q0 * s == x exactly, which keeps the sign of a zero quotient.
+__device__ __forceinline__ float div_by_scale(float x, float s, float r) {
+  const float q0 = __fmul_rn(x, r);
+  const float e = __builtin_fmaf(-q0, s, x);
+  return e == 0.f ? q0 : __builtin_fmaf(e, r, q0);
+}
+
+// the quotients of a lane's values by a float16 scale; s == 0 (an all-zero or
+// nearly zero page) keeps the IEEE division and its infinities and NaNs
+template <int NL>
+__device__ __forceinline__ void scale_quotients(const float (&x)[NL][8], float s, float (&q)[NL][8]) {
+  if (s > 0.f) {
+    const float r = 1.0f / s;
+#pragma unroll
+    for (int i = 0; i < NL; ++i)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) q[i][e] = div_by_scale(x[i][e], s, r);
+  } else {
+#pragma unroll
+    for (int i = 0; i < NL; ++i)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) q[i][e] = x[i][e] / s;
+  }
+}
 
 // float16 value -> e4m3fn code, round to nearest even; magnitudes that round
 // above 448 are NaN (0x7F | sign); NaN keeps its sign bit.
@@ -64,122 +93,152 @@ __device__ __forceinline__ uint32_t e4m3fn_rne(float v) {
   return sign | code;
 }
 
-template <int D>
+// KIND: the precision tag for IAK_QUANT_FAKE_QUANTIZE, or KIND_FUSED / KIND_TRITON
+constexpr int KIND_FUSED = 16, KIND_TRITON = 17;
+
+template <int D, int KIND>
 __global__ __launch_bounds__(256) void quantize_pages_kernel(const iak_quantize_args a) {
-  constexpr int PER = D / 4;                  // channels per lane
+  constexpr int NL = PS * D * 2 / 1024;       // 1 KB runs per page: 4 (D = 128) or 2 (D = 64)
+  constexpr int LPT = D / 8;                  // lanes per token: 16 or 8
+  constexpr int TPL = 64 / LPT;               // tokens per run: 4 or 8
   const int lane = threadIdx.x & 63;
   const int page = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (page >= a.num_pages) return;
   const int64_t dst = a.dst_pages ? (int64_t)a.dst_pages[page] : page;
   if (dst < 0 || dst >= a.pool_pages) return;
-  const int tok = lane >> 2, j = lane & 3;
+  const int c0 = 8 * (lane % LPT);            // first channel of this lane
+  const int t0 = lane / LPT;                  // token of run 0; run i holds token t0 + TPL * i
 
-  // this lane's PER channels of its token
-  const _Float16* src = reinterpret_cast<const _Float16*>(a.src) + ((int64_t)page * PS + tok) * D + PER * j;
-  float x[PER];
+  const _Float16* src = reinterpret_cast<const _Float16*>(a.src) + (int64_t)page * PS * D;
+  float x[NL][8];
 #pragma unroll
-  for (int i = 0; i < PER; i += 8) {
-    const h8 v = *reinterpret_cast<const h8*>(src + i);
+  for (int i = 0; i < NL; ++i) {
+    const h8 v = *reinterpret_cast<const h8*>(src + i * 512 + 8 * lane);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) x[i + e] = (float)v[e];
+    for (int e = 0; e < 8; ++e) x[i][e] = (float)v[e];
   }
   float am = 0.f;
 #pragma unroll
-  for (int i = 0; i < PER; ++i) am = fmaxf(am, fabsf(x[i]));
+  for (int i = 0; i < NL; ++i)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) am = fmaxf(am, fabsf(x[i][e]));
 
-  const int prec = a.precision;
   uint8_t* codes = reinterpret_cast<uint8_t*>(a.codes);
 
-  if (prec == IAK_TAG_INT4) {
-    // group scale of this lane's channels; lanes per group = group / PER
-    const int lpg = a.int4_group / PER;
-    const float gam = wave_max(am, lpg >= 4 ? 2 : (lpg >= 2 ? 1 : 0));
+  if constexpr (KIND == IAK_TAG_INT4) {
+    // group = the lanes of one token whose channels share the group, over all tokens
+    const int lpg = a.int4_group / 8;         // lanes per group within a token (>= LPT / 4 >= 2)
+    const float gam = wave_max(am, (63 & ~(LPT - 1)) | (lpg - 1));
     const float s = f16r(gam / 127.0f);
-    uint32_t packed[PER / 8];
+    float qs[NL][8];
+    scale_quotients(x, s, qs);
 #pragma unroll
-    for (int i = 0; i < PER / 8; ++i) packed[i] = 0;
+    for (int i = 0; i < NL; ++i) {
+      uint32_t packed = 0;
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const float q = f16r(x[i] / s);
-      const float r = (q != q) ? 0.f : __builtin_rintf(fminf(fmaxf(q, -7.f), 7.f));
-      packed[i / 8] |= (uint32_t)((int)r + 8) << (4 * (i % 8));
+      for (int e = 0; e < 8; ++e) {
+        const float q = f16r(qs[i][e]);
+        const float r = (q != q) ? 0.f : __builtin_rintf(fminf(fmaxf(q, -7.f), 7.f));
+        packed |= (uint32_t)((int)r + 8) << (4 * e);
+      }
+      *reinterpret_cast<uint32_t*>(codes + (dst * PS + t0 + TPL * i) * (D / 2) + c0 / 2) = packed;
     }
-    uint32_t* cp = reinterpret_cast<uint32_t*>(codes + dst * PS * (D / 2) + tok * (D / 2) + (PER / 2) * j);
-#pragma unroll
-    for (int i = 0; i < PER / 8; ++i) cp[i] = packed[i];
-    const int ng = D / a.int4_group;
-    const int gi = (PER * j) / a.int4_group;
-    if (tok == 0 && (PER * j) % a.int4_group == 0) {
+    if (t0 == 0 && c0 % a.int4_group == 0) {
+      const int ng = D / a.int4_group, gi = c0 / a.int4_group;
       if (a.scale_dtype == IAK_DTYPE_F32) reinterpret_cast<float*>(a.scales)[dst * ng + gi] = s;
       else reinterpret_cast<_Float16*>(a.scales)[dst * ng + gi] = (_Float16)s;
     }
     return;
   }
 
-  const float pam = wave_max(am, 2);
-  uint32_t out[PER / 4];
+  const float pam = wave_max(am, 63);
+  uint32_t out[NL][2];
 #pragma unroll
-  for (int i = 0; i < PER / 4; ++i) out[i] = 0;
+  for (int i = 0; i < NL; ++i) out[i][0] = out[i][1] = 0;
   float s = 0.f, s2 = 0.f;
 
-  if (a.mode == IAK_QUANT_FUSED_INT8) {
+  if constexpr (KIND == KIND_FUSED) {
     s = f16r(f16r(fmaxf(pam, 1e-6f)) / 127.0f);
+    float qs[NL][8];
+    scale_quotients(x, s, qs);
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const float q = f16r(x[i] / s);   // 0/0 when the float16 scale underflows to 0
-      const float r = (q != q) ? 0.f : fminf(fmaxf(__builtin_rintf(q), -128.f), 127.f);
-      out[i / 4] |= ((uint32_t)(int)r & 0xFFu) << (8 * (i % 4));
-    }
-  } else if (a.mode == IAK_QUANT_TRITON_INT8) {
+    for (int i = 0; i < NL; ++i)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float q = f16r(qs[i][e]);      // 0/0 when the float16 scale underflows to 0
+        const float r = (q != q) ? 0.f : fminf(fmaxf(__builtin_rintf(q), -128.f), 127.f);
+        out[i][e / 4] |= ((uint32_t)(int)r & 0xFFu) << (8 * (e % 4));
+      }
+  } else if constexpr (KIND == KIND_TRITON) {
     s = fmaxf(pam, 1e-6f) / 127.0f;
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const float q = x[i] / s;
-      const float r = (q != q) ? 0.f : fminf(fmaxf(__builtin_rintf(q), -127.f), 127.f);
-      out[i / 4] |= ((uint32_t)(int)r & 0xFFu) << (8 * (i % 4));
-    }
-  } else if (prec == IAK_TAG_FP8) {
-    s = f16r(pam / 127.0f);
+    for (int i = 0; i < NL; ++i)
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      // 0/0 on the host is the negative default NaN -> code 0xFF
-      const uint32_t cd = (s == 0.f && x[i] == 0.f) ? 0xFFu : e4m3fn_rne(f16r(x[i] / s));
-      out[i / 4] |= cd << (8 * (i % 4));
-    }
-  } else if (prec == IAK_TAG_INT8) {
+      for (int e = 0; e < 8; ++e) {
+        const float q = x[i][e] / s;
+        const float r = (q != q) ? 0.f : fminf(fmaxf(__builtin_rintf(q), -127.f), 127.f);
+        out[i][e / 4] |= ((uint32_t)(int)r & 0xFFu) << (8 * (e % 4));
+      }
+  } else if constexpr (KIND == IAK_TAG_FP8) {
     s = f16r(pam / 127.0f);
+    float qs[NL][8];
+    scale_quotients(x, s, qs);
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const float q = f16r(x[i] / s);
-      const float r = (q != q) ? 0.f : __builtin_rintf(fminf(fmaxf(q, -127.f), 127.f));
-      out[i / 4] |= ((uint32_t)(int)r & 0xFFu) << (8 * (i % 4));
-    }
+    for (int i = 0; i < NL; ++i)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        // 0/0 on the host is the negative default NaN -> code 0xFF
+        const uint32_t cd = (s == 0.f && x[i][e] == 0.f) ? 0xFFu : e4m3fn_rne(f16r(qs[i][e]));
+        out[i][e / 4] |= cd << (8 * (e % 4));
+      }
+  } else if constexpr (KIND == IAK_TAG_INT8) {
+    s = f16r(pam / 127.0f);
+    float qs[NL][8];
+    scale_quotients(x, s, qs);
+#pragma unroll
+    for (int i = 0; i < NL; ++i)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float q = f16r(qs[i][e]);
+        const float r = (q != q) ? 0.f : __builtin_rintf(fminf(fmaxf(q, -127.f), 127.f));
+        out[i][e / 4] |= ((uint32_t)(int)r & 0xFFu) << (8 * (e % 4));
+      }
   } else {   // INT4_RESIDUAL
     s = f16r(pam / 127.0f);
-    float res[PER];
-    int q1[PER];
+    float res[NL][8];
+    int q1[NL][8];
     float ram = 0.f;
+    float qs[NL][8];
+    scale_quotients(x, s, qs);
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const float q = f16r(x[i] / s);
-      q1[i] = (q != q) ? 0 : (int)__builtin_rintf(fminf(fmaxf(q, -7.f), 7.f));
-      res[i] = x[i] - (float)q1[i] * s;                 // float32, as the reference promotes
-      ram = fmaxf(ram, fabsf(res[i]));
-    }
-    s2 = fmaxf(wave_max(ram, 2) / 127.0f, 1e-8f);
+    for (int i = 0; i < NL; ++i)
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const float q = res[i] / s2;
-      const int q2 = (q != q) ? 0 : (int)__builtin_rintf(fminf(fmaxf(q, -7.f), 7.f));
-      out[i / 4] |= (uint32_t)((q1[i] + 8) | ((q2 + 8) << 4)) << (8 * (i % 4));
-    }
+      for (int e = 0; e < 8; ++e) {
+        const float q = f16r(qs[i][e]);
+        q1[i][e] = (q != q) ? 0 : (int)__builtin_rintf(fminf(fmaxf(q, -7.f), 7.f));
+        res[i][e] = x[i][e] - (float)q1[i][e] * s;      // float32, as the reference promotes
+        ram = fmaxf(ram, fabsf(res[i][e]));
+      }
+    s2 = fmaxf(wave_max(ram, 63) / 127.0f, 1e-8f);
+#pragma unroll
+    for (int i = 0; i < NL; ++i)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float q = res[i][e] / s2;
+        const int q2 = (q != q) ? 0 : (int)__builtin_rintf(fminf(fmaxf(q, -7.f), 7.f));
+        out[i][e / 4] |= (uint32_t)((q1[i][e] + 8) | ((q2 + 8) << 4)) << (8 * (e % 4));
+      }
   }
 
-  uint32_t* cp = reinterpret_cast<uint32_t*>(codes + dst * PS * D + tok * D + PER * j);
 #pragma unroll
-  for (int i = 0; i < PER / 4; ++i) cp[i] = out[i];
+  for (int i = 0; i < NL; ++i) {
+    u2 v;
+    v[0] = out[i][0];
+    v[1] = out[i][1];
+    *reinterpret_cast<u2*>(codes + (dst * PS + t0 + TPL * i) * D + c0) = v;
+  }
   if (lane == 0) {
-    if (prec == IAK_TAG_INT4_RESIDUAL && a.mode == IAK_QUANT_FAKE_QUANTIZE) {
+    if (KIND == IAK_TAG_INT4_RESIDUAL) {
       reinterpret_cast<float*>(a.scales)[2 * dst] = s;
       reinterpret_cast<float*>(a.scales)[2 * dst + 1] = s2;
     } else if (a.scale_dtype == IAK_DTYPE_F32) {
@@ -190,11 +249,26 @@ __global__ __launch_bounds__(256) void quantize_pages_kernel(const iak_quantize_
   }
 }
 
-hipError_t launch_quantize_pages(const iak_quantize_args& a, hipStream_t stream) {
-  const int blocks = (a.num_pages + 3) / 4;
-  if (a.head_dim == 128) hipLaunchKernelGGL(quantize_pages_kernel<128>, dim3(blocks), dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL(quantize_pages_kernel<64>, dim3(blocks), dim3(256), 0, stream, a);
+template <int D>
+static hipError_t launch_d(const iak_quantize_args& a, hipStream_t stream) {
+  const dim3 grid((a.num_pages + 3) / 4), block(256);
+  if (a.mode == IAK_QUANT_FUSED_INT8)
+    hipLaunchKernelGGL((quantize_pages_kernel<D, KIND_FUSED>), grid, block, 0, stream, a);
+  else if (a.mode == IAK_QUANT_TRITON_INT8)
+    hipLaunchKernelGGL((quantize_pages_kernel<D, KIND_TRITON>), grid, block, 0, stream, a);
+  else if (a.precision == IAK_TAG_FP8)
+    hipLaunchKernelGGL((quantize_pages_kernel<D, IAK_TAG_FP8>), grid, block, 0, stream, a);
+  else if (a.precision == IAK_TAG_INT8)
+    hipLaunchKernelGGL((quantize_pages_kernel<D, IAK_TAG_INT8>), grid, block, 0, stream, a);
+  else if (a.precision == IAK_TAG_INT4)
+    hipLaunchKernelGGL((quantize_pages_kernel<D, IAK_TAG_INT4>), grid, block, 0, stream, a);
+  else
+    hipLaunchKernelGGL((quantize_pages_kernel<D, IAK_TAG_INT4_RESIDUAL>), grid, block, 0, stream, a);
   return hipGetLastError();
+}
+
+hipError_t launch_quantize_pages(const iak_quantize_args& a, hipStream_t stream) {
+  return a.head_dim == 128 ? launch_d<128>(a, stream) : launch_d<64>(a, stream);
 }
 
 }  // namespace iak

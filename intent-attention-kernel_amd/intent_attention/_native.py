@@ -124,9 +124,11 @@ def load() -> ctypes.CDLL:
         _load_error = f"cannot load {LIB_PATH}: {e}"
         raise RuntimeError(_load_error) from e
     lib.iak_abi_version.restype = ctypes.c_int
+    lib.iak_abi_version.argtypes = []
     lib.iak_status_string.restype = ctypes.c_char_p
     lib.iak_status_string.argtypes = [ctypes.c_int]
     lib.iak_last_error.restype = ctypes.c_char_p
+    lib.iak_last_error.argtypes = []
     lib.iak_paged_decode_workspace.restype = ctypes.c_int
     lib.iak_paged_decode_workspace.argtypes = [ctypes.POINTER(PagedDecodeArgs), ctypes.POINTER(ctypes.c_size_t)]
     lib.iak_paged_decode.restype = ctypes.c_int
@@ -137,6 +139,8 @@ def load() -> ctypes.CDLL:
     lib.iak_mla_decode.argtypes = [ctypes.POINTER(MlaDecodeArgs), c_void_p, ctypes.c_size_t, c_void_p]
     lib.iak_quantize_pages.restype = ctypes.c_int
     lib.iak_quantize_pages.argtypes = [ctypes.POINTER(QuantizeArgs), c_void_p]
+    lib.iak_build_page_tables.restype = ctypes.c_int
+    lib.iak_build_page_tables.argtypes = [ctypes.POINTER(PageTableArgs), c_void_p]
     ver = lib.iak_abi_version()
     if ver != ABI_VERSION:
         _load_error = f"libiak.so ABI version {ver} != expected {ABI_VERSION}; rebuild the library"

@@ -29,6 +29,9 @@ def test_library_exports_every_declared_symbol():
     assert set(N.EXPORTED) <= set(declared)
     assert lib.iak_abi_version() == N.ABI_VERSION
     assert lib.iak_status_string(0) == b"ok"
+    # undeclared argtypes would pass a stream handle as a masked C int
+    for name in N.EXPORTED:
+        assert getattr(lib, name).argtypes is not None, f"{name} has no ctypes argtypes"
 
 
 @pytest.mark.parametrize("cname,pyname", [("iak_paged_decode_args", "PagedDecodeArgs"),

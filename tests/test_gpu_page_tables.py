@@ -189,3 +189,46 @@ def test_device_routing_feeds_the_decode(dev):
 def _to_oracle(routings):
     return [[P.RoutedBlock(r.name, r.start, r.end, r.policy.value, r.score, r.decision.value, r.precision.value,
                            r.reason) for r in rs] for rs in routings]
+
+
+def test_side_stream_and_graph_replays(dev):
+    """The builder on a non-default stream and captured in a HIP graph: every
+    replay (outputs clobbered by eager work in between) equals the eager result."""
+    import torch
+    from intent_attention import _native as N
+    _say("page tables: side stream + graph replays")
+    rng = np.random.default_rng(12)
+    lists = [_random_spans(rng, 40, 200 * 16, 300) for _ in range(4)]
+    R, W, NP = 8, 64, 4 * 200
+    offs, b, e, t = (torch.tensor(x, dtype=torch.int32, device=dev) for x in _flatten(lists))
+    bt = torch.from_numpy(np.stack([rng.permutation(NP)[:200] for _ in range(4)]).astype(np.int32)).to(dev)
+    table = torch.empty((R, W), dtype=torch.int32, device=dev)
+    counts = torch.empty(R, dtype=torch.int32, device=dev)
+    prec = torch.empty(NP, dtype=torch.int32, device=dev)
+    a = N.PageTableArgs()
+    a.num_rows, a.rows_per_seq, a.rows_per_list, a.table_width, a.page_size, a.num_pages = R, 2, 2, W, 16, NP
+    a.dedupe, a.default_tag, a.block_table_width = 1, 0, 200
+    a.span_offsets, a.span_begin, a.span_end, a.span_tag = offs.data_ptr(), b.data_ptr(), e.data_ptr(), t.data_ptr()
+    a.block_table, a.page_table, a.page_counts, a.page_precision = (bt.data_ptr(), table.data_ptr(),
+                                                                    counts.data_ptr(), prec.data_ptr())
+    want = P.build_page_tables_oracle(lists, R, W, 16, NP, rows_per_seq=2, rows_per_list=2,
+                                      block_table=bt.cpu().numpy())
+    side = torch.cuda.Stream(dev)
+    with torch.cuda.stream(side):
+        N.build_page_tables(a, side.cuda_stream)
+    side.synchronize()
+    assert np.array_equal(_np(table), want[0]) and np.array_equal(_np(counts), want[2])
+    assert np.array_equal(_np(prec), want[1])
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        N.build_page_tables(a, torch.cuda.current_stream(dev).cuda_stream)
+    for rep in range(3):
+        table.fill_(-7)
+        counts.fill_(-7)
+        prec.fill_(-7)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(_np(table), want[0]), rep
+        assert np.array_equal(_np(counts), want[2]), rep
+        assert np.array_equal(_np(prec), want[1]), rep
