@@ -183,14 +183,27 @@ __global__ __launch_bounds__(256) void quantize_pages_kernel(const iak_quantize_
     s = f16r(pam / 127.0f);
     float qs[NL][8];
     scale_quotients(x, s, qs);
+    if (s > 0.f) {
+      // finite quotients, |q| <= 127 * (1 + 2^-11): the hardware's round-to-
+      // nearest-even e4m3fn conversion, two codes per instruction
 #pragma unroll
-    for (int i = 0; i < NL; ++i)
+      for (int i = 0; i < NL; ++i)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        // 0/0 on the host is the negative default NaN -> code 0xFF
-        const uint32_t cd = (s == 0.f && x[i][e] == 0.f) ? 0xFFu : e4m3fn_rne(f16r(qs[i][e]));
-        out[i][e / 4] |= cd << (8 * (e % 4));
-      }
+        for (int w = 0; w < 2; ++w) {
+          int v = __builtin_amdgcn_cvt_pk_fp8_f32(f16r(qs[i][4 * w]), f16r(qs[i][4 * w + 1]), 0, false);
+          v = __builtin_amdgcn_cvt_pk_fp8_f32(f16r(qs[i][4 * w + 2]), f16r(qs[i][4 * w + 3]), v, true);
+          out[i][w] = (uint32_t)v;
+        }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NL; ++i)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          // 0/0 on the host is the negative default NaN -> code 0xFF
+          const uint32_t cd = x[i][e] == 0.f ? 0xFFu : e4m3fn_rne(f16r(qs[i][e]));
+          out[i][e / 4] |= cd << (8 * (e % 4));
+        }
+    }
   } else if constexpr (KIND == IAK_TAG_INT8) {
     s = f16r(pam / 127.0f);
     float qs[NL][8];
