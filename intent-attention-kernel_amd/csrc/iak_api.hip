@@ -177,10 +177,10 @@ iak_status validate_mla(const iak_mla_decode_args* a, MPlan* plan) {
     if (!aligned16(pool)) return fail(IAK_EINVAL, "%s latent pool must be 16-byte aligned", tag_name(n));
   }
 
-  // split plan: one workgroup per (sequence, split, 64 heads); enough
+  // split plan: one workgroup per (sequence, split, 128 heads); enough
   // workgroups for every CU when the table is long enough
   const int W = a->table_width;
-  const int HG = (a->num_heads + 63) / 64;
+  const int HG = (a->num_heads + 127) / 128;
   int chunk = a->pages_per_split;
   if (chunk == 0) {
     const long long units = (long long)a->batch * HG;

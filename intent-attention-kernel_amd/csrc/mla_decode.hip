@@ -9,24 +9,31 @@
 // to the context is a plain GEMM and stays outside this kernel.
 //
 // Work decomposition
-//   One workgroup of 4 waves (one per SIMD, up to 512 registers each) reduces
+//   One workgroup of 8 waves (two per SIMD, up to 256 registers each) reduces
 //   one split -- up to 64 consecutive page-table entries of one sequence -- for
-//   64 heads. Each latent page is loaded once per workgroup, two pages ahead
-//   in registers, and staged in LDS as two f16 tiles: [token][dim] for the
-//   score product and [dim][token] (value dims only) for the value product.
+//   128 heads, so each latent page is read from HBM once per sequence. Pages
+//   stream from HBM straight into an LDS ring (global_load_lds), three pages
+//   ahead, and are staged once per workgroup as two f16 tiles: [token][dim]
+//   for the score product and [dim][token] (value dims) for the value product.
 //   FP8 / INT8 codes are converted to f16 exactly while staging; the page
 //   scale folds into the score multiplier and into P.
-//   Scores: wave w owns heads 16w .. 16w+15:
-//     S^T[16 tok x 16 heads] = C[16 tok x DQK] . Q^T on v_mfma_f32_16x16x32_f16,
-//     the A operand read from the [token][dim] tile, Q resident in registers.
-//     Online softmax per head in the exp2 domain (max shared by the four lane
-//     groups, lazy rescale with 2^8 head-room as in the paged decode).
-//   Values: wave w owns value dims (DV/4)w .. (DV/4)(w+1)-1 for all 64 heads:
-//     O[16 heads x 16 dims] += P[16 heads x 16 tok] . C[16 tok x 16 dims] on
-//     v_mfma_f32_16x16x16f16; P comes through LDS in the A-operand layout the
-//     score result already has, C from the [dim][token] tile.
-//   Splits write (m, l, acc) partials merged by splitk_merge_kernel; a sequence
-//   that fits one split writes the output directly.
+//   Wave w owns heads 16w .. 16w+15 end to end (its score and value
+//   accumulators live in VGPRs: this file is built with MFMA results in VGPRs,
+//   so the softmax rescale is plain VALU work):
+//     scores  S^T[16 tok x 16 heads] = C[16 tok x DQK] . Q^T on
+//             v_mfma_f32_16x16x32_f16, C from the [token][dim] tile, Q
+//             resident in registers;
+//     softmax online per head in the exp2 domain (max shared by the four lane
+//             groups, lazy rescale with 2^8 head-room as in the paged decode),
+//             entirely inside the wave;
+//     values  O[16 heads x 16 dims] += P[16 heads x 16 tok] . C[16 tok x 16 dims]
+//             on v_mfma_f32_16x16x16f16 for all DV dims: the score result's
+//             register layout (lane: head column, four consecutive tokens) is
+//             exactly the A operand P, so P never leaves the registers; C comes
+//             from the [dim][token] tile.
+//   Two barriers per page (tile ready; tile buffer free). Splits write (m, l,
+//   acc) partials merged by splitk_merge_kernel; a sequence that fits one
+//   split writes the output directly.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -40,22 +47,20 @@
 namespace iak {
 
 template <int DQK, int DV, bool WIDE> struct Mla {
-  static constexpr int WAVES = 4;
+  static constexpr int WAVES = 8;              // two per SIMD
   static constexpr int THREADS = 64 * WAVES;
-  static constexpr int QB = 1;                 // score head blocks (of 16) per wave
-  static constexpr int HEADS = 16 * QB * WAVES;  // heads per workgroup
-  static constexpr int HB = HEADS / 16;
+  static constexpr int HT = 1;                 // 16-head tiles per wave
+  static constexpr int HEADS = 16 * HT * WAVES;  // heads per workgroup
   static constexpr int KSTEPS = DQK / 32;      // score k-steps
-  static constexpr int DVW = DV / WAVES;       // value dims per wave
-  static constexpr int NDB = DVW / 16;         // 16-dim blocks per wave
+  static constexpr int NDB = DV / 16;          // 16-dim value blocks (all of them, per wave)
   static constexpr int T1 = DQK + 8;           // [token][dim] row stride (halves)
   static constexpr int T2 = 20;                // [dim][token] row stride (halves)
   static constexpr int PAGE8 = PS * DQK;       // bytes of a one-byte page (a multiple of 1 KB)
   static constexpr int SLOT = WIDE ? 2 * PAGE8 : PAGE8;   // raw ring slot: the widest page
   static constexpr int NDMA = (SLOT / 1024 + WAVES - 1) / WAVES;   // 1 KB copies per wave per page
-  static constexpr int RING = 4;               // raw slots: pages stream in two steps ahead
+  static constexpr int RING = WIDE ? 4 : 5;    // raw slots; pages stream RING - 2 steps ahead of staging
   static constexpr int TASKS = DQK;            // 4 tokens x 4 dims per staging task
-  static_assert(DQK % 32 == 0 && DV % 64 == 0 && DV <= DQK && PAGE8 % 1024 == 0, "unsupported MLA shape");
+  static_assert(DQK % 32 == 0 && DV % 16 == 0 && DV <= DQK && PAGE8 % 1024 == 0, "unsupported MLA shape");
 };
 
 template <int DQK, int DV, bool WIDE> struct MlaShared {
@@ -63,11 +68,8 @@ template <int DQK, int DV, bool WIDE> struct MlaShared {
   _Float16 t1[2][PS][C::T1];              // [buffer][token][dim]
   _Float16 t2[2][DV][C::T2];              // [buffer][value dim][token]
   alignas(16) uint8_t ring[C::RING][C::SLOT];   // raw pages as copied from HBM
-  u2 pbuf[C::HB][64];                     // P of every head block, A-operand layout
-  alignas(16) float alpha[C::HEADS];      // rescale factor of every head this page
   float lsum[C::HEADS];                   // final denominators
   float mmax[C::HEADS];                   // final maxima
-  int grow[C::WAVES];
 };
 
 // Page metadata of one split: lane i holds entry i.
@@ -145,8 +147,17 @@ template <int DQK, int DV, bool WIDE>
 __device__ __forceinline__ void mla_stage_tiles(MlaShared<DQK, DV, WIDE>& sh, int slot, int buf, int tag, int voff,
                                                 int tid) {
   using C = Mla<DQK, DV, WIDE>;
+  constexpr int NB = DQK / 4;   // 4-dim blocks
+  static_assert(NB % 16 == 0, "staging lane map needs a multiple of 16 dim blocks");
   for (int task = tid; task < C::TASKS; task += C::THREADS) {
-    const int tg = task / (DQK / 4), d = 4 * (task % (DQK / 4));
+    // lane map: token group = task % 4, dim block = 16 (task / 64 + tg) +
+    // (task / 4) % 16 (mod NB), a bijection onto (tg, block). For DQK = 576 the
+    // token groups' rows start on the same LDS bank; the skew of 16 blocks per
+    // group spreads the ring reads over all banks, and the [dim][token] writes
+    // of a wave cover every bank twice (the minimum for 512 bytes).
+    const int tg = task & 3;
+    const int blk = (16 * ((task >> 6) + tg) + ((task >> 2) & 15)) % NB;
+    const int d = 4 * blk;
     uint32_t lo[4], hi[4];   // token 4tg+t: f16 pairs (d, d+1), (d+2, d+3)
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
@@ -173,7 +184,7 @@ __device__ __forceinline__ void mla_stage_tiles(MlaShared<DQK, DV, WIDE>& sh, in
 }
 
 template <int DQK, int DV, bool WIDE>
-__global__ __launch_bounds__(256, 1) void mla_decode_kernel(const MArgs a) {
+__global__ __launch_bounds__(512, 1) void mla_decode_kernel(const MArgs a) {
   using C = Mla<DQK, DV, WIDE>;
   __shared__ MlaShared<DQK, DV, WIDE> sh;
   const int tid = threadIdx.x;
@@ -183,6 +194,7 @@ __global__ __launch_bounds__(256, 1) void mla_decode_kernel(const MArgs a) {
   const int split = blockIdx.x - b * a.splits;
   const int hg = blockIdx.y;
   const int start = split * a.chunk;
+  const int head0 = hg * C::HEADS + 16 * C::HT * w;   // first head of this wave
 
   // token bound of the sequence (table entry e holds tokens 16e .. 16e+15)
   const int limit = a.valid ? __builtin_amdgcn_readfirstlane(a.valid[b]) : 0x7FFFFFFF;
@@ -190,11 +202,11 @@ __global__ __launch_bounds__(256, 1) void mla_decode_kernel(const MArgs a) {
   const uint64_t mask = __builtin_amdgcn_ballot_w64(meta.pid >= 0);
   const int np = __builtin_popcountll(mask);
 
-  // Q of the wave's head blocks, rounded to f16: dims 32i + 8g .. +7 of head c
-  h8 q[C::QB][C::KSTEPS];
+  // Q of the wave's head tiles, rounded to f16: dims 32i + 8g .. +7 of head c
+  h8 q[C::HT][C::KSTEPS];
 #pragma unroll
-  for (int k = 0; k < C::QB; ++k) {
-    const int h = hg * C::HEADS + 16 * (C::QB * w + k) + c;
+  for (int k = 0; k < C::HT; ++k) {
+    const int h = head0 + 16 * k + c;
     const bool live = h < a.H;
     const int64_t off = (int64_t)b * a.qsb + (int64_t)(live ? h : 0) * a.qsh + 8 * g;
 #pragma unroll
@@ -220,14 +232,17 @@ __global__ __launch_bounds__(256, 1) void mla_decode_kernel(const MArgs a) {
     }
   }
 
-  float m[C::QB], l[C::QB];
+  // per lane: running max and partial denominator of head column c of tile k
+  // (the partial covers the lane's four token rows; summed over g at the end)
+  float m[C::HT], l[C::HT];
 #pragma unroll
-  for (int k = 0; k < C::QB; ++k) { m[k] = -__builtin_inff(); l[k] = 0.f; }
-  f4 acc[C::HB][C::NDB];
+  for (int k = 0; k < C::HT; ++k) { m[k] = -__builtin_inff(); l[k] = 0.f; }
+  // O tile (k, db): rows = heads 4g .. 4g+3 of tile k, column = value dim 16 db + c
+  f4 acc[C::HT][C::NDB];
 #pragma unroll
-  for (int hb = 0; hb < C::HB; ++hb)
+  for (int k = 0; k < C::HT; ++k)
 #pragma unroll
-    for (int db = 0; db < C::NDB; ++db) acc[hb][db] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int db = 0; db < C::NDB; ++db) acc[k][db] = f4{0.f, 0.f, 0.f, 0.f};
 
   if (np > 0) {
     // page cursor: lanes of the pages in table order; past the end the last
@@ -251,166 +266,148 @@ __global__ __launch_bounds__(256, 1) void mla_decode_kernel(const MArgs a) {
     mla_wait_pages<C::NDMA, C::RING - 2>();
     __syncthreads();
     mla_stage_tiles<DQK, DV, WIDE>(sh, 0, 0, page_tag(qi[0]), a.VOFF, tid);
-    __syncthreads();
 
-    // One page: page j+RING-1 starts streaming, page j+1 (landed) is staged into
-    // the other tile buffer, then scores and values of page j. `R` is the tile
-    // buffer of page j; page p streams into ring slot p % RING.
-    auto step = [&](auto RC, int j) {
-      constexpr int R = decltype(RC)::value;
+    // One page per iteration and one barrier: each wave waits for its copies
+    // of page j+1, then the barrier makes page j's tiles (staged in the
+    // previous iteration) and page j+1's raw bytes visible to every wave and
+    // ends every read of the other tile buffer. Then page j+RING-1 starts
+    // streaming, page j+1 is staged into the other buffer while the scores of
+    // page j run on the matrix cores, and the softmax and values of page j
+    // follow. R = j & 1 is the tile buffer of page j; page p streams into ring
+    // slot p % RING.
+    int slot_new = C::RING - 1, slot_nxt = 1;
+    for (int j = 0; j < np; ++j) {
+      const int R = j & 1;
       const int cur = qi[0], nxt = qi[1];
+      mla_wait_pages<C::NDMA, C::RING - 3>();
+      __syncthreads();
       const int inew = next_page();
-      mla_dma_page<DQK, DV, WIDE>(sh, (j + C::RING - 1) % C::RING, a, page_pid(inew), page_tag(inew), w, lane);
+      mla_dma_page<DQK, DV, WIDE>(sh, slot_new, a, page_pid(inew), page_tag(inew), w, lane);
 
-      // ---- scores of page j (buffer R) for the wave's head blocks, issued
-      // first so the MFMAs run while the wave stages page j+1; in a step past
-      // the end they see stale data and their result is dropped ----
-      const float pscale = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, meta.scale), cur));
-      const float smul = a.score_mult * pscale;
-      // NCH independent accumulation chains keep the MFMA pipe busy; summed after
-      constexpr int NCH = C::KSTEPS >= 4 ? 4 : C::KSTEPS;
-      f4 s[C::QB], sc[C::QB][NCH];
+      // ---- scores of page j (buffer R), issued first so the MFMAs run while
+      // the wave stages page j+1 ----
+      constexpr int NCH = C::KSTEPS >= 2 ? 2 : 1;    // chains per head tile
+      f4 sc[C::HT][NCH];
 #pragma unroll
-      for (int k = 0; k < C::QB; ++k)
+      for (int k = 0; k < C::HT; ++k)
 #pragma unroll
         for (int ch = 0; ch < NCH; ++ch) sc[k][ch] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int i = 0; i < C::KSTEPS; ++i) {
         const h8 av = *reinterpret_cast<const h8*>(&sh.t1[R][c][32 * i + 8 * g]);
 #pragma unroll
-        for (int k = 0; k < C::QB; ++k)
+        for (int k = 0; k < C::HT; ++k)
           sc[k][i % NCH] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, q[k][i], sc[k][i % NCH], 0, 0, 0);
       }
 
-      // ---- stage page j+1 (landed: this wave's copies, then every wave's) ----
+      // ---- stage page j+1 (landed before the barrier) ----
       const bool have_next = j + 1 < np;
-      mla_wait_pages<C::NDMA, C::RING - 2>();
-      __syncthreads();
-      if (have_next) mla_stage_tiles<DQK, DV, WIDE>(sh, (j + 1) % C::RING, 1 - R, page_tag(nxt), a.VOFF, tid);
+      if (have_next) mla_stage_tiles<DQK, DV, WIDE>(sh, slot_nxt, 1 - R, page_tag(nxt), a.VOFF, tid);
 #pragma unroll
       for (int k = 0; k < C::RING - 2; ++k) qi[k] = qi[k + 1];
       qi[C::RING - 2] = inew;
+      slot_new = slot_new + 1 == C::RING ? 0 : slot_new + 1;
+      slot_nxt = slot_nxt + 1 == C::RING ? 0 : slot_nxt + 1;
 
-      if (j >= np) return;
-#pragma unroll
-      for (int k = 0; k < C::QB; ++k) {
-        s[k] = sc[k][0];
-#pragma unroll
-        for (int ch = 1; ch < NCH; ++ch) s[k] += sc[k][ch];
-      }
-      float pm[C::QB];
-      bool grow[C::QB];
-      bool wgrow = false;
+      const float pscale = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, meta.scale), cur));
+      const float smul = a.score_mult * pscale;
       // tokens at or past the bound (only in the sequence's last visited page)
       const int64_t tok0 = (int64_t)(start + cur) * PS + 4 * g;
       const bool ragged = (int64_t)(start + cur) * PS + PS > limit;
+      h4 pa[C::HT];        // P of tile k: A operand (row = head c, k = tokens 4g .. 4g+3)
+      float al[C::HT];
+      bool grow_any = false;
 #pragma unroll
-      for (int k = 0; k < C::QB; ++k) {
-        s[k] *= smul;
+      for (int k = 0; k < C::HT; ++k) {
+        f4 s = sc[k][0];
+#pragma unroll
+        for (int ch = 1; ch < NCH; ++ch) s += sc[k][ch];
+        s *= smul;
         if (ragged) {
 #pragma unroll
           for (int r = 0; r < 4; ++r)
-            if (tok0 + r >= limit) s[k][r] = -__builtin_inff();
+            if (tok0 + r >= limit) s[r] = -__builtin_inff();
         }
-        pm[k] = xmax16_32(fmaxf(fmaxf(s[k][0], s[k][1]), fmaxf(s[k][2], s[k][3])));
-        grow[k] = pm[k] > m[k] + RESCALE_SLACK;
-        wgrow = wgrow || grow[k];
-      }
-      const bool any = __builtin_amdgcn_ballot_w64(wgrow) != 0;
-#pragma unroll
-      for (int k = 0; k < C::QB; ++k) {
-        float al = 1.0f;
-        if (any) {
-          const float mn = grow[k] ? pm[k] : m[k];
-          al = __builtin_amdgcn_exp2f(m[k] - mn);   // 0 on the first page (m = -inf)
-          l[k] *= al;
-          m[k] = mn;
+        const float pm = xmax16_32(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
+        const bool grow = pm > m[k] + RESCALE_SLACK;
+        al[k] = 1.0f;
+        if (grow) {
+          al[k] = __builtin_amdgcn_exp2f(m[k] - pm);   // 0 on the first page (m = -inf)
+          m[k] = pm;
         }
-        const float p0 = __builtin_amdgcn_exp2f(s[k][0] - m[k]);
-        const float p1 = __builtin_amdgcn_exp2f(s[k][1] - m[k]);
-        const float p2 = __builtin_amdgcn_exp2f(s[k][2] - m[k]);
-        const float p3 = __builtin_amdgcn_exp2f(s[k][3] - m[k]);
-        l[k] += (p0 + p1) + (p2 + p3);
+        grow_any = grow_any || grow;
+        const float p0 = __builtin_amdgcn_exp2f(s[0] - m[k]);
+        const float p1 = __builtin_amdgcn_exp2f(s[1] - m[k]);
+        const float p2 = __builtin_amdgcn_exp2f(s[2] - m[k]);
+        const float p3 = __builtin_amdgcn_exp2f(s[3] - m[k]);
+        l[k] = l[k] * al[k] + ((p0 + p1) + (p2 + p3));
         typedef float f2 __attribute__((ext_vector_type(2)));
         const h2 x = __builtin_convertvector((f2{p0, p1} * pscale), h2);
         const h2 y = __builtin_convertvector((f2{p2, p3} * pscale), h2);
-        sh.pbuf[C::QB * w + k][lane] = u2{bits(x), bits(y)};
-        if (g == 0) sh.alpha[16 * (C::QB * w + k) + c] = al;
+        pa[k] = __builtin_bit_cast(h4, u2{bits(x), bits(y)});
       }
-      if (lane == 0) sh.grow[w] = any ? 1 : 0;
-      __syncthreads();
-
-      // ---- values of page j: all the workgroup's heads, the wave's value dims ----
-      if (sh.grow[0] | sh.grow[1] | sh.grow[2] | sh.grow[3]) {
+      // rescale: the O rows are heads 4g + r, whose factor sits in lane 4g + r
+      if (__builtin_amdgcn_ballot_w64(grow_any) != 0) {
 #pragma unroll
-        for (int hb = 0; hb < C::HB; ++hb) {
-          const f4 al = *reinterpret_cast<const f4*>(&sh.alpha[16 * hb + 4 * g]);
+        for (int k = 0; k < C::HT; ++k) {
+          f4 ar;
 #pragma unroll
-          for (int db = 0; db < C::NDB; ++db) acc[hb][db] *= al;
+          for (int r = 0; r < 4; ++r) ar[r] = __shfl(al[k], 4 * g + r, 64);
+#pragma unroll
+          for (int db = 0; db < C::NDB; ++db) acc[k][db] *= ar;
         }
       }
-      h4 bop[C::NDB];
-#pragma unroll
-      for (int db = 0; db < C::NDB; ++db)
-        bop[db] = *reinterpret_cast<const h4*>(&sh.t2[R][C::DVW * w + 16 * db + c][4 * g]);
-#pragma unroll
-      for (int hb = 0; hb < C::HB; ++hb) {
-        const h4 aop = __builtin_bit_cast(h4, sh.pbuf[hb][lane]);
-#pragma unroll
-        for (int db = 0; db < C::NDB; ++db)
-          acc[hb][db] = __builtin_amdgcn_mfma_f32_16x16x16f16(aop, bop[db], acc[hb][db], 0, 0, 0);
-      }
-    };
 
-    // pages in pairs so the tile-buffer indices are static
-    // (both steps of a pair always run -- an exit between them makes the
-    // compiler keep two copies of the accumulators -- and a step past the end
-    // issues its loads but skips its compute)
-    for (int j = 0; j < np; j += 2) {
-      step(std::integral_constant<int, 0>{}, j);
-      step(std::integral_constant<int, 1>{}, j + 1);
+      // ---- values of page j: the wave's heads, every value dim ----
+#pragma unroll
+      for (int db = 0; db < C::NDB; ++db) {
+        const h4 bop = *reinterpret_cast<const h4*>(&sh.t2[R][16 * db + c][4 * g]);
+#pragma unroll
+        for (int k = 0; k < C::HT; ++k)
+          acc[k][db] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa[k], bop, acc[k][db], 0, 0, 0);
+      }
     }
     // the copies of the pages past the end land before the LDS is reused or released
     mla_wait_pages<C::NDMA, 0>();
   }
 
-  // ---- denominators and maxima of every head, then the output or the partials ----
+  // ---- denominators and maxima of the wave's heads, then the output or the partials ----
 #pragma unroll
-  for (int k = 0; k < C::QB; ++k) {
+  for (int k = 0; k < C::HT; ++k) {
     const float ls = xsum16_32(l[k]);
     if (g == 0) {
-      sh.lsum[16 * (C::QB * w + k) + c] = ls;
-      sh.mmax[16 * (C::QB * w + k) + c] = m[k];
+      sh.lsum[16 * (C::HT * w + k) + c] = ls;
+      sh.mmax[16 * (C::HT * w + k) + c] = m[k];
     }
   }
   __syncthreads();
 #pragma unroll
-  for (int hb = 0; hb < C::HB; ++hb) {
+  for (int k = 0; k < C::HT; ++k) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int hl = 16 * hb + 4 * g + r;
+      const int hl = 16 * (C::HT * w + k) + 4 * g + r;
       const int h = hg * C::HEADS + hl;
       if (h >= a.H) continue;
       if (a.splits == 1) {
         const float ls = sh.lsum[hl];
         const float inv = ls > 0.f ? 1.0f / ls : 0.0f;
-        const int64_t o = (int64_t)b * a.osb + (int64_t)h * a.osh + C::DVW * w + c;
+        const int64_t o = (int64_t)b * a.osb + (int64_t)h * a.osh + c;
 #pragma unroll
         for (int db = 0; db < C::NDB; ++db) {
-          const float v = acc[hb][db][r] * inv;
+          const float v = acc[k][db][r] * inv;
           if (a.out_dtype == IAK_DTYPE_F32) reinterpret_cast<float*>(a.out)[o + 16 * db] = v;
           else if (a.out_dtype == IAK_DTYPE_F16) reinterpret_cast<_Float16*>(a.out)[o + 16 * db] = (_Float16)v;
           else reinterpret_cast<__bf16*>(a.out)[o + 16 * db] = (__bf16)v;
         }
       } else {
         const int64_t slot = ((int64_t)b * a.splits + split) * a.H + h;
-        if (w == 0 && c == 0) {
+        if (c == 0) {
           a.ws_m[slot] = sh.mmax[hl];
           a.ws_l[slot] = sh.lsum[hl];
         }
-        float* op = a.ws_acc + slot * DV + C::DVW * w + c;
+        float* op = a.ws_acc + slot * DV + c;
 #pragma unroll
-        for (int db = 0; db < C::NDB; ++db) op[16 * db] = acc[hb][db][r];
+        for (int db = 0; db < C::NDB; ++db) op[16 * db] = acc[k][db][r];
       }
     }
   }
