@@ -13,6 +13,8 @@
  *                               and intent_quant_decode_attention_triton()
  *                                                                      triton_intent_quant_attention.py:342-457
  *   iak_paged_decode_workspace  (no counterpart: sizes the split-K partial buffer the caller allocates)
+ *   iak_paged_decode_timed,     (no counterpart: the same calls with HIP events around the split
+ *   iak_mla_decode_timed         kernel, for timing it apart from the merge)
  *   iak_mla_decode              mla_decode_triton() / _mla_decode_cpu()    triton_mla_decode.py:110-186
  *                               (the latent context; mla_sparse_decode_reference mla.py:61-92,
  *                               mla_triton_decode mla.py:95-136)
@@ -137,6 +139,13 @@ iak_status iak_paged_decode_workspace(const iak_paged_decode_args* args, size_t*
 iak_status iak_paged_decode(const iak_paged_decode_args* args, void* workspace,
                             size_t workspace_bytes, void* stream);
 
+/* iak_paged_decode with two hipEvent_t (either may be NULL) recorded on `stream`
+ * immediately before and after the split kernel's launch, so a caller can time
+ * that kernel apart from the merge. No counterpart in the reference: it is the
+ * measurement hook of bench.py's roofline figure. */
+iak_status iak_paged_decode_timed(const iak_paged_decode_args* args, void* workspace,
+                                  size_t workspace_bytes, void* stream, void* ev_begin, void* ev_end);
+
 /*
  * MLA latent decode: every query head attends to one shared compressed KV
  * (latent rows of qk_dim values; dims v_offset .. v_offset + v_dim - 1 of a
@@ -180,6 +189,11 @@ iak_status iak_mla_decode_workspace(const iak_mla_decode_args* args, size_t* byt
 /* MLA latent decode on MFMA, split-K over pages with an LSE merge; async on `stream`. */
 iak_status iak_mla_decode(const iak_mla_decode_args* args, void* workspace, size_t workspace_bytes,
                           void* stream);
+
+/* iak_mla_decode with events around the split kernel, as iak_paged_decode_timed
+ * (no counterpart in the reference). */
+iak_status iak_mla_decode_timed(const iak_mla_decode_args* args, void* workspace, size_t workspace_bytes,
+                                void* stream, void* ev_begin, void* ev_end);
 
 /*
  * Quantise-on-write: float16 pages [num_pages, page_size, head_dim] -> codes and

@@ -234,8 +234,8 @@ iak_status iak_paged_decode_workspace(const iak_paged_decode_args* args, size_t*
   return IAK_OK;
 }
 
-iak_status iak_paged_decode(const iak_paged_decode_args* a, void* workspace, size_t workspace_bytes,
-                            void* stream) {
+static iak_status paged_decode_impl(const iak_paged_decode_args* a, void* workspace, size_t workspace_bytes,
+                                    void* stream, void* ev_begin, void* ev_end) {
   Plan plan;
   iak_status st = validate(a, &plan);
   if (st != IAK_OK) return st;
@@ -279,9 +279,20 @@ iak_status iak_paged_decode(const iak_paged_decode_args* a, void* workspace, siz
     k.ws_l = reinterpret_cast<float*>(ws + plan.ws_l);
     k.ws_acc = reinterpret_cast<float*>(ws + plan.ws_acc);
   }
-  const hipError_t e = iak::launch_paged_decode(k, static_cast<hipStream_t>(stream));
+  const hipError_t e = iak::launch_paged_decode(k, static_cast<hipStream_t>(stream),
+                                                static_cast<hipEvent_t>(ev_begin), static_cast<hipEvent_t>(ev_end));
   if (e != hipSuccess) return fail(IAK_EHIP, "kernel launch failed: %s", hipGetErrorString(e));
   return IAK_OK;
+}
+
+iak_status iak_paged_decode(const iak_paged_decode_args* a, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+  return paged_decode_impl(a, workspace, workspace_bytes, stream, nullptr, nullptr);
+}
+
+iak_status iak_paged_decode_timed(const iak_paged_decode_args* a, void* workspace, size_t workspace_bytes,
+                                  void* stream, void* ev_begin, void* ev_end) {
+  return paged_decode_impl(a, workspace, workspace_bytes, stream, ev_begin, ev_end);
 }
 
 iak_status iak_mla_decode_workspace(const iak_mla_decode_args* args, size_t* bytes) {
@@ -293,7 +304,8 @@ iak_status iak_mla_decode_workspace(const iak_mla_decode_args* args, size_t* byt
   return IAK_OK;
 }
 
-iak_status iak_mla_decode(const iak_mla_decode_args* a, void* workspace, size_t workspace_bytes, void* stream) {
+static iak_status mla_decode_impl(const iak_mla_decode_args* a, void* workspace, size_t workspace_bytes,
+                                  void* stream, void* ev_begin, void* ev_end) {
   MPlan plan;
   iak_status st = validate_mla(a, &plan);
   if (st != IAK_OK) return st;
@@ -332,9 +344,19 @@ iak_status iak_mla_decode(const iak_mla_decode_args* a, void* workspace, size_t 
     m.ws_l = reinterpret_cast<float*>(ws + plan.ws_l);
     m.ws_acc = reinterpret_cast<float*>(ws + plan.ws_acc);
   }
-  const hipError_t e = iak::launch_mla_decode(m, static_cast<hipStream_t>(stream));
+  const hipError_t e = iak::launch_mla_decode(m, static_cast<hipStream_t>(stream),
+                                              static_cast<hipEvent_t>(ev_begin), static_cast<hipEvent_t>(ev_end));
   if (e != hipSuccess) return fail(IAK_EHIP, "kernel launch failed: %s", hipGetErrorString(e));
   return IAK_OK;
+}
+
+iak_status iak_mla_decode(const iak_mla_decode_args* a, void* workspace, size_t workspace_bytes, void* stream) {
+  return mla_decode_impl(a, workspace, workspace_bytes, stream, nullptr, nullptr);
+}
+
+iak_status iak_mla_decode_timed(const iak_mla_decode_args* a, void* workspace, size_t workspace_bytes,
+                                void* stream, void* ev_begin, void* ev_end) {
+  return mla_decode_impl(a, workspace, workspace_bytes, stream, ev_begin, ev_end);
 }
 
 iak_status iak_quantize_pages(const iak_quantize_args* a, void* stream) {

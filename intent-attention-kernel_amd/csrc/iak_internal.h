@@ -56,7 +56,10 @@ struct KArgs {
   float* ws_acc;      // [B, Hkv, splits, G, D]
 };
 
-hipError_t launch_paged_decode(const KArgs& k, hipStream_t stream);
+// ev_begin / ev_end (may be null) are recorded on `stream` around the split
+// kernel alone, so callers can time it apart from the merge
+hipError_t launch_paged_decode(const KArgs& k, hipStream_t stream, hipEvent_t ev_begin = nullptr,
+                               hipEvent_t ev_end = nullptr);
 
 // Kernel-side arguments of the MLA latent decode (built from iak_mla_decode_args).
 struct MArgs {
@@ -87,7 +90,8 @@ struct MArgs {
   float* ws_acc;      // [B, splits, H, DV]
 };
 
-hipError_t launch_mla_decode(const MArgs& m, hipStream_t stream);
+hipError_t launch_mla_decode(const MArgs& m, hipStream_t stream, hipEvent_t ev_begin = nullptr,
+                             hipEvent_t ev_end = nullptr);
 
 hipError_t launch_quantize_pages(const iak_quantize_args& a, hipStream_t stream);
 

@@ -414,10 +414,12 @@ __global__ __launch_bounds__(512, 1) void mla_decode_kernel(const MArgs a) {
 }
 
 template <int DQK, int DV, bool WIDE>
-hipError_t launch_mla_w(const MArgs& m, hipStream_t stream) {
+hipError_t launch_mla_w(const MArgs& m, hipStream_t stream, hipEvent_t ev_begin, hipEvent_t ev_end) {
+  if (ev_begin) hipEventRecord(ev_begin, stream);
   hipLaunchKernelGGL((mla_decode_kernel<DQK, DV, WIDE>), dim3(m.B * m.splits, m.HG),
                      dim3(Mla<DQK, DV, WIDE>::THREADS), 0, stream, m);
   hipError_t e = hipGetLastError();
+  if (ev_end) hipEventRecord(ev_end, stream);
   if (e != hipSuccess || m.splits == 1) return e;
   // the paged-decode merge over rows (b, 0) of H heads
   KArgs k{};
@@ -431,18 +433,18 @@ hipError_t launch_mla_w(const MArgs& m, hipStream_t stream) {
 
 // WIDE: FP16 latent pages are reachable (ring slots sized for two bytes per value)
 template <int DQK, int DV>
-hipError_t launch_mla(const MArgs& m, hipStream_t stream) {
-  return m.wide ? launch_mla_w<DQK, DV, true>(m, stream) : launch_mla_w<DQK, DV, false>(m, stream);
+hipError_t launch_mla(const MArgs& m, hipStream_t stream, hipEvent_t eb, hipEvent_t ee) {
+  return m.wide ? launch_mla_w<DQK, DV, true>(m, stream, eb, ee) : launch_mla_w<DQK, DV, false>(m, stream, eb, ee);
 }
 
-hipError_t launch_mla_decode(const MArgs& m, hipStream_t stream) {
+hipError_t launch_mla_decode(const MArgs& m, hipStream_t stream, hipEvent_t eb, hipEvent_t ee) {
   switch (m.DQK * 1000 + m.DV) {
-    case 64064: return launch_mla<64, 64>(m, stream);
-    case 128128: return launch_mla<128, 128>(m, stream);
-    case 256256: return launch_mla<256, 256>(m, stream);
-    case 512512: return launch_mla<512, 512>(m, stream);
-    case 576512: return launch_mla<576, 512>(m, stream);
-    case 576064: return launch_mla<576, 64>(m, stream);
+    case 64064: return launch_mla<64, 64>(m, stream, eb, ee);
+    case 128128: return launch_mla<128, 128>(m, stream, eb, ee);
+    case 256256: return launch_mla<256, 256>(m, stream, eb, ee);
+    case 512512: return launch_mla<512, 512>(m, stream, eb, ee);
+    case 576512: return launch_mla<576, 512>(m, stream, eb, ee);
+    case 576064: return launch_mla<576, 64>(m, stream, eb, ee);
   }
   return hipErrorInvalidValue;
 }

@@ -592,11 +592,13 @@ void paged_decode_kernel(const KArgs a) {
 }
 
 template <int D, int QT>
-hipError_t launch_decode(const KArgs& k, hipStream_t stream) {
+hipError_t launch_decode(const KArgs& k, hipStream_t stream, hipEvent_t ev_begin, hipEvent_t ev_end) {
   const int blocks = (k.items + IAK_WAVES_PER_BLOCK - 1) / IAK_WAVES_PER_BLOCK;
+  if (ev_begin) hipEventRecord(ev_begin, stream);
   hipLaunchKernelGGL((paged_decode_kernel<D, QT>), dim3(blocks), dim3(64 * IAK_WAVES_PER_BLOCK), 0,
                      stream, k);
   hipError_t e = hipGetLastError();
+  if (ev_end) hipEventRecord(ev_end, stream);
   if (e != hipSuccess || k.splits == 1) return e;
   const int mblocks = (k.B * k.Hq + 3) / 4;
   hipLaunchKernelGGL((splitk_merge_kernel<D>), dim3(mblocks), dim3(256), 0, stream, k);
@@ -604,16 +606,16 @@ hipError_t launch_decode(const KArgs& k, hipStream_t stream) {
 }
 
 template <int D>
-hipError_t launch_d(const KArgs& k, hipStream_t stream) {
+hipError_t launch_d(const KArgs& k, hipStream_t stream, hipEvent_t eb, hipEvent_t ee) {
   switch (k.q_dtype) {
-    case IAK_DTYPE_F32: return launch_decode<D, IAK_DTYPE_F32>(k, stream);
-    case IAK_DTYPE_BF16: return launch_decode<D, IAK_DTYPE_BF16>(k, stream);
-    default: return launch_decode<D, IAK_DTYPE_F16>(k, stream);
+    case IAK_DTYPE_F32: return launch_decode<D, IAK_DTYPE_F32>(k, stream, eb, ee);
+    case IAK_DTYPE_BF16: return launch_decode<D, IAK_DTYPE_BF16>(k, stream, eb, ee);
+    default: return launch_decode<D, IAK_DTYPE_F16>(k, stream, eb, ee);
   }
 }
 
-hipError_t launch_paged_decode(const KArgs& k, hipStream_t stream) {
-  return k.D == 128 ? launch_d<128>(k, stream) : launch_d<64>(k, stream);
+hipError_t launch_paged_decode(const KArgs& k, hipStream_t stream, hipEvent_t ev_begin, hipEvent_t ev_end) {
+  return k.D == 128 ? launch_d<128>(k, stream, ev_begin, ev_end) : launch_d<64>(k, stream, ev_begin, ev_end);
 }
 
 }  // namespace iak

@@ -101,7 +101,7 @@ class PageTableArgs(ctypes.Structure):
 EXPORTED = ("iak_abi_version", "iak_status_string", "iak_last_error",
             "iak_paged_decode_workspace", "iak_paged_decode",
             "iak_mla_decode_workspace", "iak_mla_decode", "iak_quantize_pages",
-            "iak_build_page_tables")
+            "iak_build_page_tables", "iak_paged_decode_timed", "iak_mla_decode_timed")
 
 _lib: Optional[ctypes.CDLL] = None
 _load_error: Optional[str] = None
@@ -139,6 +139,12 @@ def load() -> ctypes.CDLL:
     lib.iak_mla_decode.argtypes = [ctypes.POINTER(MlaDecodeArgs), c_void_p, ctypes.c_size_t, c_void_p]
     lib.iak_quantize_pages.restype = ctypes.c_int
     lib.iak_quantize_pages.argtypes = [ctypes.POINTER(QuantizeArgs), c_void_p]
+    lib.iak_paged_decode_timed.restype = ctypes.c_int
+    lib.iak_paged_decode_timed.argtypes = [ctypes.POINTER(PagedDecodeArgs), c_void_p, ctypes.c_size_t, c_void_p,
+                                           c_void_p, c_void_p]
+    lib.iak_mla_decode_timed.restype = ctypes.c_int
+    lib.iak_mla_decode_timed.argtypes = [ctypes.POINTER(MlaDecodeArgs), c_void_p, ctypes.c_size_t, c_void_p,
+                                         c_void_p, c_void_p]
     lib.iak_build_page_tables.restype = ctypes.c_int
     lib.iak_build_page_tables.argtypes = [ctypes.POINTER(PageTableArgs), c_void_p]
     ver = lib.iak_abi_version()
@@ -167,8 +173,14 @@ def workspace_bytes(args: PagedDecodeArgs) -> int:
     return int(n.value)
 
 
-def paged_decode(args: PagedDecodeArgs, workspace_ptr: int, workspace_size: int, stream: int) -> None:
-    check(load().iak_paged_decode(ctypes.byref(args), workspace_ptr or None, workspace_size, stream or None))
+def paged_decode(args: PagedDecodeArgs, workspace_ptr: int, workspace_size: int, stream: int,
+                 events: Optional[tuple] = None) -> None:
+    """``events``: optional (begin, end) hipEvent_t handles recorded around the split kernel."""
+    if events is None:
+        check(load().iak_paged_decode(ctypes.byref(args), workspace_ptr or None, workspace_size, stream or None))
+    else:
+        check(load().iak_paged_decode_timed(ctypes.byref(args), workspace_ptr or None, workspace_size,
+                                            stream or None, events[0] or None, events[1] or None))
 
 
 def mla_workspace_bytes(args: MlaDecodeArgs) -> int:
@@ -177,8 +189,14 @@ def mla_workspace_bytes(args: MlaDecodeArgs) -> int:
     return int(n.value)
 
 
-def mla_decode(args: MlaDecodeArgs, workspace_ptr: int, workspace_size: int, stream: int) -> None:
-    check(load().iak_mla_decode(ctypes.byref(args), workspace_ptr or None, workspace_size, stream or None))
+def mla_decode(args: MlaDecodeArgs, workspace_ptr: int, workspace_size: int, stream: int,
+               events: Optional[tuple] = None) -> None:
+    """``events``: optional (begin, end) hipEvent_t handles recorded around the split kernel."""
+    if events is None:
+        check(load().iak_mla_decode(ctypes.byref(args), workspace_ptr or None, workspace_size, stream or None))
+    else:
+        check(load().iak_mla_decode_timed(ctypes.byref(args), workspace_ptr or None, workspace_size,
+                                          stream or None, events[0] or None, events[1] or None))
 
 
 def quantize_pages(args: QuantizeArgs, stream: int) -> None:

@@ -60,9 +60,12 @@ class MlaPlan:
         self._ws = (torch.empty(self.workspace_bytes, dtype=torch.uint8, device=device)
                     if self.workspace_bytes else None)
 
-    def run(self, stream: Optional[int] = None) -> None:
+    def run(self, stream: Optional[int] = None, events: Optional[tuple] = None) -> None:
+        """Launch on ``stream`` (default: torch's current stream). ``events``: an
+        optional pair of torch.cuda.Event recorded around the split kernel alone."""
         s = torch.cuda.current_stream(self.device).cuda_stream if stream is None else stream
-        N.mla_decode(self.args, self._ws.data_ptr() if self._ws is not None else 0, self.workspace_bytes, s)
+        ev = None if events is None else (events[0].cuda_event, events[1].cuda_event)
+        N.mla_decode(self.args, self._ws.data_ptr() if self._ws is not None else 0, self.workspace_bytes, s, ev)
 
 
 def make_mla_plan(q: torch.Tensor, pools: LatentPools, page_table: torch.Tensor, page_counts: torch.Tensor,
