@@ -18,6 +18,7 @@ from .fused_selected_quant_decode import (
     FusedDecodeConfig,
     FusedKVPrecision,
     fused_selected_quant_decode,
+    fused_selected_quant_decode_reference,
     is_native_available,
     metadata_to_kernel_tensors,
 )
@@ -48,7 +49,8 @@ __all__ = [
     "SELECTED_POLICIES", "BlockLayout", "BlockPolicy", "SemanticBlock",
     "BlockDecision", "BlockRouter", "RoutedBlock", "RouterConfig", "compute_block_scores",
     "routing_to_kernel_metadata",
-    "FusedDecodeConfig", "FusedKVPrecision", "fused_selected_quant_decode", "is_native_available",
+    "FusedDecodeConfig", "FusedKVPrecision", "fused_selected_quant_decode", "fused_selected_quant_decode_reference",
+    "is_native_available",
     "metadata_to_kernel_tensors",
     "IntentQuantizer", "KVPrecision", "QuantPolicy", "compute_quant_error", "fake_dequantize_tensor",
     "fake_quantize_tensor",

@@ -176,6 +176,29 @@ def fused_selected_quant_decode(
     return out
 
 
+def fused_selected_quant_decode_reference(
+    query: torch.Tensor,
+    k_pages_fp16: torch.Tensor,
+    v_pages_fp16: torch.Tensor,
+    k_pages_int8: torch.Tensor,
+    v_pages_int8: torch.Tensor,
+    k_scales: torch.Tensor,
+    v_scales: torch.Tensor,
+    page_table: torch.Tensor,
+    page_precision: torch.Tensor,
+    page_counts: torch.Tensor,
+    config: FusedDecodeConfig,
+) -> torch.Tensor:
+    """The reference's correctness entry point (fused_selected_quant_decode.py:267-336),
+    same signature (``config`` required) and result: [B, H, 1, D] float16 of
+    the per-(b, h) online-softmax loop over the listed pages. Here it is the
+    same computation as ``fused_selected_quant_decode``, on the MI355X kernel:
+    device tensors only (host tensors raise RuntimeError; the CPU restatement
+    of the loop is test code in ``oracle/``, not a product path)."""
+    return fused_selected_quant_decode(query, k_pages_fp16, v_pages_fp16, k_pages_int8, v_pages_int8, k_scales,
+                                       v_scales, page_table, page_precision, page_counts, config)
+
+
 def fake_int8_pages_from_fp16(pages: torch.Tensor, eps: float = 1e-6) -> Tuple[torch.Tensor, torch.Tensor]:
     """[num_pages, page_size, D] float16 -> (int8 codes, float16 scales [num_pages]).
 

@@ -186,6 +186,12 @@ def test_fused_api_matches_reference_golden(dev, g3, variant):
     assert out.shape == (2, 4, 1, 64) and out.dtype == torch.float16 and out.is_cuda
     ref = g3["out_triton_scales" if pre else "out"].astype(np.float32)
     assert np.abs(out.float().cpu().numpy() - ref).max() <= TOL_FP16
+    # the reference's correctness entry point, same arguments, same device result
+    from intent_attention import fused_selected_quant_decode_reference
+    out_r = fused_selected_quant_decode_reference(t("q"), t("k16"), t("v16"), t(f"{pre}k8"), t(f"{pre}v8"),
+                                                  t(f"{pre}ks"), t(f"{pre}vs"), t("page_table"), t("page_precision"),
+                                                  t("page_counts"), cfg)
+    assert torch.equal(out_r, out)
 
 
 def test_fused_api_reference_test_facts(dev):

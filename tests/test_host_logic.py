@@ -141,6 +141,10 @@ def test_decode_entry_points_refuse_host_tensors():
         ia.fused_selected_quant_decode(x, p, p, i8, i8, s, s, torch.zeros(1, 1, 1, dtype=torch.int32),
                                        torch.zeros(2, dtype=torch.int32), torch.ones(1, 1, dtype=torch.int32),
                                        ia.FusedDecodeConfig())
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        ia.fused_selected_quant_decode_reference(x, p, p, i8, i8, s, s, torch.zeros(1, 1, 1, dtype=torch.int32),
+                                                 torch.zeros(2, dtype=torch.int32), torch.ones(1, 1, dtype=torch.int32),
+                                                 ia.FusedDecodeConfig())
     with pytest.raises(ValueError, match="head_dim"):
         ia.fused_selected_quant_decode(x, p, p, i8, i8, s, s, torch.zeros(1, 1, 1, dtype=torch.int32),
                                        torch.zeros(2, dtype=torch.int32), torch.ones(1, 1, dtype=torch.int32),
