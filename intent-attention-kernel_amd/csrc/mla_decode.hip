@@ -49,27 +49,26 @@ namespace iak {
 template <int DQK, int DV, bool WIDE> struct Mla {
   static constexpr int WAVES = 8;              // two per SIMD
   static constexpr int THREADS = 64 * WAVES;
-  static constexpr int HT = 1;                 // 16-head tiles per wave
-  static constexpr int HEADS = 16 * HT * WAVES;  // heads per workgroup
+  static constexpr int HEADS = 16 * WAVES;     // heads per workgroup (16 per wave)
   static constexpr int KSTEPS = DQK / 32;      // score k-steps
   static constexpr int NDB = DV / 16;          // 16-dim value blocks (all of them, per wave)
+  static constexpr int TOK = 2 * PS;           // tokens per step: two pages
   static constexpr int T1 = DQK + 8;           // [token][dim] row stride (halves)
-  static constexpr int T2 = 20;                // [dim][token] row stride (halves)
   static constexpr int PAGE8 = PS * DQK;       // bytes of a one-byte page (a multiple of 1 KB)
   static constexpr int SLOT = WIDE ? 2 * PAGE8 : PAGE8;   // raw ring slot: the widest page
   static constexpr int NDMA = (SLOT / 1024 + WAVES - 1) / WAVES;   // 1 KB copies per wave per page
-  static constexpr int RING = WIDE ? 4 : 5;    // raw slots; pages stream RING - 2 steps ahead of staging
-  static constexpr int TASKS = DQK;            // 4 tokens x 4 dims per staging task
+  static constexpr int SLOTS = WIDE ? 2 : 4;   // page pairs in the ring = steps a pair streams in ahead
+  static constexpr int CHUNKS = DQK / 8;       // 8-value staging chunks per token
   static_assert(DQK % 32 == 0 && DV % 16 == 0 && DV <= DQK && PAGE8 % 1024 == 0, "unsupported MLA shape");
+  static_assert((SLOTS & (SLOTS - 1)) == 0 && SLOTS >= 2, "ring of a power-of-two number of page pairs");
 };
 
 template <int DQK, int DV, bool WIDE> struct MlaShared {
   using C = Mla<DQK, DV, WIDE>;
-  _Float16 t1[2][PS][C::T1];              // [buffer][token][dim]
-  _Float16 t2[2][DV][C::T2];              // [buffer][value dim][token]
-  alignas(16) uint8_t ring[C::RING][C::SLOT];   // raw pages as copied from HBM
-  float lsum[C::HEADS];                   // final denominators
-  float mmax[C::HEADS];                   // final maxima
+  _Float16 t1[2][C::TOK][C::T1];                    // [buffer][token][dim], f16
+  alignas(16) uint8_t ring[C::SLOTS][2][C::SLOT];   // raw page pairs as copied from HBM
+  float lsum[C::HEADS];                             // final denominators
+  float mmax[C::HEADS];                             // final maxima
 };
 
 // Page metadata of one split: lane i holds entry i.
@@ -116,8 +115,7 @@ __device__ __forceinline__ MlaPages mla_page_meta(const MArgs& a, int b, int sta
 // for them are written out (mla_wait_pages) and no compiler-issued load runs
 // inside the page loop.
 template <int DQK, int DV, bool WIDE>
-__device__ __forceinline__ void mla_dma_page(MlaShared<DQK, DV, WIDE>& sh, int slot, const MArgs& a, int pid,
-                                             int tag, int w, int lane) {
+__device__ __forceinline__ void mla_dma_page(uint8_t* slot, const MArgs& a, int pid, int tag, int w, int lane) {
   using C = Mla<DQK, DV, WIDE>;
   const bool wide = WIDE && tag == IAK_TAG_FP16;
   const int nch = (wide ? 2 * C::PAGE8 : C::PAGE8) / 1024;
@@ -130,7 +128,7 @@ __device__ __forceinline__ void mla_dma_page(MlaShared<DQK, DV, WIDE>& sh, int s
     int ch = w + C::WAVES * k;
     ch = ch < nch ? ch : nch - 1;
     const uint8_t* src = base + (int64_t)ch * 1024 + 16 * lane;
-    const uint32_t dst = (uint32_t)(uintptr_t)(lds_u8*)&sh.ring[slot][ch * 1024];
+    const uint32_t dst = (uint32_t)(uintptr_t)(lds_u8*)(slot + ch * 1024);
     asm volatile("global_load_lds_dwordx4 %0, off" : : "v"(src), "{m0}"(dst) : "memory");
   }
 }
@@ -140,47 +138,47 @@ template <int NDMA, int PAGES> __device__ __forceinline__ void mla_wait_pages() 
   asm volatile("s_waitcnt vmcnt(%0)" : : "n"(NDMA * PAGES) : "memory");
 }
 
-// LDS -> tiles: each task takes 4 tokens x 4 dims, converts one-byte codes to
-// f16 (exact) into the [token][dim] tile and writes the value dims transposed
-// into the [dim][token] tile.
+// LDS ring -> [token][dim] f16 tile for a page pair: each task converts one
+// 8-value chunk of one token (8 code bytes, or 16 bytes of f16) -- consecutive
+// tasks are consecutive chunks, so reads and writes are contiguous per wave.
+// FP8 / INT8 codes convert to f16 exactly.
 template <int DQK, int DV, bool WIDE>
-__device__ __forceinline__ void mla_stage_tiles(MlaShared<DQK, DV, WIDE>& sh, int slot, int buf, int tag, int voff,
-                                                int tid) {
+__device__ __forceinline__ void mla_stage_pair(MlaShared<DQK, DV, WIDE>& sh, int slot, int buf, int tag0, int tag1,
+                                               int tid) {
   using C = Mla<DQK, DV, WIDE>;
-  constexpr int NB = DQK / 4;   // 4-dim blocks
-  static_assert(NB % 16 == 0, "staging lane map needs a multiple of 16 dim blocks");
-  for (int task = tid; task < C::TASKS; task += C::THREADS) {
-    // lane map: token group = task % 4, dim block = 16 (task / 64 + tg) +
-    // (task / 4) % 16 (mod NB), a bijection onto (tg, block). For DQK = 576 the
-    // token groups' rows start on the same LDS bank; the skew of 16 blocks per
-    // group spreads the ring reads over all banks, and the [dim][token] writes
-    // of a wave cover every bank twice (the minimum for 512 bytes).
-    const int tg = task & 3;
-    const int blk = (16 * ((task >> 6) + tg) + ((task >> 2) & 15)) % NB;
-    const int d = 4 * blk;
-    uint32_t lo[4], hi[4];   // token 4tg+t: f16 pairs (d, d+1), (d+2, d+3)
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int tok = 4 * tg + t;
-      if (WIDE && tag == IAK_TAG_FP16) {
-        const u2 x = *reinterpret_cast<const u2*>(&sh.ring[slot][(tok * DQK + d) * 2]);
-        lo[t] = x[0];
-        hi[t] = x[1];
-      } else {
-        const uint32_t x = *reinterpret_cast<const uint32_t*>(&sh.ring[slot][tok * DQK + d]);
-        if (tag == IAK_TAG_FP8) fp8x4_to_f16(x, lo[t], hi[t]);
-        else i8x4_to_f16(x, lo[t], hi[t]);
-      }
-      *reinterpret_cast<u2*>(&sh.t1[buf][tok][d]) = u2{lo[t], hi[t]};
+  constexpr int PER_PAGE = PS * C::CHUNKS;
+  for (int task = tid; task < 2 * PER_PAGE; task += C::THREADS) {
+    const int half = task >= PER_PAGE ? 1 : 0;
+    const int t = task - half * PER_PAGE;
+    const int tok = t / C::CHUNKS, ch = t - tok * C::CHUNKS;
+    const int tag = half ? tag1 : tag0;
+    const uint8_t* raw = sh.ring[slot][half];
+    u4 v;
+    if (WIDE && tag == IAK_TAG_FP16) {
+      v = *reinterpret_cast<const u4*>(raw + (tok * DQK + 8 * ch) * 2);
+    } else {
+      const u2 x = *reinterpret_cast<const u2*>(raw + tok * DQK + 8 * ch);
+      uint32_t lo0, hi0, lo1, hi1;
+      if (tag == IAK_TAG_FP8) { fp8x4_to_f16(x[0], lo0, hi0); fp8x4_to_f16(x[1], lo1, hi1); }
+      else { i8x4_to_f16(x[0], lo0, hi0); i8x4_to_f16(x[1], lo1, hi1); }
+      v = u4{lo0, hi0, lo1, hi1};
     }
-    const int vd = d - voff;
-    if (vd >= 0 && vd < DV) {
-      *reinterpret_cast<u2*>(&sh.t2[buf][vd + 0][4 * tg]) = u2{pack_lo(lo[0], lo[1]), pack_lo(lo[2], lo[3])};
-      *reinterpret_cast<u2*>(&sh.t2[buf][vd + 1][4 * tg]) = u2{pack_hi(lo[0], lo[1]), pack_hi(lo[2], lo[3])};
-      *reinterpret_cast<u2*>(&sh.t2[buf][vd + 2][4 * tg]) = u2{pack_lo(hi[0], hi[1]), pack_lo(hi[2], hi[3])};
-      *reinterpret_cast<u2*>(&sh.t2[buf][vd + 3][4 * tg]) = u2{pack_hi(hi[0], hi[1]), pack_hi(hi[2], hi[3])};
-    }
+    *reinterpret_cast<u4*>(&sh.t1[buf][PS * half + tok][8 * ch]) = v;
   }
+}
+
+// Four f16 of a value column, transposed out of the [token][dim] tile: lane i of
+// each 16-lane group names row `row0 + i / 4`, columns col0 + 4 (i % 4) .. +3;
+// lane j receives column col0 + j of rows row0 .. row0 + 3 (ds_read_b64_tr_b16:
+// element m of lane j comes from lane 4m + j / 4 of its group, element j % 4).
+template <int DQK, int DV, bool WIDE>
+__device__ __forceinline__ h4 mla_read_column(const MlaShared<DQK, DV, WIDE>& sh, int buf, int row0, int col0,
+                                              int c) {
+  typedef short s4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s4 lds_s4;
+  const _Float16* p = &sh.t1[buf][row0 + (c >> 2)][col0 + 4 * (c & 3)];
+  const s4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p));
+  return __builtin_bit_cast(h4, v);
 }
 
 template <int DQK, int DV, bool WIDE>
@@ -194,7 +192,7 @@ __global__ __launch_bounds__(512, 1) void mla_decode_kernel(const MArgs a) {
   const int split = blockIdx.x - b * a.splits;
   const int hg = blockIdx.y;
   const int start = split * a.chunk;
-  const int head0 = hg * C::HEADS + 16 * C::HT * w;   // first head of this wave
+  const int head = hg * C::HEADS + 16 * w + c;   // this lane's score / P head
 
   // token bound of the sequence (table entry e holds tokens 16e .. 16e+15)
   const int limit = a.valid ? __builtin_amdgcn_readfirstlane(a.valid[b]) : 0x7FFFFFFF;
@@ -202,13 +200,11 @@ __global__ __launch_bounds__(512, 1) void mla_decode_kernel(const MArgs a) {
   const uint64_t mask = __builtin_amdgcn_ballot_w64(meta.pid >= 0);
   const int np = __builtin_popcountll(mask);
 
-  // Q of the wave's head tiles, rounded to f16: dims 32i + 8g .. +7 of head c
-  h8 q[C::HT][C::KSTEPS];
-#pragma unroll
-  for (int k = 0; k < C::HT; ++k) {
-    const int h = head0 + 16 * k + c;
-    const bool live = h < a.H;
-    const int64_t off = (int64_t)b * a.qsb + (int64_t)(live ? h : 0) * a.qsh + 8 * g;
+  // Q of the lane's head, rounded to f16: dims 32i + 8g .. +7 (B operand of the scores)
+  h8 q[C::KSTEPS];
+  {
+    const bool live = head < a.H;
+    const int64_t off = (int64_t)b * a.qsb + (int64_t)(live ? head : 0) * a.qsh + 8 * g;
 #pragma unroll
     for (int i = 0; i < C::KSTEPS; ++i) {
       h8 v;
@@ -228,25 +224,22 @@ __global__ __launch_bounds__(512, 1) void mla_decode_kernel(const MArgs a) {
         }
       }
       if (!live) v = h8{0, 0, 0, 0, 0, 0, 0, 0};
-      q[k][i] = v;
+      q[i] = v;
     }
   }
 
-  // per lane: running max and partial denominator of head column c of tile k
-  // (the partial covers the lane's four token rows; summed over g at the end)
-  float m[C::HT], l[C::HT];
+  // per lane: running max and partial denominator of head column c (the
+  // partial covers the lane's token rows; summed over g at the end)
+  float m = -__builtin_inff(), l = 0.f;
+  // O tile db: rows = heads 4g .. 4g+3, column = value dim 16 db + c
+  f4 acc[C::NDB];
 #pragma unroll
-  for (int k = 0; k < C::HT; ++k) { m[k] = -__builtin_inff(); l[k] = 0.f; }
-  // O tile (k, db): rows = heads 4g .. 4g+3 of tile k, column = value dim 16 db + c
-  f4 acc[C::HT][C::NDB];
-#pragma unroll
-  for (int k = 0; k < C::HT; ++k)
-#pragma unroll
-    for (int db = 0; db < C::NDB; ++db) acc[k][db] = f4{0.f, 0.f, 0.f, 0.f};
+  for (int db = 0; db < C::NDB; ++db) acc[db] = f4{0.f, 0.f, 0.f, 0.f};
 
   if (np > 0) {
+    const int nsteps = (np + 1) >> 1;
     // page cursor: lanes of the pages in table order; past the end the last
-    // page is named again (loads stay unconditional, compute is skipped)
+    // page is named again (copies stay unconditional, compute is masked)
     uint64_t rem = mask;
     int last = __builtin_ctzll(mask);
     auto next_page = [&]() {
@@ -255,116 +248,111 @@ __global__ __launch_bounds__(512, 1) void mla_decode_kernel(const MArgs a) {
     };
     auto page_pid = [&](int idx) { return __builtin_amdgcn_readlane(meta.pid, idx); };
     auto page_tag = [&](int idx) { return __builtin_amdgcn_readlane(meta.tag, idx); };
-    // pages 0 .. RING-2 start streaming into ring slots 0 .. RING-2; page 0 is
-    // staged into tile buffer 0. qi[k] = lane of page j+k.
-    int qi[C::RING - 1];
+    auto page_scale = [&](int idx) {
+      return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, meta.scale), idx));
+    };
+    // pq[2k], pq[2k+1]: lanes of the pages of step s+k (ring slot (s+k) % SLOTS)
+    int pq[2 * C::SLOTS];
 #pragma unroll
-    for (int k = 0; k < C::RING - 1; ++k) {
-      qi[k] = next_page();
-      mla_dma_page<DQK, DV, WIDE>(sh, k, a, page_pid(qi[k]), page_tag(qi[k]), w, lane);
-    }
-    mla_wait_pages<C::NDMA, C::RING - 2>();
+    for (int k = 0; k < C::SLOTS; ++k)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        pq[2 * k + h] = next_page();
+        mla_dma_page<DQK, DV, WIDE>(sh.ring[k][h], a, page_pid(pq[2 * k + h]), page_tag(pq[2 * k + h]), w, lane);
+      }
+    mla_wait_pages<C::NDMA, 2 * (C::SLOTS - 1)>();
     __syncthreads();
-    mla_stage_tiles<DQK, DV, WIDE>(sh, 0, 0, page_tag(qi[0]), a.VOFF, tid);
+    mla_stage_pair<DQK, DV, WIDE>(sh, 0, 0, page_tag(pq[0]), page_tag(pq[1]), tid);
 
-    // One page per iteration and one barrier: each wave waits for its copies
-    // of page j+1, then the barrier makes page j's tiles (staged in the
-    // previous iteration) and page j+1's raw bytes visible to every wave and
-    // ends every read of the other tile buffer. Then page j+RING-1 starts
-    // streaming, page j+1 is staged into the other buffer while the scores of
-    // page j run on the matrix cores, and the softmax and values of page j
-    // follow. R = j & 1 is the tile buffer of page j; page p streams into ring
-    // slot p % RING.
-    int slot_new = C::RING - 1, slot_nxt = 1;
-    for (int j = 0; j < np; ++j) {
-      const int R = j & 1;
-      const int cur = qi[0], nxt = qi[1];
-      mla_wait_pages<C::NDMA, C::RING - 3>();
+    // One page pair per iteration and one barrier: each wave waits for its
+    // copies of pair s+1, then the barrier makes pair s's tile (staged in the
+    // previous iteration) and pair s+1's raw bytes visible to every wave and
+    // ends every read of the other tile buffer. Then pair s+SLOTS starts
+    // streaming into the ring slot pair s came from, pair s+1 is staged into
+    // the other tile buffer while pair s's score MFMAs run, and the softmax and
+    // values of pair s follow. R = s & 1 is pair s's tile buffer.
+    for (int st = 0; st < nsteps; ++st) {
+      const int R = st & 1;
+      const int cur0 = pq[0], cur1 = pq[1], nx0 = pq[2], nx1 = pq[3];
+      mla_wait_pages<C::NDMA, 2 * (C::SLOTS - 2)>();
       __syncthreads();
-      const int inew = next_page();
-      mla_dma_page<DQK, DV, WIDE>(sh, slot_new, a, page_pid(inew), page_tag(inew), w, lane);
+      const int slot = st & (C::SLOTS - 1);
+      const int in0 = next_page(), in1 = next_page();
+      mla_dma_page<DQK, DV, WIDE>(sh.ring[slot][0], a, page_pid(in0), page_tag(in0), w, lane);
+      mla_dma_page<DQK, DV, WIDE>(sh.ring[slot][1], a, page_pid(in1), page_tag(in1), w, lane);
 
-      // ---- scores of page j (buffer R), issued first so the MFMAs run while
-      // the wave stages page j+1 ----
-      constexpr int NCH = C::KSTEPS >= 2 ? 2 : 1;    // chains per head tile
-      f4 sc[C::HT][NCH];
-#pragma unroll
-      for (int k = 0; k < C::HT; ++k)
-#pragma unroll
-        for (int ch = 0; ch < NCH; ++ch) sc[k][ch] = f4{0.f, 0.f, 0.f, 0.f};
+      // ---- scores of pair s: S^T[16 tok x 16 heads] per page, two chains ----
+      f4 s0 = f4{0.f, 0.f, 0.f, 0.f}, s1 = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int i = 0; i < C::KSTEPS; ++i) {
-        const h8 av = *reinterpret_cast<const h8*>(&sh.t1[R][c][32 * i + 8 * g]);
-#pragma unroll
-        for (int k = 0; k < C::HT; ++k)
-          sc[k][i % NCH] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, q[k][i], sc[k][i % NCH], 0, 0, 0);
+        const h8 a0 = *reinterpret_cast<const h8*>(&sh.t1[R][c][32 * i + 8 * g]);
+        const h8 a1 = *reinterpret_cast<const h8*>(&sh.t1[R][PS + c][32 * i + 8 * g]);
+        s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, q[i], s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, q[i], s1, 0, 0, 0);
       }
 
-      // ---- stage page j+1 (landed before the barrier) ----
-      const bool have_next = j + 1 < np;
-      if (have_next) mla_stage_tiles<DQK, DV, WIDE>(sh, slot_nxt, 1 - R, page_tag(nxt), a.VOFF, tid);
+      // ---- stage pair s+1 (landed before the barrier) ----
+      if (st + 1 < nsteps)
+        mla_stage_pair<DQK, DV, WIDE>(sh, (st + 1) & (C::SLOTS - 1), 1 - R, page_tag(nx0), page_tag(nx1), tid);
 #pragma unroll
-      for (int k = 0; k < C::RING - 2; ++k) qi[k] = qi[k + 1];
-      qi[C::RING - 2] = inew;
-      slot_new = slot_new + 1 == C::RING ? 0 : slot_new + 1;
-      slot_nxt = slot_nxt + 1 == C::RING ? 0 : slot_nxt + 1;
+      for (int k = 0; k < 2 * C::SLOTS - 2; ++k) pq[k] = pq[k + 2];
+      pq[2 * C::SLOTS - 2] = in0;
+      pq[2 * C::SLOTS - 1] = in1;
 
-      const float pscale = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, meta.scale), cur));
-      const float smul = a.score_mult * pscale;
-      // tokens at or past the bound (only in the sequence's last visited page)
-      const int64_t tok0 = (int64_t)(start + cur) * PS + 4 * g;
-      const bool ragged = (int64_t)(start + cur) * PS + PS > limit;
-      h4 pa[C::HT];        // P of tile k: A operand (row = head c, k = tokens 4g .. 4g+3)
-      float al[C::HT];
-      bool grow_any = false;
+      // ---- softmax over the pair's 32 tokens ----
+      const float ps0 = page_scale(cur0), ps1 = page_scale(cur1);
+      s0 *= a.score_mult * ps0;
+      s1 *= a.score_mult * ps1;
+      // tokens at or past the bound (the sequence's last visited page), and the
+      // second page of a pair past the end
+      const bool live1 = 2 * st + 1 < np;
+      const int64_t lim0 = (int64_t)limit - (int64_t)(start + cur0) * PS - 4 * g;
+      const int64_t lim1 = live1 ? (int64_t)limit - (int64_t)(start + cur1) * PS - 4 * g : 0;
 #pragma unroll
-      for (int k = 0; k < C::HT; ++k) {
-        f4 s = sc[k][0];
+      for (int r = 0; r < 4; ++r) {
+        if (r >= lim0) s0[r] = -__builtin_inff();
+        if (r >= lim1) s1[r] = -__builtin_inff();
+      }
+      const float pm = xmax16_32(fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])),
+                                       fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3]))));
+      const bool grow = pm > m + RESCALE_SLACK;
+      float al = 1.0f;
+      if (grow) {
+        al = __builtin_amdgcn_exp2f(m - pm);   // 0 on the first pair (m = -inf)
+        m = pm;
+      }
+      f4 p0, p1;
 #pragma unroll
-        for (int ch = 1; ch < NCH; ++ch) s += sc[k][ch];
-        s *= smul;
-        if (ragged) {
+      for (int r = 0; r < 4; ++r) {
+        p0[r] = __builtin_amdgcn_exp2f(s0[r] - m);
+        p1[r] = __builtin_amdgcn_exp2f(s1[r] - m);
+      }
+      l = l * al + (((p0[0] + p0[1]) + (p0[2] + p0[3])) + ((p1[0] + p1[1]) + (p1[2] + p1[3])));
+      // P: A operand of the value product (row = head c, k = 8g + m:
+      // tokens 4g + m of the first page, then of the second); V scales fold in
+      h8 pa;
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (tok0 + r >= limit) s[r] = -__builtin_inff();
-        }
-        const float pm = xmax16_32(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
-        const bool grow = pm > m[k] + RESCALE_SLACK;
-        al[k] = 1.0f;
-        if (grow) {
-          al[k] = __builtin_amdgcn_exp2f(m[k] - pm);   // 0 on the first page (m = -inf)
-          m[k] = pm;
-        }
-        grow_any = grow_any || grow;
-        const float p0 = __builtin_amdgcn_exp2f(s[0] - m[k]);
-        const float p1 = __builtin_amdgcn_exp2f(s[1] - m[k]);
-        const float p2 = __builtin_amdgcn_exp2f(s[2] - m[k]);
-        const float p3 = __builtin_amdgcn_exp2f(s[3] - m[k]);
-        l[k] = l[k] * al[k] + ((p0 + p1) + (p2 + p3));
-        typedef float f2 __attribute__((ext_vector_type(2)));
-        const h2 x = __builtin_convertvector((f2{p0, p1} * pscale), h2);
-        const h2 y = __builtin_convertvector((f2{p2, p3} * pscale), h2);
-        pa[k] = __builtin_bit_cast(h4, u2{bits(x), bits(y)});
+      for (int r = 0; r < 4; ++r) {
+        pa[r] = (_Float16)(p0[r] * ps0);
+        pa[4 + r] = (_Float16)(p1[r] * ps1);
       }
       // rescale: the O rows are heads 4g + r, whose factor sits in lane 4g + r
-      if (__builtin_amdgcn_ballot_w64(grow_any) != 0) {
+      if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+        f4 ar;
 #pragma unroll
-        for (int k = 0; k < C::HT; ++k) {
-          f4 ar;
+        for (int r = 0; r < 4; ++r) ar[r] = __shfl(al, 4 * g + r, 64);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) ar[r] = __shfl(al[k], 4 * g + r, 64);
-#pragma unroll
-          for (int db = 0; db < C::NDB; ++db) acc[k][db] *= ar;
-        }
+        for (int db = 0; db < C::NDB; ++db) acc[db] *= ar;
       }
 
-      // ---- values of page j: the wave's heads, every value dim ----
+      // ---- values of pair s: the wave's heads, every value dim ----
 #pragma unroll
       for (int db = 0; db < C::NDB; ++db) {
-        const h4 bop = *reinterpret_cast<const h4*>(&sh.t2[R][16 * db + c][4 * g]);
-#pragma unroll
-        for (int k = 0; k < C::HT; ++k)
-          acc[k][db] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa[k], bop, acc[k][db], 0, 0, 0);
+        const int col = a.VOFF + 16 * db;
+        const h4 b0 = mla_read_column<DQK, DV, WIDE>(sh, R, 4 * g, col, c);
+        const h4 b1 = mla_read_column<DQK, DV, WIDE>(sh, R, PS + 4 * g, col, c);
+        const h8 bop = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
+        acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, bop, acc[db], 0, 0, 0);
       }
     }
     // the copies of the pages past the end land before the LDS is reused or released
@@ -372,43 +360,39 @@ __global__ __launch_bounds__(512, 1) void mla_decode_kernel(const MArgs a) {
   }
 
   // ---- denominators and maxima of the wave's heads, then the output or the partials ----
-#pragma unroll
-  for (int k = 0; k < C::HT; ++k) {
-    const float ls = xsum16_32(l[k]);
+  {
+    const float ls = xsum16_32(l);
     if (g == 0) {
-      sh.lsum[16 * (C::HT * w + k) + c] = ls;
-      sh.mmax[16 * (C::HT * w + k) + c] = m[k];
+      sh.lsum[16 * w + c] = ls;
+      sh.mmax[16 * w + c] = m;
     }
   }
   __syncthreads();
 #pragma unroll
-  for (int k = 0; k < C::HT; ++k) {
+  for (int r = 0; r < 4; ++r) {
+    const int hl = 16 * w + 4 * g + r;
+    const int h = hg * C::HEADS + hl;
+    if (h >= a.H) continue;
+    if (a.splits == 1) {
+      const float ls = sh.lsum[hl];
+      const float inv = ls > 0.f ? 1.0f / ls : 0.0f;
+      const int64_t o = (int64_t)b * a.osb + (int64_t)h * a.osh + c;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int hl = 16 * (C::HT * w + k) + 4 * g + r;
-      const int h = hg * C::HEADS + hl;
-      if (h >= a.H) continue;
-      if (a.splits == 1) {
-        const float ls = sh.lsum[hl];
-        const float inv = ls > 0.f ? 1.0f / ls : 0.0f;
-        const int64_t o = (int64_t)b * a.osb + (int64_t)h * a.osh + c;
-#pragma unroll
-        for (int db = 0; db < C::NDB; ++db) {
-          const float v = acc[k][db][r] * inv;
-          if (a.out_dtype == IAK_DTYPE_F32) reinterpret_cast<float*>(a.out)[o + 16 * db] = v;
-          else if (a.out_dtype == IAK_DTYPE_F16) reinterpret_cast<_Float16*>(a.out)[o + 16 * db] = (_Float16)v;
-          else reinterpret_cast<__bf16*>(a.out)[o + 16 * db] = (__bf16)v;
-        }
-      } else {
-        const int64_t slot = ((int64_t)b * a.splits + split) * a.H + h;
-        if (c == 0) {
-          a.ws_m[slot] = sh.mmax[hl];
-          a.ws_l[slot] = sh.lsum[hl];
-        }
-        float* op = a.ws_acc + slot * DV + c;
-#pragma unroll
-        for (int db = 0; db < C::NDB; ++db) op[16 * db] = acc[k][db][r];
+      for (int db = 0; db < C::NDB; ++db) {
+        const float v = acc[db][r] * inv;
+        if (a.out_dtype == IAK_DTYPE_F32) reinterpret_cast<float*>(a.out)[o + 16 * db] = v;
+        else if (a.out_dtype == IAK_DTYPE_F16) reinterpret_cast<_Float16*>(a.out)[o + 16 * db] = (_Float16)v;
+        else reinterpret_cast<__bf16*>(a.out)[o + 16 * db] = (__bf16)v;
       }
+    } else {
+      const int64_t slot = ((int64_t)b * a.splits + split) * a.H + h;
+      if (c == 0) {
+        a.ws_m[slot] = sh.mmax[hl];
+        a.ws_l[slot] = sh.lsum[hl];
+      }
+      float* op = a.ws_acc + slot * DV + c;
+#pragma unroll
+      for (int db = 0; db < C::NDB; ++db) op[16 * db] = acc[db][r];
     }
   }
 }
