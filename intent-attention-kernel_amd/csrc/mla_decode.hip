@@ -53,7 +53,10 @@ template <int DQK, int DV, bool WIDE> struct Mla {
   static constexpr int KSTEPS = DQK / 32;      // score k-steps
   static constexpr int NDB = DV / 16;          // 16-dim value blocks (all of them, per wave)
   static constexpr int TOK = 2 * PS;           // tokens per step: two pages
-  static constexpr int T1 = DQK + 8;           // [token][dim] row stride (halves)
+  // [token][dim] row stride (halves), = 16 mod 128: the 16-byte score-operand
+  // reads of 16 rows and the 8-byte transposing value reads of 16 rows both
+  // spread evenly over the 64 LDS banks
+  static constexpr int T1 = DQK + ((16 - DQK) % 128 + 128) % 128;
   static constexpr int PAGE8 = PS * DQK;       // bytes of a one-byte page (a multiple of 1 KB)
   static constexpr int SLOT = WIDE ? 2 * PAGE8 : PAGE8;   // raw ring slot: the widest page
   static constexpr int NDMA = (SLOT / 1024 + WAVES - 1) / WAVES;   // 1 KB copies per wave per page
