@@ -30,3 +30,80 @@ def test_device_workload_codes_and_decode():
     err = np.abs(out.cpu().numpy() - ref).max()
     print(f"[gpu-case] tiny workload max abs err {err:.2e}", flush=True)
     assert err <= 1e-2
+
+
+def _row_oracle(wl, rows):
+    """Oracle output of the given (batch * kv_head) rows of a bench workload:
+    their pages gathered to the host, everything else as the bench builds it."""
+    cfg = wl["cfg"]
+    B, Hkv, G, D = cfg["B"], cfg["Hkv"], cfg["Hq"] // cfg["Hkv"], cfg["D"]
+    table = wl["table"].reshape(B * Hkv, -1)
+    ids = table[rows].flatten()
+    uniq, inv = torch.unique(ids, return_inverse=True)
+    p = wl["pools"]
+
+    def host(t):
+        return t[uniq.long()].cpu().numpy()
+
+    pools = {"k_fp16": host(p.k_fp16), "v_fp16": host(p.v_fp16)}
+    for nm, src in (("fp8", "fp8"), ("i8", "int8"), ("i4", "int4"), ("i4r", "int4r")):
+        for w in ("k", "v"):
+            if getattr(p, f"{w}_{src}") is not None:
+                pools[f"{w}_{nm}"] = host(getattr(p, f"{w}_{src}"))
+                pools[f"{w}_{nm}_scale"] = host(getattr(p, f"{w}_{src}_scale"))
+    tags = wl["tags"][uniq.long()].cpu().numpy()
+    tbl = inv.reshape(len(rows), 1, -1).cpu().numpy().astype(np.int32)
+    cnt = wl["counts"].reshape(B * Hkv)[rows].reshape(len(rows), 1).cpu().numpy()
+    q = wl["q"].reshape(B, Hkv, G, D).reshape(B * Hkv, G, D)[rows].cpu().numpy()
+    return paged_decode_oracle(q, pools, tbl, cnt, tags, dtype=np.float32)
+
+
+@pytest.mark.parametrize("name,tol", [("cfg2", 2e-3), ("cfg3", 1e-2), ("cfg4", 1e-2)])
+def test_full_config_sampled_rows(name, tol):
+    """The benchmark's own configurations at full size through the same plan the
+    bench times; 6 rows spread over the batch checked against the oracle."""
+    print(f"[gpu-case] full {name} workload, sampled rows", flush=True)
+    from intent_attention.decode_core import make_plan
+    dev = torch.device("cuda:0")
+    wl = bench.build_workload(name, dev)
+    cfg = wl["cfg"]
+    out = torch.empty((cfg["B"], cfg["Hq"], cfg["D"]), dtype=torch.float32, device=dev)
+    make_plan(wl["q"], wl["pools"], wl["table"], wl["counts"], wl["tags"], out=out).run()
+    torch.cuda.synchronize()
+    R = cfg["B"] * cfg["Hkv"]
+    rows = sorted({0, R - 1, *range(R // 6, R, R // 6)})[:6]
+    ref = _row_oracle(wl, rows)
+    G = cfg["Hq"] // cfg["Hkv"]
+    got = out.reshape(R, G, cfg["D"])[rows].cpu().numpy()
+    err = np.abs(got - ref.reshape(got.shape)).max()
+    print(f"[gpu-case] {name} rows {rows} max abs err {err:.2e}", flush=True)
+    assert err <= tol
+    del wl, out
+    torch.cuda.empty_cache()
+
+
+def test_full_mla_config_sampled_sequences():
+    """cfg5 (MLA) at full size through the bench's plan; 3 sequences against the oracle."""
+    print("[gpu-case] full cfg5 MLA workload, sampled sequences", flush=True)
+    from intent_attention.mla_core import make_mla_plan
+    from oracle.mla import mla_paged_decode_oracle
+    dev = torch.device("cuda:0")
+    wl = bench.build_mla_workload("cfg5", dev)
+    cfg = wl["cfg"]
+    out = torch.empty((cfg["B"], cfg["H"], cfg["DV"]), dtype=torch.float32, device=dev)
+    make_mla_plan(wl["q"], wl["pools"], wl["tables"][0], wl["counts"], wl["tags"], v_dim=cfg["DV"], out=out).run()
+    torch.cuda.synchronize()
+    p = wl["pools"]
+    for b in (0, cfg["B"] // 2, cfg["B"] - 1):
+        ids = wl["tables"][0][b].long()
+        uniq, inv = torch.unique(ids, return_inverse=True)
+        pools = {"c_fp8": p.c_fp8[uniq].cpu().numpy(), "c_fp8_scale": p.c_fp8_scale[uniq].cpu().numpy(),
+                 "c_i8": p.c_int8[uniq].cpu().numpy(), "c_i8_scale": p.c_int8_scale[uniq].cpu().numpy()}
+        ref = mla_paged_decode_oracle(wl["q"][b:b + 1].cpu().numpy(), pools,
+                                      inv[None].cpu().numpy().astype(np.int32), np.array([wl["W"]]),
+                                      wl["tags"][uniq].cpu().numpy(), v_dim=cfg["DV"])
+        err = np.abs(out[b].cpu().numpy() - ref[0]).max()
+        print(f"[gpu-case] cfg5 sequence {b} max abs err {err:.2e}", flush=True)
+        assert err <= 1e-2
+    del wl, out
+    torch.cuda.empty_cache()
