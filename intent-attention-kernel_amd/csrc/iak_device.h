@@ -21,6 +21,11 @@ typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 
 constexpr int PS = 16;
 constexpr float RESCALE_SLACK = 8.0f;      // p <= 2^8 between rescales
+// A page whose V scale exceeds this is folded into p only with p <= 1: its
+// softmax step rescales to the page's own maximum whenever that exceeds the
+// running one (no 2^8 head-room), so p * scale stays within f16 range for every
+// f16 source value (|x| <= 65504, INT4 codes <= 8: scale <= 65504 / 7).
+constexpr float P_SCALE_LIMIT = 255.0f;
 constexpr uint32_t MAGIC_I8 = 0x64646464u;  // f16 0x64xx = 1024 + xx
 constexpr uint32_t MAGIC_I4 = 0x64006400u;
 
@@ -59,32 +64,44 @@ __device__ __forceinline__ void fp8x4_to_f16(uint32_t x, uint32_t& lo, uint32_t&
   hi = bits(__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x, 1.0f, true));
 }
 
+// (y & mask) | magic as one v_and_or_b32, with `magic` (MAGIC_I4) in a VGPR
+// from magic_i4(): gfx950's three-operand VALU encoding takes no literal, and
+// the compiler would otherwise split it into v_and_b32 + v_or_b32.
+__device__ __forceinline__ uint32_t and_or(uint32_t y, uint32_t mask, uint32_t magic) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(y), "s"(mask), "v"(magic));
+  return r;
+}
+// MAGIC_I4 in a VGPR the compiler cannot rematerialise as a literal
+__device__ __forceinline__ uint32_t magic_i4() {
+  uint32_t m;
+  asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(m));
+  return m;
+}
 // Nibbles at bits 0-3 and 16-19 of y (code + 8) -> f16 pair of codes, exactly.
-__device__ __forceinline__ h2 nib_pair(uint32_t y) {
-  return as_h2((y & 0x000F000Fu) | MAGIC_I4) + splat2((_Float16)-1032.0f);
+__device__ __forceinline__ h2 nib_pair(uint32_t y, uint32_t magic) {
+  return as_h2(and_or(y, 0x000F000Fu, magic)) + splat2((_Float16)-1032.0f);
+}
+
+// INT4_RESIDUAL bytes (low nibble = base code + 8, high nibble = residual code
+// + 8) at bytes 0 and 2 of y -> the f16 pair of base codes and the f16 pair of
+// 16 x residual codes, both exact integers.
+__device__ __forceinline__ h2 i4r_base_pair(uint32_t y, uint32_t magic) { return nib_pair(y, magic); }
+__device__ __forceinline__ h2 i4r_resid16_pair(uint32_t y, uint32_t magic) {
+  return as_h2(and_or(y, 0x00F000F0u, magic)) + splat2((_Float16)-1152.0f);   // 1024 + 16 * 8
 }
 
 // Eight packed INT4 codes (element j = nibble j) -> four f16 pairs in element
-// order, multiplied by scale s.
-__device__ __forceinline__ void i4x8_to_f16(uint32_t x, h2 s, uint32_t o[4]) {
-  const h2 p04 = nib_pair(x) * s;         // (e0, e4)
-  const h2 p15 = nib_pair(x >> 4) * s;    // (e1, e5)
-  const h2 p26 = nib_pair(x >> 8) * s;    // (e2, e6)
-  const h2 p37 = nib_pair(x >> 12) * s;   // (e3, e7)
+// order, multiplied by scale s (`magic` from magic_i4()).
+__device__ __forceinline__ void i4x8_to_f16(uint32_t x, h2 s, uint32_t magic, uint32_t o[4]) {
+  const h2 p04 = nib_pair(x, magic) * s;         // (e0, e4)
+  const h2 p15 = nib_pair(x >> 4, magic) * s;    // (e1, e5)
+  const h2 p26 = nib_pair(x >> 8, magic) * s;    // (e2, e6)
+  const h2 p37 = nib_pair(x >> 12, magic) * s;   // (e3, e7)
   o[0] = pack_lo(bits(p04), bits(p15));
   o[1] = pack_lo(bits(p26), bits(p37));
   o[2] = pack_hi(bits(p04), bits(p15));
   o[3] = pack_hi(bits(p26), bits(p37));
-}
-
-// Four INT4_RESIDUAL bytes (base | resid<<4) -> two f16 pairs of base*s0 + resid*s1.
-__device__ __forceinline__ void i4r_x4_to_f16(uint32_t x, h2 s0, h2 s1, uint32_t& lo, uint32_t& hi) {
-  const h2 b02 = nib_pair(x), r02 = nib_pair(x >> 4);
-  const h2 b13 = nib_pair(x >> 8), r13 = nib_pair(x >> 12);
-  const h2 v02 = __builtin_elementwise_fma(r02, s1, b02 * s0);
-  const h2 v13 = __builtin_elementwise_fma(r13, s1, b13 * s0);
-  lo = pack_lo(bits(v02), bits(v13));
-  hi = pack_hi(bits(v02), bits(v13));
 }
 
 // Cross-lane reductions over the lanes {l, l^16, l^32, l^48} with the gfx950

@@ -11,29 +11,31 @@
 // Work decomposition
 //   One workgroup of 8 waves (two per SIMD, up to 256 registers each) reduces
 //   one split -- up to 64 consecutive page-table entries of one sequence -- for
-//   128 heads, so each latent page is read from HBM once per sequence. Pages
-//   stream from HBM straight into an LDS ring (global_load_lds), three pages
-//   ahead, and are staged once per workgroup as two f16 tiles: [token][dim]
-//   for the score product and [dim][token] (value dims) for the value product.
-//   FP8 / INT8 codes are converted to f16 exactly while staging; the page
-//   scale folds into the score multiplier and into P.
+//   128 heads, so each latent page is read from HBM once per sequence. A step
+//   is a pair of pages (32 tokens). Pages stream from HBM straight into an LDS
+//   ring of page pairs (global_load_lds), SLOTS - 1 steps ahead, and each pair
+//   is staged once per workgroup into one f16 tile [token][dim]; FP8 / INT8
+//   codes convert to f16 exactly while staging, and the page scale folds into
+//   the score multiplier and into P.
 //   Wave w owns heads 16w .. 16w+15 end to end (its score and value
 //   accumulators live in VGPRs: this file is built with MFMA results in VGPRs,
 //   so the softmax rescale is plain VALU work):
-//     scores  S^T[16 tok x 16 heads] = C[16 tok x DQK] . Q^T on
-//             v_mfma_f32_16x16x32_f16, C from the [token][dim] tile, Q
-//             resident in registers;
-//     softmax online per head in the exp2 domain (max shared by the four lane
-//             groups, lazy rescale with 2^8 head-room as in the paged decode),
-//             entirely inside the wave;
-//     values  O[16 heads x 16 dims] += P[16 heads x 16 tok] . C[16 tok x 16 dims]
-//             on v_mfma_f32_16x16x16f16 for all DV dims: the score result's
-//             register layout (lane: head column, four consecutive tokens) is
-//             exactly the A operand P, so P never leaves the registers; C comes
-//             from the [dim][token] tile.
-//   Two barriers per page (tile ready; tile buffer free). Splits write (m, l,
-//   acc) partials merged by splitk_merge_kernel; a sequence that fits one
-//   split writes the output directly.
+//     scores  S^T[16 tok x 16 heads] = C[16 tok x DQK] . Q^T per page on
+//             v_mfma_f32_16x16x32_f16, C from the tile, Q resident in
+//             registers;
+//     softmax online per head over the pair's 32 tokens in the exp2 domain
+//             (max shared by the four lane groups, lazy rescale with 2^8
+//             head-room as in the paged decode), entirely inside the wave;
+//     values  O[16 heads x 16 dims] += P[16 heads x 32 tok] . C[32 tok x 16 dims]
+//             on v_mfma_f32_16x16x32_f16 for all DV dims: the two score
+//             results' register layout (lane: head column, four consecutive
+//             tokens of each page) is exactly the A operand P, so P never leaves
+//             the registers; the C operand comes out of the same [token][dim]
+//             tile through the transposing read ds_read_b64_tr_b16.
+//   One barrier per pair: pair s+1 is staged into the other tile buffer while
+//   pair s is computed. Splits write (m, l, acc) partials merged by
+//   splitk_merge_kernel; a sequence that fits one split writes the output
+//   directly.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -318,7 +320,9 @@ __global__ __launch_bounds__(512, 1) void mla_decode_kernel(const MArgs a) {
       }
       const float pm = xmax16_32(fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])),
                                        fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3]))));
-      const bool grow = pm > m + RESCALE_SLACK;
+      // V scales above P_SCALE_LIMIT are folded into P only with p <= 1
+      const bool tight = fmaxf(ps0, ps1) > P_SCALE_LIMIT;
+      const bool grow = pm > m + (tight ? 0.0f : RESCALE_SLACK);
       float al = 1.0f;
       if (grow) {
         al = __builtin_amdgcn_exp2f(m - pm);   // 0 on the first pair (m = -inf)
@@ -402,11 +406,11 @@ __global__ __launch_bounds__(512, 1) void mla_decode_kernel(const MArgs a) {
 
 template <int DQK, int DV, bool WIDE>
 hipError_t launch_mla_w(const MArgs& m, hipStream_t stream, hipEvent_t ev_begin, hipEvent_t ev_end) {
-  if (ev_begin) hipEventRecord(ev_begin, stream);
+  if (ev_begin) (void)hipEventRecord(ev_begin, stream);
   hipLaunchKernelGGL((mla_decode_kernel<DQK, DV, WIDE>), dim3(m.B * m.splits, m.HG),
                      dim3(Mla<DQK, DV, WIDE>::THREADS), 0, stream, m);
   hipError_t e = hipGetLastError();
-  if (ev_end) hipEventRecord(ev_end, stream);
+  if (ev_end) (void)hipEventRecord(ev_end, stream);
   if (e != hipSuccess || m.splits == 1) return e;
   // the paged-decode merge over rows (b, 0) of H heads
   KArgs k{};

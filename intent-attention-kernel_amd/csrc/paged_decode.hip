@@ -32,8 +32,9 @@
 //           4g..4g+3 -- exactly the score result layout, converted to f16.
 //           Accumulator: lane holds head c, dims (D/4)g .. (D/4)g + D/4 - 1.
 //   Per-page scalar scales fold into the score multiplier (K) and into p (V);
-//   INT4 group scales and INT4_RESIDUAL values are applied in f16 during
-//   dequantisation.
+//   INT4 group scales are applied in f16 during dequantisation; INT4_RESIDUAL
+//   pages keep their base and residual codes exact and apply the two scales to
+//   the f32 products (page_int4r).
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -144,14 +145,16 @@ __device__ __forceinline__ f4 scores(const Wave<D, QF32>& w, const h8 (&ka)[D / 
 }
 
 // Online-softmax update for one page whose raw scores are `s` (lane: head c,
-// tokens 4g..4g+3); `smul` = softmax scale * log2(e) * K scale; `vmul` = V page
-// scale (1 when V carries its own scale). Returns the P operand (f16).
+// tokens 4g..4g+3); `smul` = softmax scale * log2(e) * K scale. Returns the
+// page's probabilities p (f32, <= 2^8; <= 1 when `tight`, for pages whose V
+// scale exceeds P_SCALE_LIMIT); softmax_step also multiplies them by the V
+// page scale `vmul` (1 when V carries its own scale) into the f16 P operand.
 template <int D, bool QF32>
-__device__ __forceinline__ h4 softmax_step(Wave<D, QF32>& w, f4 s, float smul, float vmul) {
+__device__ __forceinline__ f4 softmax_p(Wave<D, QF32>& w, f4 s, float smul, bool tight = false) {
   s *= smul;
   float pm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
   pm = xmax16_32(pm);
-  const bool grow = pm > w.m + RESCALE_SLACK;
+  const bool grow = pm > w.m + (tight ? 0.0f : RESCALE_SLACK);
   if (__builtin_amdgcn_ballot_w64(grow)) {        // wave-uniform, rare after the first page
     const float mn = grow ? pm : w.m;
     const float alpha = __builtin_amdgcn_exp2f(w.m - mn);   // 0 on the first page (m = -inf)
@@ -160,15 +163,24 @@ __device__ __forceinline__ h4 softmax_step(Wave<D, QF32>& w, f4 s, float smul, f
     for (int mb = 0; mb < D / 16; ++mb) w.acc[mb] *= alpha;
     w.m = mn;
   }
-  float p0 = __builtin_amdgcn_exp2f(s[0] - w.m);
-  float p1 = __builtin_amdgcn_exp2f(s[1] - w.m);
-  float p2 = __builtin_amdgcn_exp2f(s[2] - w.m);
-  float p3 = __builtin_amdgcn_exp2f(s[3] - w.m);
-  w.l += (p0 + p1) + (p2 + p3);
+  f4 p;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f(s[r] - w.m);
+  w.l += (p[0] + p[1]) + (p[2] + p[3]);
+  return p;
+}
+
+// Probabilities times a V scale, as the f16 B operand of the value product.
+__device__ __forceinline__ h4 p_operand(f4 p, float vmul) {
   typedef float f2 __attribute__((ext_vector_type(2)));
-  const h2 a = __builtin_convertvector((f2{p0, p1} * vmul), h2);
-  const h2 b = __builtin_convertvector((f2{p2, p3} * vmul), h2);
+  const h2 a = __builtin_convertvector((f2{p[0], p[1]} * vmul), h2);
+  const h2 b = __builtin_convertvector((f2{p[2], p[3]} * vmul), h2);
   return make_h4(bits(a), bits(b));
+}
+
+template <int D, bool QF32>
+__device__ __forceinline__ h4 softmax_step(Wave<D, QF32>& w, f4 s, float smul, float vmul) {
+  return p_operand(softmax_p(w, s, smul, vmul > P_SCALE_LIMIT), vmul);
 }
 
 // V operand of row block mb from four f16-pair rows vt[t][w] = dims (2w, 2w+1)
@@ -209,19 +221,19 @@ __device__ __forceinline__ void page_fp16(Wave<D, QF32>& w, const Raw16<D>& r, f
   pv_rows(w, r.v, pb);
 }
 
+// FP8 / INT8 page: codes convert to f16 exactly; the K page scale is in
+// `smul`, the V page scale `vmul` multiplies p.
 template <int D, bool QF32, int TAG>
-__device__ __forceinline__ void page_byte(Wave<D, QF32>& w, const Raw8<D>& r, float smul, float vmul,
-                                          h2 ks0, h2 ks1, h2 vs0, h2 vs1) {
+__device__ __forceinline__ void page_byte(Wave<D, QF32>& w, const Raw8<D>& r, float smul, float vmul) {
   h8 ka[D / 32];
 #pragma unroll
   for (int i = 0; i < D / 32; ++i) {
     uint32_t o[4];
     if constexpr (TAG == IAK_TAG_FP8) {
       fp8x4_to_f16(r.k[2 * i], o[0], o[1]); fp8x4_to_f16(r.k[2 * i + 1], o[2], o[3]);
-    } else if constexpr (TAG == IAK_TAG_INT8) {
-      i8x4_to_f16(r.k[2 * i], o[0], o[1]); i8x4_to_f16(r.k[2 * i + 1], o[2], o[3]);
     } else {
-      i4r_x4_to_f16(r.k[2 * i], ks0, ks1, o[0], o[1]); i4r_x4_to_f16(r.k[2 * i + 1], ks0, ks1, o[2], o[3]);
+      static_assert(TAG == IAK_TAG_INT8, "page_byte handles FP8 and INT8 pages");
+      i8x4_to_f16(r.k[2 * i], o[0], o[1]); i8x4_to_f16(r.k[2 * i + 1], o[2], o[3]);
     }
     ka[i] = make_h8(o[0], o[1], o[2], o[3]);
   }
@@ -232,20 +244,79 @@ __device__ __forceinline__ void page_byte(Wave<D, QF32>& w, const Raw8<D>& r, fl
 #pragma unroll
     for (int j = 0; j < D / 64; ++j) {
       if constexpr (TAG == IAK_TAG_FP8) fp8x4_to_f16(r.v[t][j], vt[t][2 * j], vt[t][2 * j + 1]);
-      else if constexpr (TAG == IAK_TAG_INT8) i8x4_to_f16(r.v[t][j], vt[t][2 * j], vt[t][2 * j + 1]);
-      else i4r_x4_to_f16(r.v[t][j], vs0, vs1, vt[t][2 * j], vt[t][2 * j + 1]);
+      else i8x4_to_f16(r.v[t][j], vt[t][2 * j], vt[t][2 * j + 1]);
     }
   }
   pv_rows(w, vt, pb);
 }
 
+// INT4_RESIDUAL page: every value is base * s0 + resid * s1 with two 4-bit
+// codes per byte. Both codes convert to f16 exactly (the residual as 16 x code)
+// and the page scales are applied to the f32 products instead of to every
+// value:
+//   scores  two MFMA chains over the exact codes, s = s0 * (K_base . q) +
+//           (s1 / 16) * (K_resid16 . q);
+//   values  one v_mfma_f32_16x16x32_f16 per row block whose K dimension
+//           stacks the 4 tokens' base codes (k-slots 8g .. 8g+3) and 16 x
+//           residual codes (8g+4 .. 8g+7) of the lane's dim, against
+//           B = (p * vs0, p * vs1 / 16) of the same tokens.
+// `ks0, ks1, vs0, vs1`: K base / residual and V base / residual scales.
+template <int D, bool QF32>
+__device__ __forceinline__ void page_int4r(Wave<D, QF32>& w, const Raw8<D>& r, float smul, float ks0, float ks1,
+                                           float vs0, float vs1) {
+  const uint32_t mg = magic_i4();
+  f4 sb = {0.f, 0.f, 0.f, 0.f}, sr = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < D / 32; ++i) {
+    // dims 8i .. 8i+7 of the lane's K slice: bytes 0-3 of r.k[2i], then of r.k[2i+1]
+    uint32_t b[4], q16[4];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t x = r.k[2 * i + h];
+      const uint32_t y01 = __builtin_amdgcn_perm(x, x, 0x01010000u);   // bytes 0, 1 -> 0, 2
+      const uint32_t y23 = __builtin_amdgcn_perm(x, x, 0x03030202u);   // bytes 2, 3 -> 0, 2
+      b[2 * h] = bits(i4r_base_pair(y01, mg));
+      b[2 * h + 1] = bits(i4r_base_pair(y23, mg));
+      q16[2 * h] = bits(i4r_resid16_pair(y01, mg));
+      q16[2 * h + 1] = bits(i4r_resid16_pair(y23, mg));
+    }
+    const h8 kb = make_h8(b[0], b[1], b[2], b[3]), kr = make_h8(q16[0], q16[1], q16[2], q16[3]);
+    sb = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb, w.qhi[i], sb, 0, 0, 0);
+    sr = __builtin_amdgcn_mfma_f32_16x16x32_f16(kr, w.qhi[i], sr, 0, 0, 0);
+    if constexpr (QF32) {
+      sb = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb, w.qlo[i], sb, 0, 0, 0);
+      sr = __builtin_amdgcn_mfma_f32_16x16x32_f16(kr, w.qlo[i], sr, 0, 0, 0);
+    }
+  }
+  const float kr16 = ks1 * 0.0625f;
+  f4 s;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) s[e] = sb[e] * ks0 + sr[e] * kr16;
+  const float vr16 = vs1 * 0.0625f;
+  const f4 p = softmax_p(w, s, smul, fmaxf(vs0, vr16) > P_SCALE_LIMIT);
+  const h4 pb = p_operand(p, vs0), pr = p_operand(p, vr16);
+  const h8 pop = __builtin_shufflevector(pb, pr, 0, 1, 2, 3, 4, 5, 6, 7);
+  // V: r.v[t][j] holds dims (D/16)c + 4j .. +3 of token 4g+t
+#pragma unroll
+  for (int mb = 0; mb < D / 16; ++mb) {
+    const int j = mb >> 2, k = mb & 3;
+    const uint32_t sel = (uint32_t)k * 0x00000101u + (uint32_t)(4 + k) * 0x01010000u;   // (t_even byte k, t_odd byte k)
+    const uint32_t y01 = __builtin_amdgcn_perm(r.v[1][j], r.v[0][j], sel);
+    const uint32_t y23 = __builtin_amdgcn_perm(r.v[3][j], r.v[2][j], sel);
+    const h8 va = make_h8(bits(i4r_base_pair(y01, mg)), bits(i4r_base_pair(y23, mg)), bits(i4r_resid16_pair(y01, mg)),
+                          bits(i4r_resid16_pair(y23, mg)));
+    w.acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pop, w.acc[mb], 0, 0, 0);
+  }
+}
+
 template <int D, bool QF32>
 __device__ __forceinline__ void page_int4(Wave<D, QF32>& w, const Raw4<D>& r, float smul, h2 ks, h2 vs) {
+  const uint32_t mg = magic_i4();
   h8 ka[D / 32];
 #pragma unroll
   for (int i = 0; i < D / 32; ++i) {
     uint32_t o[4];
-    i4x8_to_f16(r.k[i], ks, o);
+    i4x8_to_f16(r.k[i], ks, mg, o);
     ka[i] = make_h8(o[0], o[1], o[2], o[3]);
   }
   const h4 pb = softmax_step(w, scores(w, ka), smul, 1.0f);
@@ -259,13 +330,13 @@ __device__ __forceinline__ void page_int4(Wave<D, QF32>& w, const Raw4<D>& r, fl
     for (int d = 0; d < 8; ++d) {
       const uint32_t y01 = d < 4 ? y01l : y01h, y23 = d < 4 ? y23l : y23h;
       const int sh = 4 * (d & 3);
-      va[d] = make_h4(bits(nib_pair(y01 >> sh) * vs), bits(nib_pair(y23 >> sh) * vs));
+      va[d] = make_h4(bits(nib_pair(y01 >> sh, mg) * vs), bits(nib_pair(y23 >> sh, mg) * vs));
     }
   } else {   // D == 64: two bytes (4 dims) per token
     const uint32_t y01 = pack_lo(r.v[0], r.v[1]), y23 = pack_lo(r.v[2], r.v[3]);
 #pragma unroll
     for (int d = 0; d < 4; ++d)
-      va[d] = make_h4(bits(nib_pair(y01 >> (4 * d)) * vs), bits(nib_pair(y23 >> (4 * d)) * vs));
+      va[d] = make_h4(bits(nib_pair(y01 >> (4 * d), mg) * vs), bits(nib_pair(y23 >> (4 * d), mg) * vs));
   }
   pv(w, va, pb);
 }
@@ -544,7 +615,7 @@ void paged_decode_kernel(const KArgs a) {
         [&](Raw8<D>& r, int p) { load8<D>(r, kp + (int64_t)p * PS * D, vp + (int64_t)p * PS * D, c, g); },
         [&](const Raw8<D>& r, int idx) {
           const Scales s = read_scales(slot, idx);
-          page_byte<D, QF32, IAK_TAG_FP8>(w, r, smul * u2f(s.s[0]), u2f(s.s[1]), one, one, one, one);
+          page_byte<D, QF32, IAK_TAG_FP8>(w, r, smul * u2f(s.s[0]), u2f(s.s[1]));
         });
   }
   {
@@ -555,7 +626,7 @@ void paged_decode_kernel(const KArgs a) {
         [&](Raw8<D>& r, int p) { load8<D>(r, kp + (int64_t)p * PS * D, vp + (int64_t)p * PS * D, c, g); },
         [&](const Raw8<D>& r, int idx) {
           const Scales s = read_scales(slot, idx);
-          page_byte<D, QF32, IAK_TAG_INT8>(w, r, smul * u2f(s.s[0]), u2f(s.s[1]), one, one, one, one);
+          page_byte<D, QF32, IAK_TAG_INT8>(w, r, smul * u2f(s.s[0]), u2f(s.s[1]));
         });
   }
   {
@@ -566,9 +637,7 @@ void paged_decode_kernel(const KArgs a) {
         [&](Raw8<D>& r, int p) { load8<D>(r, kp + (int64_t)p * PS * D, vp + (int64_t)p * PS * D, c, g); },
         [&](const Raw8<D>& r, int idx) {
           const Scales s = read_scales(slot, idx);
-          page_byte<D, QF32, IAK_TAG_INT4_RESIDUAL>(
-              w, r, smul, 1.0f, splat2((_Float16)u2f(s.s[0])), splat2((_Float16)u2f(s.s[1])),
-              splat2((_Float16)u2f(s.s[2])), splat2((_Float16)u2f(s.s[3])));
+          page_int4r(w, r, smul, u2f(s.s[0]), u2f(s.s[1]), u2f(s.s[2]), u2f(s.s[3]));
         });
   }
   // ---- INT4 pages: lane K dims (D/4)g.. lie in group kg, V dims (D/16)c.. in group vg ----
@@ -594,11 +663,11 @@ void paged_decode_kernel(const KArgs a) {
 template <int D, int QT>
 hipError_t launch_decode(const KArgs& k, hipStream_t stream, hipEvent_t ev_begin, hipEvent_t ev_end) {
   const int blocks = (k.items + IAK_WAVES_PER_BLOCK - 1) / IAK_WAVES_PER_BLOCK;
-  if (ev_begin) hipEventRecord(ev_begin, stream);
+  if (ev_begin) (void)hipEventRecord(ev_begin, stream);
   hipLaunchKernelGGL((paged_decode_kernel<D, QT>), dim3(blocks), dim3(64 * IAK_WAVES_PER_BLOCK), 0,
                      stream, k);
   hipError_t e = hipGetLastError();
-  if (ev_end) hipEventRecord(ev_end, stream);
+  if (ev_end) (void)hipEventRecord(ev_end, stream);
   if (e != hipSuccess || k.splits == 1) return e;
   const int mblocks = (k.B * k.Hq + 3) / 4;
   hipLaunchKernelGGL((splitk_merge_kernel<D>), dim3(mblocks), dim3(256), 0, stream, k);

@@ -17,11 +17,12 @@ TAGS = {"FP16": Dm.FP16, "INT8": Dm.INT8, "SKIP": Dm.SKIP, "FP8": Dm.FP8, "INT4"
 
 
 def build_pools(rng: np.random.Generator, num_pages: int, D: int, tags: np.ndarray, *,
-                outliers: float = 0.0, int4_group: int = 32, scale_f32: bool = False):
-    """numpy pools dict in the layout ``oracle.decode.dequant_page`` reads."""
+                outliers: float = 0.0, int4_group: int = 32, scale_f32: bool = False, v_scale: float = 1.0):
+    """numpy pools dict in the layout ``oracle.decode.dequant_page`` reads
+    (V values N(0, v_scale^2), rounded to float16)."""
     PS = 16
     k = rng.standard_normal((num_pages, PS, D)).astype(np.float16)
-    v = rng.standard_normal((num_pages, PS, D)).astype(np.float16)
+    v = (rng.standard_normal((num_pages, PS, D)) * v_scale).astype(np.float16)
     if outliers > 0:
         m = rng.random(k.shape) < outliers
         k = np.where(m, (8.0 * np.sign(k.astype(np.float32))).astype(np.float16), k)
@@ -77,13 +78,13 @@ def to_device_pools(pools, device, int4_group: int = 32):
 
 
 def random_case(seed: int, B: int, Hq: int, Hkv: int, D: int, NP: int, W: int, mix=None, *,
-                outliers: float = 0.0, q_scale: float = 1.0, scale_f32: bool = False):
+                outliers: float = 0.0, q_scale: float = 1.0, scale_f32: bool = False, v_scale: float = 1.0):
     """(q, pools, table, counts, tags) with a seeded mixed-precision setup."""
     rng = np.random.default_rng(seed)
     names = list(mix or {"FP16": 1.0})
     probs = np.array([mix[n] for n in names] if mix else [1.0])
     tags = np.array([TAGS[n] for n in rng.choice(names, size=NP, p=probs / probs.sum())], np.int32)
-    pools = build_pools(rng, NP, D, tags, outliers=outliers, scale_f32=scale_f32)
+    pools = build_pools(rng, NP, D, tags, outliers=outliers, scale_f32=scale_f32, v_scale=v_scale)
     table = rng.integers(0, NP, size=(B, Hkv, W)).astype(np.int32)
     counts = rng.integers(0, W + 1, size=(B, Hkv)).astype(np.int32)
     counts.flat[0] = W

@@ -120,6 +120,25 @@ def test_q_and_out_dtypes(dev, qdt, odt):
     assert np.abs(out.float().cpu().numpy() - ref).max() <= tol
 
 
+@pytest.mark.parametrize("pps", [0, 16])
+def test_large_value_magnitudes(dev, pps):
+    """V values N(0, 9000^2) (|v| up to ~4e4, inside float16): V page scales
+    exceed what p (up to 2^8 between lazy rescales) times the scale can hold
+    in float16, so those pages take the softmax step with p <= 1. The output
+    matches the oracle to the same relative bar as unit-scale values, with no
+    inf or nan; K stays unit-scale, with outliers to move the running max."""
+    vs = 9000.0
+    _say("large V magnitudes", f"v_scale={vs} pages_per_split={pps}")
+    q, pools, table, counts, tags = random_case(
+        61, 2, 8, 2, 128, 64, 48, {"FP16": .2, "FP8": .2, "INT8": .3, "INT4_RESIDUAL": .3},
+        outliers=0.02, v_scale=vs)
+    got = _run(dev, q, pools, table, counts, tags, pages_per_split=pps)
+    assert np.all(np.isfinite(got))
+    ref = Dm.paged_decode_oracle(q, pools, table, counts, tags)
+    err = np.abs(got - ref).max() / vs
+    assert err <= TOL_QUANT, f"max abs err / v_scale {err:.3e}"
+
+
 def test_invalid_ids_and_clamped_counts(dev):
     import torch
     _say("invalid ids / clamped counts")

@@ -31,13 +31,13 @@ def dev():
     return torch.device("cuda:0")
 
 
-def _latent_case(seed, B, H, DQK, NP, W, mix, scale_f32=False):
+def _latent_case(seed, B, H, DQK, NP, W, mix, scale_f32=False, lat_scale=1.0, q_scale=1.0):
     rng = np.random.default_rng(seed)
     names = list(mix)
     probs = np.array([mix[n] for n in names], float)
     code = {"FP16": Dm.FP16, "FP8": Dm.FP8, "INT8": Dm.INT8, "SKIP": Dm.SKIP}
     tags = np.array([code[n] for n in rng.choice(names, size=NP, p=probs / probs.sum())], np.int32)
-    lat = rng.standard_normal((NP, 16, DQK)).astype(np.float16)
+    lat = (rng.standard_normal((NP, 16, DQK)) * lat_scale).astype(np.float16)
     sdt = np.float32 if scale_f32 else np.float16
     pools = {"c_fp16": lat, "c_fp8": np.zeros((NP, 16, DQK), np.uint8), "c_fp8_scale": np.zeros(NP, sdt),
              "c_i8": np.zeros((NP, 16, DQK), np.int8), "c_i8_scale": np.zeros(NP, sdt)}
@@ -51,7 +51,7 @@ def _latent_case(seed, B, H, DQK, NP, W, mix, scale_f32=False):
     table = rng.integers(0, NP, size=(B, W)).astype(np.int32)
     counts = rng.integers(1, W + 1, size=B).astype(np.int32)
     counts[0] = W
-    q = rng.standard_normal((B, H, DQK)).astype(np.float16)
+    q = (rng.standard_normal((B, H, DQK)) * q_scale).astype(np.float16)
     return q, pools, table, counts, tags
 
 
@@ -105,6 +105,29 @@ def test_mla_fp16_pages_and_f32_scales(dev):
     torch.cuda.synchronize()
     ref = M.mla_paged_decode_oracle(q, pools, table, counts, tags, v_dim=512)
     assert np.abs(got.cpu().numpy() - ref).max() <= 1e-2
+
+
+def test_mla_large_latent_magnitudes(dev):
+    """Latent values N(0, 9000^2) (|c| up to ~4e4, inside float16) with queries
+    scaled by 1/9000: INT8 page scales exceed what p (up to 2^8 between lazy
+    rescales) times the scale can hold in float16, so those pairs take the
+    softmax step with p <= 1. Same relative bar as unit-scale latents, no inf
+    or nan."""
+    import torch
+    from intent_attention import mla_paged_decode
+    ls = 9000.0
+    _say("mla large latent magnitudes", f"lat_scale={ls}")
+    q, pools, table, counts, tags = _latent_case(7, 2, 128, 576, 64, 80, {"FP16": .2, "FP8": .3, "INT8": .5},
+                                                 lat_scale=ls, q_scale=1.0 / ls)
+    got = mla_paged_decode(torch.from_numpy(q).to(dev), _device_pools(pools, dev), torch.from_numpy(table).to(dev),
+                           torch.from_numpy(counts).to(dev), torch.from_numpy(tags).to(dev), v_dim=512,
+                           out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    got = got.cpu().numpy()
+    assert np.all(np.isfinite(got))
+    ref = M.mla_paged_decode_oracle(q, pools, table, counts, tags, v_dim=512)
+    err = np.abs(got - ref).max() / ls
+    assert err <= 1e-2, f"max abs err / lat_scale {err:.3e}"
 
 
 def test_mla_empty_rows_are_zero(dev):
