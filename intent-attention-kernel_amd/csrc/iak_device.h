@@ -159,38 +159,52 @@ __device__ __forceinline__ float u2f(uint32_t x) { return __builtin_bit_cast(flo
 __device__ __forceinline__ uint32_t f2u(float x) { return __builtin_bit_cast(uint32_t, x); }
 
 // --------------------------------------------------------------------------- //
-// Cross-split merge: one wave per (batch, query head). Partial slot of split s
-// of head c in row (b, hk): ((b * Hkv + hk) * splits + s) * G + c.
+// Cross-split merge. Partial slot of split s of head c in row (b, hk):
+// ((b * Hkv + hk) * splits + s) * G + c. WPR waves (1, 2 or 4) share one
+// (batch, query head): wave part p takes the splits s = p (mod WPR), eight at a
+// time with their loads issued together; the parts agree on the global max
+// and add their sums through LDS. A 256-thread block holds 4 / WPR heads.
 // --------------------------------------------------------------------------- //
 
-template <int D>
+template <int D, int WPR>
 __global__ __launch_bounds__(256) void splitk_merge_kernel(const KArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int bh = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (bh >= a.B * a.Hq) return;
-  const int b = bh / a.Hq, h = bh - b * a.Hq;
+  static_assert(WPR == 1 || WPR == 2 || WPR == 4, "1, 2 or 4 waves per head");
+  constexpr int PER = D / 64;   // dims per lane
+  __shared__ float part_m[4], part_l[4];
+  __shared__ float part_o[WPR > 1 ? 4 : 1][WPR > 1 ? D : 1];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int p = w % WPR;                       // this wave's part of its head
+  const int bh = blockIdx.x * (4 / WPR) + w / WPR;
+  const bool live = bh < a.B * a.Hq;           // uniform per wave; no early return (barriers below)
+  const int b = live ? bh / a.Hq : 0, h = live ? bh - b * a.Hq : 0;
   const int hk = h / a.G, c = h - hk * a.G;
-  const int S = a.splits;
-  const int64_t first = (((int64_t)b * a.Hkv + hk) * S) * a.G + c;   // slot of split 0
-  // global max over the splits: lanes read splits in parallel, then reduce
+  const int S = live ? a.splits : 0;
+  const int64_t first = (((int64_t)b * a.Hkv + hk) * a.splits) * a.G + c;   // slot of split 0
+  // max over the part's splits, then over the parts
   float M = -__builtin_inff();
-  for (int s = lane; s < S; s += 64) M = fmaxf(M, a.ws_m[first + (int64_t)s * a.G]);
+  for (int s = p + WPR * lane; s < S; s += WPR * 64) M = fmaxf(M, a.ws_m[first + (int64_t)s * a.G]);
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
-  constexpr int PER = D / 64;   // dims per lane
+  if constexpr (WPR > 1) {
+    if (lane == 0) part_m[w] = M;
+    __syncthreads();
+    const int w0 = w - p;
+#pragma unroll
+    for (int k = 0; k < WPR; ++k) M = fmaxf(M, part_m[w0 + k]);
+  }
   float o[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) o[j] = 0.f;
   float L = 0.f;
   if (M > -__builtin_inff()) {
-    // eight splits per step with their loads issued together
     constexpr int U = 8;
-    int s = 0;
-    for (; s < S; s += U) {
+    const int n = S > p ? (S - p + WPR - 1) / WPR : 0;   // splits of this part
+    for (int i = 0; i < n; i += U) {
       float ms[U], ls[U], av[U][PER];
 #pragma unroll
       for (int k = 0; k < U; ++k) {
-        const int64_t slot = first + (int64_t)(s + k < S ? s + k : S - 1) * a.G;
+        const int s = p + WPR * (i + k < n ? i + k : n - 1);
+        const int64_t slot = first + (int64_t)s * a.G;
         ms[k] = a.ws_m[slot];
         ls[k] = a.ws_l[slot];
         const float* ap = a.ws_acc + slot * D + PER * lane;
@@ -199,14 +213,28 @@ __global__ __launch_bounds__(256) void splitk_merge_kernel(const KArgs a) {
       }
 #pragma unroll
       for (int k = 0; k < U; ++k) {
-        // 0 for empty splits (m = -inf) and for the clamped reloads past S
-        const float wgt = s + k < S ? __builtin_amdgcn_exp2f(ms[k] - M) : 0.f;
+        // 0 for empty splits (m = -inf) and for the clamped reloads past the part's end
+        const float wgt = i + k < n ? __builtin_amdgcn_exp2f(ms[k] - M) : 0.f;
         L += wgt * ls[k];
 #pragma unroll
         for (int j = 0; j < PER; ++j) o[j] += wgt * av[k][j];
       }
     }
   }
+  if constexpr (WPR > 1) {
+    if (lane == 0) part_l[w] = L;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) part_o[w][PER * lane + j] = o[j];
+    __syncthreads();
+    if (p != 0) return;
+#pragma unroll
+    for (int k = 1; k < WPR; ++k) {
+      L += part_l[w + k];
+#pragma unroll
+      for (int j = 0; j < PER; ++j) o[j] += part_o[w + k][PER * lane + j];
+    }
+  }
+  if (!live) return;
   const float inv = L > 0.f ? 1.0f / L : 0.f;
   const int64_t base = (int64_t)b * a.osb + (int64_t)h * a.osh + PER * lane;
 #pragma unroll
@@ -216,6 +244,17 @@ __global__ __launch_bounds__(256) void splitk_merge_kernel(const KArgs a) {
     else if (a.out_dtype == IAK_DTYPE_F16) reinterpret_cast<_Float16*>(a.out)[base + j] = (_Float16)v;
     else reinterpret_cast<__bf16*>(a.out)[base + j] = (__bf16)v;
   }
+}
+
+// Merge launch: more waves per head when each has many splits to read.
+template <int D> hipError_t launch_merge(const KArgs& k, hipStream_t stream) {
+  const int heads = k.B * k.Hq;
+  const int wpr = k.splits >= 24 ? 4 : (k.splits >= 12 ? 2 : 1);
+  const int blocks = (heads * wpr + 3) / 4;
+  if (wpr == 4) hipLaunchKernelGGL((splitk_merge_kernel<D, 4>), dim3(blocks), dim3(256), 0, stream, k);
+  else if (wpr == 2) hipLaunchKernelGGL((splitk_merge_kernel<D, 2>), dim3(blocks), dim3(256), 0, stream, k);
+  else hipLaunchKernelGGL((splitk_merge_kernel<D, 1>), dim3(blocks), dim3(256), 0, stream, k);
+  return hipGetLastError();
 }
 
 }  // namespace iak

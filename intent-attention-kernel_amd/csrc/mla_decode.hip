@@ -417,9 +417,7 @@ hipError_t launch_mla_w(const MArgs& m, hipStream_t stream, hipEvent_t ev_begin,
   k.B = m.B; k.Hq = m.H; k.Hkv = 1; k.G = m.H; k.D = DV; k.splits = m.splits;
   k.out = m.out; k.out_dtype = m.out_dtype; k.osb = m.osb; k.osh = m.osh;
   k.ws_m = m.ws_m; k.ws_l = m.ws_l; k.ws_acc = m.ws_acc;
-  const int mblocks = (m.B * m.H + 3) / 4;
-  hipLaunchKernelGGL((splitk_merge_kernel<DV>), dim3(mblocks), dim3(256), 0, stream, k);
-  return hipGetLastError();
+  return launch_merge<DV>(k, stream);
 }
 
 // WIDE: FP16 latent pages are reachable (ring slots sized for two bytes per value)

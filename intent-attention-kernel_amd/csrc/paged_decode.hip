@@ -669,9 +669,7 @@ hipError_t launch_decode(const KArgs& k, hipStream_t stream, hipEvent_t ev_begin
   hipError_t e = hipGetLastError();
   if (ev_end) (void)hipEventRecord(ev_end, stream);
   if (e != hipSuccess || k.splits == 1) return e;
-  const int mblocks = (k.B * k.Hq + 3) / 4;
-  hipLaunchKernelGGL((splitk_merge_kernel<D>), dim3(mblocks), dim3(256), 0, stream, k);
-  return hipGetLastError();
+  return launch_merge<D>(k, stream);
 }
 
 template <int D>
