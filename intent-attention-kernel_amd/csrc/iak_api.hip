@@ -409,6 +409,12 @@ iak_status iak_build_page_tables(const iak_page_table_args* a, void* stream) {
     if (!a->page_counts || (a->table_width > 0 && !a->page_table))
       return fail(IAK_EINVAL, "page_table / page_counts is NULL");
   }
+  {
+    const void* arrays[] = {a->span_offsets, a->span_begin, a->span_end,  a->span_tag,
+                            a->block_table,  a->page_table, a->page_counts, a->page_precision};
+    for (const void* p : arrays)
+      if (reinterpret_cast<uintptr_t>(p) & 3u) return fail(IAK_EINVAL, "int32 arrays must be 4-byte aligned");
+  }
   const hipError_t e = iak::launch_page_tables(*a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(IAK_EHIP, "kernel launch failed: %s", hipGetErrorString(e));
   return IAK_OK;

@@ -36,6 +36,8 @@
 
 namespace iak {
 
+typedef int32_t i4 __attribute__((ext_vector_type(4)));
+
 constexpr int PT_THREADS = 256;
 constexpr int PT_OWNER = 16384;   // page ids one list may span for the LDS first-seen map (64 KB)
 constexpr int PT_PER = 8;         // consecutive pairs per thread in the emit pass
@@ -236,21 +238,49 @@ __global__ __launch_bounds__(PT_THREADS) void page_tables_kernel(const iak_page_
   for (int64_t e = cnt + tid; e < W; e += PT_THREADS) table[e] = 0;
 }
 
+// The precision passes touch every page once: 16-byte accesses over the
+// 16-byte-aligned body of the array, single words for the (at most three)
+// elements before it and after it.
+struct I32Span {
+  int32_t* p;
+  int64_t n, head, body;   // head: words before the first 16-byte boundary; body: int4 count
+};
+__device__ __forceinline__ I32Span i32_span(int32_t* p, int64_t n) {
+  I32Span s{p, n, 0, 0};
+  const int64_t mis = (int64_t)(((16u - ((uint32_t)(uintptr_t)p & 15u)) & 15u) >> 2);
+  s.head = mis < n ? mis : n;
+  s.body = (n - s.head) >> 2;
+  return s;
+}
+
+template <typename F> __device__ __forceinline__ void for_each_i32(int32_t* p, int64_t n, F f) {
+  const I32Span s = i32_span(p, n);
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t t0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  i4* body = reinterpret_cast<i4*>(p + s.head);
+  for (int64_t i = t0; i < s.body; i += stride) {
+    i4 v = body[i];
+    v[0] = f(v[0]); v[1] = f(v[1]); v[2] = f(v[2]); v[3] = f(v[3]);
+    body[i] = v;
+  }
+  // the words outside the body: head and tail, at most 6
+  const int64_t tail0 = s.head + 4 * s.body;
+  if (t0 < s.head) p[t0] = f(p[t0]);
+  if (t0 < n - tail0) p[tail0 + t0] = f(p[tail0 + t0]);
+}
+
 __global__ __launch_bounds__(256) void fill_i32_kernel(int32_t* p, int64_t n, int32_t v) {
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
-    p[i] = v;
+  for_each_i32(p, n, [v](int32_t) { return v; });
 }
 
 __global__ __launch_bounds__(256) void precision_keys_to_tags_kernel(int32_t* p, int64_t n, int32_t dflt) {
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-    const int32_t v = p[i];
-    p[i] = v == INT_MAX ? dflt : (v & 7);
-  }
+  for_each_i32(p, n, [dflt](int32_t x) { return x == INT_MAX ? dflt : (x & 7); });
 }
 
 hipError_t launch_page_tables(const iak_page_table_args& a, hipStream_t stream) {
   const int64_t np = a.page_precision ? a.num_pages : 0;
-  const int fill_blocks = (int)((np + 255) / 256 < 4096 ? (np + 255) / 256 : 4096);
+  const int64_t vec = (np + 3) / 4;   // 16-byte groups, one per thread
+  const int fill_blocks = (int)((vec + 255) / 256 < 4096 ? (vec + 255) / 256 : 4096);
   if (np > 0) hipLaunchKernelGGL(fill_i32_kernel, dim3(fill_blocks), dim3(256), 0, stream, a.page_precision, np,
                                  (int32_t)INT_MAX);
   if (a.num_rows > 0)

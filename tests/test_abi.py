@@ -157,3 +157,6 @@ def test_page_table_validation_errors_without_gpu():
     a.num_rows, a.page_precision = 1 << 28, 16
     with pytest.raises(ValueError, match="2\\^28"):
         N.build_page_tables(a, 0)
+    a.num_rows, a.page_table, a.page_counts, a.page_precision = 4, 32, 64, 18   # precision 2 bytes off
+    with pytest.raises(ValueError, match="4-byte aligned"):
+        N.build_page_tables(a, 0)

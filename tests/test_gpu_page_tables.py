@@ -130,6 +130,39 @@ def test_many_spans_and_wide_lists(dev):
     _check(dev, rows, 8, 64, 7, 500, rows_per_seq=8, rows_per_list=1)
 
 
+@pytest.mark.parametrize("lead", [0, 1, 2, 3])
+def test_precision_array_unaligned_and_odd_length(dev, lead):
+    """The precision passes use 16-byte accesses on the 16-byte-aligned body of
+    the array and single words around it: an array starting `lead` words past a
+    16-byte boundary with 1003 pages is written exactly and its neighbours are
+    left alone (through the C ABI, which takes any 4-byte-aligned pointer)."""
+    import torch
+    from intent_attention import _native as N
+    _say("page tables: precision array offset", lead)
+    rng = np.random.default_rng(9 + lead)
+    R, W, ps, NP = 3, 500, 16, 1003
+    lists = [_random_spans(rng, 40, NP * ps, 200)]
+    want = P.build_page_tables_oracle(lists, R, W, ps, NP)
+    offs, b, e, t = _flatten(lists)
+    i32 = lambda x: torch.tensor(x, dtype=torch.int32, device=dev)  # noqa: E731
+    spans = [i32(x) for x in (offs, b, e, t)]
+    table = torch.empty((R, W), dtype=torch.int32, device=dev)
+    counts = torch.empty(R, dtype=torch.int32, device=dev)
+    buf = torch.full((NP + 8,), -77, dtype=torch.int32, device=dev)
+    prec = buf[lead:lead + NP]
+    a = N.PageTableArgs()
+    a.num_rows, a.rows_per_seq, a.rows_per_list = R, 1, R
+    a.table_width, a.page_size, a.num_pages, a.dedupe, a.default_tag = W, ps, NP, 1, 0
+    a.span_offsets, a.span_begin, a.span_end, a.span_tag = (x.data_ptr() for x in spans)
+    a.page_table, a.page_counts, a.page_precision = table.data_ptr(), counts.data_ptr(), prec.data_ptr()
+    N.build_page_tables(a, torch.cuda.current_stream(dev).cuda_stream)
+    torch.cuda.synchronize()
+    got = buf.cpu().numpy()
+    assert np.array_equal(got[lead:lead + NP], want[1])
+    assert np.all(got[:lead] == -77) and np.all(got[lead + NP:] == -77)
+    assert np.array_equal(_np(table), want[0]) and np.array_equal(_np(counts), want[2])
+
+
 def test_empty_inputs(dev):
     import torch
     from intent_attention import build_page_tables
