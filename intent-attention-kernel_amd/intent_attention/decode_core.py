@@ -160,7 +160,8 @@ def make_plan(q: torch.Tensor, pools: PagePools, page_table: torch.Tensor, page_
         raise ValueError(f"q dtype {q.dtype} not supported")
     qvec = 4 if q.dtype == torch.float32 else 8
     if q.stride(-1) != 1 or q.data_ptr() % 16 or q.stride(0) % qvec or q.stride(1) % qvec:
-        q = q.contiguous()   # the kernel reads q rows as 16-byte vectors
+        # the kernel reads q rows as 16-byte vectors: a fresh (aligned) copy
+        q = torch.empty(q.shape, dtype=q.dtype, device=q.device).copy_(q)
 
     f16, u8, i8 = (torch.float16,), (torch.uint8,), (torch.int8,)
     _check_pool("k_fp16", pools.k_fp16, NP, (PAGE_SIZE, D), f16)
@@ -178,7 +179,9 @@ def make_plan(q: torch.Tensor, pools: PagePools, page_table: torch.Tensor, page_
         t = getattr(pools, n)
         if t is not None and (t.dtype not in sc or t.numel() != NP):
             raise ValueError(f"{n} must be [{NP}] float16/float32, got {tuple(t.shape)} {t.dtype}")
-    grp = pools.int4_group
+    grp = int(pools.int4_group)
+    if grp <= 0 or D % grp:
+        raise ValueError(f"int4_group must be a positive divisor of head_dim {D}, got {grp}")
     for n in ("k_int4_scale", "v_int4_scale"):
         t = getattr(pools, n)
         if t is not None and (t.dtype not in sc or t.numel() != NP * (D // grp)):
@@ -194,7 +197,7 @@ def make_plan(q: torch.Tensor, pools: PagePools, page_table: torch.Tensor, page_
     if out is None:
         out = torch.empty((B, Hq, D), dtype=out_dtype or q.dtype, device=dev)
     else:
-        if tuple(out.shape[-3:]) != (B, Hq, D) or out.dtype not in _DT or out.stride(-1) != 1:
+        if tuple(out.shape) != (B, Hq, D) or out.dtype not in _DT or out.stride(-1) != 1:
             raise ValueError(f"out must be [B, H, D] with unit last stride, got {tuple(out.shape)}")
 
     a = N.PagedDecodeArgs()

@@ -27,7 +27,7 @@ LATENT_TAG_MAP = (N.TAG_FP16, N.TAG_INT8, N.TAG_SKIP, N.TAG_FP8, N.TAG_SKIP, N.T
 @dataclass
 class LatentPools:
     """Latent page pools indexed by physical page id, [NP, 16, qk_dim]:
-    ``c_fp16`` float16 values; ``c_fp8`` uint8 e4m3fn codes and ``c_int8`` int8
+    ``c_fp16`` float16 values; ``c_fp8`` e4m3fn codes (uint8 or float8_e4m3fn) and ``c_int8`` int8
     codes, each with one scale per page (``c_fp8_scale`` / ``c_int8_scale``
     [NP], both float16 or both float32). Dequantised value = code * scale."""
 
@@ -85,8 +85,10 @@ def make_mla_plan(q: torch.Tensor, pools: LatentPools, page_table: torch.Tensor,
         raise ValueError(f"(qk_dim, v_dim) = ({DQK}, {v_dim}) is not one of {SUPPORTED_SHAPES}")
     if q.dtype not in _DT:
         raise ValueError(f"q dtype {q.dtype} is not float16 / float32 / bfloat16")
-    if q.stride(-1) != 1 or q.data_ptr() % 16 or q.stride(0) % 8 or q.stride(1) % 8:
-        q = q.contiguous()
+    qvec = 4 if q.dtype == torch.float32 else 8
+    if q.stride(-1) != 1 or q.data_ptr() % 16 or q.stride(0) % qvec or q.stride(1) % qvec:
+        # the kernel reads q rows as 16-byte vectors: a fresh (aligned) copy
+        q = torch.empty(q.shape, dtype=q.dtype, device=q.device).copy_(q)
     if page_table.dim() != 2 or page_table.shape[0] != B or page_table.dtype != torch.int32:
         raise ValueError(f"page_table must be int32 [batch, W], got {page_table.dtype} {tuple(page_table.shape)}")
     if page_counts.shape != (B,) or page_counts.dtype != torch.int32:
@@ -98,7 +100,7 @@ def make_mla_plan(q: torch.Tensor, pools: LatentPools, page_table: torch.Tensor,
         raise ValueError("no latent pool given")
     NP = next(iter(present.values())).shape[0]
     _check_pool("c_fp16", pools.c_fp16, NP, (PAGE_SIZE, DQK), (torch.float16,))
-    _check_pool("c_fp8", pools.c_fp8, NP, (PAGE_SIZE, DQK), (torch.uint8,))
+    _check_pool("c_fp8", pools.c_fp8, NP, (PAGE_SIZE, DQK), (torch.uint8, torch.float8_e4m3fn))
     _check_pool("c_int8", pools.c_int8, NP, (PAGE_SIZE, DQK), (torch.int8,))
     _check_pool("c_fp8_scale", pools.c_fp8_scale, NP, (), (torch.float16, torch.float32))
     _check_pool("c_int8_scale", pools.c_int8_scale, NP, (), (torch.float16, torch.float32))

@@ -139,6 +139,27 @@ def test_large_value_magnitudes(dev, pps):
     assert err <= TOL_QUANT, f"max abs err / v_scale {err:.3e}"
 
 
+def test_misaligned_query_view(dev):
+    """A query view 2 bytes past an aligned address (the kernel reads 16-byte
+    query vectors) is copied to an aligned buffer by the host layer; the
+    result equals the aligned query's."""
+    import torch
+    from intent_attention import paged_decode
+    _say("misaligned q view")
+    q, pools, table, counts, tags = random_case(71, 2, 8, 2, 128, 40, 30, {"FP16": .5, "INT8": .5})
+    dp = to_device_pools(pools, dev)
+    tt, ct, gt = (torch.from_numpy(x).to(dev) for x in (table, counts, tags))
+    base = torch.from_numpy(q).to(dev)
+    buf = torch.zeros(q.size + 8, dtype=torch.float16, device=dev)
+    view = buf[1:1 + q.size].view(q.shape)
+    view.copy_(base)
+    assert view.data_ptr() % 16 != 0
+    want = paged_decode(base, dp, tt, ct, gt)
+    got = paged_decode(view, dp, tt, ct, gt)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
 def test_invalid_ids_and_clamped_counts(dev):
     import torch
     _say("invalid ids / clamped counts")

@@ -130,6 +130,28 @@ def test_mla_large_latent_magnitudes(dev):
     assert err <= 1e-2, f"max abs err / lat_scale {err:.3e}"
 
 
+def test_mla_misaligned_query_and_fp8_dtype(dev):
+    """A query view 2 bytes past an aligned address, and the FP8 latent pool
+    given as torch.float8_e4m3fn instead of uint8 codes: same result."""
+    import torch
+    from intent_attention import mla_paged_decode, LatentPools
+    _say("mla misaligned q / float8 pool dtype")
+    q, pools, table, counts, tags = _latent_case(8, 2, 128, 576, 32, 20, {"FP8": .5, "INT8": .5})
+    dp = _device_pools(pools, dev)
+    tt, ct, gt = (torch.from_numpy(x).to(dev) for x in (table, counts, tags))
+    base = torch.from_numpy(q).to(dev)
+    want = mla_paged_decode(base, dp, tt, ct, gt, v_dim=512, out_dtype=torch.float32)
+    buf = torch.zeros(q.size + 8, dtype=torch.float16, device=dev)
+    view = buf[1:1 + q.size].view(q.shape)
+    view.copy_(base)
+    assert view.data_ptr() % 16 != 0
+    dp8 = LatentPools(c_fp16=dp.c_fp16, c_fp8=dp.c_fp8.view(torch.float8_e4m3fn), c_fp8_scale=dp.c_fp8_scale,
+                      c_int8=dp.c_int8, c_int8_scale=dp.c_int8_scale)
+    got = mla_paged_decode(view, dp8, tt, ct, gt, v_dim=512, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
 def test_mla_empty_rows_are_zero(dev):
     import torch
     from intent_attention import mla_paged_decode
