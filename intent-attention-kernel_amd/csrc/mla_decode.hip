@@ -64,6 +64,11 @@ template <int DQK, int DV, bool WIDE> struct Mla {
   static constexpr int NDMA = (SLOT / 1024 + WAVES - 1) / WAVES;   // 1 KB copies per wave per page
   static constexpr int SLOTS = WIDE ? 2 : 4;   // page pairs in the ring = steps a pair streams in ahead
   static constexpr int CHUNKS = DQK / 8;       // 8-value staging chunks per token
+  // operand reads issued ahead of their MFMAs (score k-steps, value blocks):
+  // the most the register budget holds without spilling; the MFMAs sit between
+  // scheduling barriers so the compiler keeps the reads that far ahead
+  static constexpr int PF_SCORE = 2;
+  static constexpr int PF_VALUE = 4;
   static_assert(DQK % 32 == 0 && DV % 16 == 0 && DV <= DQK && PAGE8 % 1024 == 0, "unsupported MLA shape");
   static_assert((SLOTS & (SLOTS - 1)) == 0 && SLOTS >= 2, "ring of a power-of-two number of page pairs");
 };
@@ -288,12 +293,26 @@ __global__ __launch_bounds__(512, 1) void mla_decode_kernel(const MArgs a) {
 
       // ---- scores of pair s: S^T[16 tok x 16 heads] per page, two chains ----
       f4 s0 = f4{0.f, 0.f, 0.f, 0.f}, s1 = f4{0.f, 0.f, 0.f, 0.f};
+      {
+        constexpr int PFS = C::PF_SCORE;
+        h8 aq0[PFS], aq1[PFS];
 #pragma unroll
-      for (int i = 0; i < C::KSTEPS; ++i) {
-        const h8 a0 = *reinterpret_cast<const h8*>(&sh.t1[R][c][32 * i + 8 * g]);
-        const h8 a1 = *reinterpret_cast<const h8*>(&sh.t1[R][PS + c][32 * i + 8 * g]);
-        s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, q[i], s0, 0, 0, 0);
-        s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, q[i], s1, 0, 0, 0);
+        for (int d = 0; d < PFS && d < C::KSTEPS; ++d) {
+          aq0[d] = *reinterpret_cast<const h8*>(&sh.t1[R][c][32 * d + 8 * g]);
+          aq1[d] = *reinterpret_cast<const h8*>(&sh.t1[R][PS + c][32 * d + 8 * g]);
+        }
+#pragma unroll
+        for (int i = 0; i < C::KSTEPS; ++i) {
+          const h8 a0 = aq0[i % PFS], a1 = aq1[i % PFS];
+          if (i + PFS < C::KSTEPS) {
+            aq0[i % PFS] = *reinterpret_cast<const h8*>(&sh.t1[R][c][32 * (i + PFS) + 8 * g]);
+            aq1[i % PFS] = *reinterpret_cast<const h8*>(&sh.t1[R][PS + c][32 * (i + PFS) + 8 * g]);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+          s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, q[i], s0, 0, 0, 0);
+          s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, q[i], s1, 0, 0, 0);
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
 
       // ---- stage pair s+1 (landed before the barrier) ----
@@ -353,13 +372,25 @@ __global__ __launch_bounds__(512, 1) void mla_decode_kernel(const MArgs a) {
       }
 
       // ---- values of pair s: the wave's heads, every value dim ----
+      {
+        constexpr int PFV = C::PF_VALUE;
+        h8 bq[PFV];
+        auto rd = [&](int db) {
+          const int col = a.VOFF + 16 * db;
+          const h4 b0 = mla_read_column<DQK, DV, WIDE>(sh, R, 4 * g, col, c);
+          const h4 b1 = mla_read_column<DQK, DV, WIDE>(sh, R, PS + 4 * g, col, c);
+          return __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
+        };
 #pragma unroll
-      for (int db = 0; db < C::NDB; ++db) {
-        const int col = a.VOFF + 16 * db;
-        const h4 b0 = mla_read_column<DQK, DV, WIDE>(sh, R, 4 * g, col, c);
-        const h4 b1 = mla_read_column<DQK, DV, WIDE>(sh, R, PS + 4 * g, col, c);
-        const h8 bop = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
-        acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, bop, acc[db], 0, 0, 0);
+        for (int d = 0; d < PFV && d < C::NDB; ++d) bq[d] = rd(d);
+#pragma unroll
+        for (int db = 0; db < C::NDB; ++db) {
+          const h8 bop = bq[db % PFV];
+          if (db + PFV < C::NDB) bq[db % PFV] = rd(db + PFV);
+          __builtin_amdgcn_sched_barrier(0);
+          acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, bop, acc[db], 0, 0, 0);
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
     }
     // the copies of the pages past the end land before the LDS is reused or released
