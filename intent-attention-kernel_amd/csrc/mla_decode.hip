@@ -148,32 +148,45 @@ template <int NDMA, int PAGES> __device__ __forceinline__ void mla_wait_pages() 
   asm volatile("s_waitcnt vmcnt(%0)" : : "n"(NDMA * PAGES) : "memory");
 }
 
-// LDS ring -> [token][dim] f16 tile for a page pair: each task converts one
-// 8-value chunk of one token (8 code bytes, or 16 bytes of f16) -- consecutive
-// tasks are consecutive chunks, so reads and writes are contiguous per wave.
-// FP8 / INT8 codes convert to f16 exactly.
+// LDS ring -> [token][dim] f16 tile for a page pair. Sixteen threads share one
+// token row (thread t: row t / 16, which is page t / 256, so every wave stages
+// one page and its tag is wave-uniform); thread q of a row converts the 8-value
+// chunks q, q + 16, ... of it (8 code bytes, or 16 bytes of f16, each). The
+// offsets of a thread's chunks differ by constants, and a row's 16 chunks are
+// contiguous in the ring and in the tile. FP8 / INT8 codes convert to f16
+// exactly.
 template <int DQK, int DV, bool WIDE>
 __device__ __forceinline__ void mla_stage_pair(MlaShared<DQK, DV, WIDE>& sh, int slot, int buf, int tag0, int tag1,
                                                int tid) {
   using C = Mla<DQK, DV, WIDE>;
-  constexpr int PER_PAGE = PS * C::CHUNKS;
-  for (int task = tid; task < 2 * PER_PAGE; task += C::THREADS) {
-    const int half = task >= PER_PAGE ? 1 : 0;
-    const int t = task - half * PER_PAGE;
-    const int tok = t / C::CHUNKS, ch = t - tok * C::CHUNKS;
-    const int tag = half ? tag1 : tag0;
-    const uint8_t* raw = sh.ring[slot][half];
-    u4 v;
-    if (WIDE && tag == IAK_TAG_FP16) {
-      v = *reinterpret_cast<const u4*>(raw + (tok * DQK + 8 * ch) * 2);
-    } else {
-      const u2 x = *reinterpret_cast<const u2*>(raw + tok * DQK + 8 * ch);
+  static_assert(C::THREADS == 16 * C::TOK, "16 threads per staged row");
+  constexpr int NJ = (C::CHUNKS + 15) / 16;   // chunks per thread (the last one partial)
+  const int row = tid >> 4, q = tid & 15;
+  const int half = row / PS;
+  const int tag = __builtin_amdgcn_readfirstlane(half ? tag1 : tag0);
+  const uint8_t* raw = sh.ring[slot][half];
+  _Float16* dst = &sh.t1[buf][row][8 * q];
+  if (WIDE && tag == IAK_TAG_FP16) {
+    const uint8_t* src = raw + (row - PS * half) * DQK * 2 + 16 * q;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+      if (q + 16 * j < C::CHUNKS)
+        *reinterpret_cast<u4*>(dst + 128 * j) = *reinterpret_cast<const u4*>(src + 256 * j);
+    return;
+  }
+  const uint8_t* src = raw + (row - PS * half) * DQK + 8 * q;
+  u2 x[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+    if (q + 16 * j < C::CHUNKS) x[j] = *reinterpret_cast<const u2*>(src + 128 * j);
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    if (q + 16 * j < C::CHUNKS) {
       uint32_t lo0, hi0, lo1, hi1;
-      if (tag == IAK_TAG_FP8) { fp8x4_to_f16(x[0], lo0, hi0); fp8x4_to_f16(x[1], lo1, hi1); }
-      else { i8x4_to_f16(x[0], lo0, hi0); i8x4_to_f16(x[1], lo1, hi1); }
-      v = u4{lo0, hi0, lo1, hi1};
+      if (tag == IAK_TAG_FP8) { fp8x4_to_f16(x[j][0], lo0, hi0); fp8x4_to_f16(x[j][1], lo1, hi1); }
+      else { i8x4_to_f16(x[j][0], lo0, hi0); i8x4_to_f16(x[j][1], lo1, hi1); }
+      *reinterpret_cast<u4*>(dst + 128 * j) = u4{lo0, hi0, lo1, hi1};
     }
-    *reinterpret_cast<u4*>(&sh.t1[buf][PS * half + tok][8 * ch]) = v;
   }
 }
 
