@@ -250,7 +250,8 @@ iak_status iak_quantize_pages(const iak_quantize_args* args, void* stream);
  * page_size), num_pages, B, H) whenever every selected page is below
  * num_pages (the reference raises IndexError otherwise).
  * span_offsets has ceil(num_rows / rows_per_list) + 1 entries (CSR into the
- * span arrays); span_tag holds IAK_TAG_* values. Work is proportional to the
+ * span arrays); span_tag holds IAK_TAG_* values. Every array is int32 and must
+ * be 4-byte aligned (IAK_EINVAL otherwise). Work is proportional to the
  * pages the lists name; a list whose pages span more than 16384 ids tests
  * first occurrence against its earlier spans (quadratic in spans).
  */
