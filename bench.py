@@ -16,7 +16,9 @@ torch ops; tests check them bit-exact against the oracle.
 
 A step is one decode of the whole batch (split kernel + merge kernel) with
 every input already in HBM; the 2 GB the step reads exceed the 256 MB
-Infinity Cache, so consecutive steps do not hit in it. Timing: HIP events on
+Infinity Cache, so consecutive steps do not hit in it (cfg4, whose step reads
+178 MB, rotates four page tables with disjoint selections; cfg5 four page
+sets). Timing: HIP events on
 the stream the kernels run on, around the K back-to-back timed steps. A second
 pass of K steps records events around each step (the p10/p50/p90 spread) and,
 through iak_paged_decode_timed, around the split kernel alone: its average
@@ -56,8 +58,11 @@ CONFIGS = {
     "cfg3": dict(B=32, Hq=32, Hkv=8, D=128, T=65536, sel=0.40,
                  mix={TAG_FP16: .25, TAG_FP8: .25, TAG_INT8: .30, TAG_INT4: .20}, outliers=0.01,
                  q_scale=1 / math.sqrt(128)),
+    # a cfg4 step reads 178 MB, which the 256 MB Infinity Cache could hold from one
+    # step to the next: four page tables with disjoint selections per (batch, KV
+    # head) rotate, so a step's pages were last read three steps (> 500 MB) before
     "cfg4": dict(B=4, Hq=32, Hkv=8, D=128, T=131072, sel=0.15,
-                 mix={TAG_FP16: .10, TAG_INT8: .30, TAG_INT4R: .60}, outliers=0.0, q_scale=1.0),
+                 mix={TAG_FP16: .10, TAG_INT8: .30, TAG_INT4R: .60}, outliers=0.0, q_scale=1.0, sets=4),
     # small all-precision case for tests and smoke runs
     "tiny": dict(B=2, Hq=8, Hkv=2, D=128, T=2048, sel=0.40,
                  mix={TAG_FP16: .2, TAG_FP8: .2, TAG_INT8: .2, TAG_INT4: .2, TAG_INT4R: .2}, outliers=0.01,
@@ -131,10 +136,16 @@ def build_workload(name: str, device: torch.device, seed: int = 1234, chunk_page
         mid = torch.stack([torch.randperm(P - 320, generator=gc)[:704] + 64 for _ in range(B * Hkv)])
         logical = torch.cat([torch.arange(64).expand(B * Hkv, 64), mid.sort(dim=1).values,
                              torch.arange(P - 256, P).expand(B * Hkv, 256)], dim=1)
+        logicals = [logical]
     else:
+        # `sets` page tables whose selections are disjoint per (batch, KV head)
         nsel = int(cfg["sel"] * P)
-        logical = torch.stack([torch.randperm(P, generator=gc)[:nsel].sort().values for _ in range(B * Hkv)])
-    table = torch.gather(perm, 1, logical).reshape(B, Hkv, -1).contiguous().to(device)
+        sets = cfg.get("sets", 1)
+        assert sets * nsel <= P, "disjoint page sets need sets * selected <= pages"
+        orders = [torch.randperm(P, generator=gc) for _ in range(B * Hkv)]
+        logicals = [torch.stack([o[k * nsel:(k + 1) * nsel].sort().values for o in orders]) for k in range(sets)]
+    tables = [torch.gather(perm, 1, lg).reshape(B, Hkv, -1).contiguous().to(device) for lg in logicals]
+    table = tables[0]
     W = table.shape[2]
     counts = torch.full((B, Hkv), W, dtype=torch.int32, device=device)
 
@@ -185,7 +196,8 @@ def build_workload(name: str, device: torch.device, seed: int = 1234, chunk_page
                 getattr(pools, f"{w}_{pool}")[lo + idx] = codes
                 getattr(pools, f"{w}_{sc}")[lo + idx] = scales.to(getattr(pools, f"{w}_{sc}").dtype)
     q = (torch.randn((B, Hq, D), generator=g, device=device) * cfg["q_scale"]).half()
-    return dict(cfg=cfg, name=name, q=q, pools=pools, table=table, counts=counts, tags=tags, NP=NP, W=W)
+    return dict(cfg=cfg, name=name, q=q, pools=pools, table=table, tables=tables, counts=counts, tags=tags, NP=NP,
+                W=W)
 
 
 # HBM bytes per decode-kernel launch (reads + writes) from rocprofv3 FETCH_SIZE /
@@ -201,11 +213,11 @@ PAGE_BYTES = {  # K+V code bytes and scale bytes per page (D = 128, fp16 scales,
 }
 
 
-def algorithmic_bytes(wl) -> dict:
+def algorithmic_bytes(wl, table=None) -> dict:
     """Bytes one step must move: each selected page's K+V codes and scales once
     per KV head (GQA shares them), its page-table entry and tag, the counts,
-    Q in and O out."""
-    tags_sel = wl["tags"][wl["table"].long()].flatten()
+    Q in and O out (for `table`, default the workload's first page table)."""
+    tags_sel = wl["tags"][(wl["table"] if table is None else table).long()].flatten()
     n = {t: int((tags_sel == t).sum()) for t in PAGE_BYTES}
     codes = sum(n[t] * PAGE_BYTES[t][0] for t in n)
     scales = sum(n[t] * PAGE_BYTES[t][1] for t in n)
@@ -726,18 +738,21 @@ def main() -> None:
           file=sys.stderr, flush=True)
     cfg = wl["cfg"]
     out = torch.empty((cfg["B"], cfg["Hq"], cfg["D"]), dtype=torch.float16, device=dev)
-    plan = make_plan(wl["q"], wl["pools"], wl["table"], wl["counts"], wl["tags"], out=out,
-                     pages_per_split=args.pages_per_split)
+    # one plan per page table; step i runs table i % sets
+    plans = [make_plan(wl["q"], wl["pools"], t, wl["counts"], wl["tags"], out=out,
+                       pages_per_split=args.pages_per_split) for t in wl["tables"]]
+    plan = plans[0]
+    nsets = len(plans)
     stream = torch.cuda.current_stream(dev)
-    for _ in range(args.warmup):
-        plan.run()
+    for i in range(args.warmup):
+        plans[i % nsets].run()
     torch.cuda.synchronize()
     # timed region: K back-to-back steps between two events on the kernels' stream
     t_start, t_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t_start.record(stream)
-    for _ in range(args.steps):
-        plan.run()
+    for i in range(args.steps):
+        plans[i % nsets].run()
     t_end.record(stream)
     torch.cuda.synchronize()
     total_ms = t_start.elapsed_time(t_end)
@@ -746,15 +761,20 @@ def main() -> None:
     # event records cost a few microseconds each, so they stay out of `value`
     ev = kernel_events(args.steps, stream)
     kev = kernel_events(args.steps, stream)
-    for (s, e), k in zip(ev, kev):
+    for i, ((s, e), k) in enumerate(zip(ev, kev)):
         s.record(stream)
-        plan.run(events=k)
+        plans[i % nsets].run(events=k)
         e.record(stream)
     torch.cuda.synchronize()
     per = sorted(s.elapsed_time(e) for s, e in ev)
     kernel_ms = sum(b.elapsed_time(e) for b, e in kev) / args.steps
     ms = total_ms / args.steps
-    ab = algorithmic_bytes(wl)
+    # bytes of the average step over the rotated page sets
+    abs_ = [algorithmic_bytes(wl, t) for t in wl["tables"]]
+    ab = dict(abs_[0])
+    for key in ("total", "codes", "scales", "meta", "qo", "pages"):
+        ab[key] = int(round(sum(x[key] for x in abs_) / nsets))
+    ab["per_tag"] = {k: int(round(sum(x["per_tag"][k] for x in abs_) / nsets)) for k in abs_[0]["per_tag"]}
     achieved = ab["total"] / (ms * 1e-3) / 1e9
     # the split kernel moves every algorithmic byte but the output, which the merge writes
     kernel_bytes = ab["total"] - ab["qo"] // 2
@@ -770,7 +790,8 @@ def main() -> None:
         "data": "synthetic (seeded torch generator; codes = reference fake-quant of N(0,1) fp16 pages)",
         "config": {"workload": f"{args.config}: Llama-3-8B GQA decode B={cfg['B']} Hq={cfg['Hq']} "
                                f"Hkv={cfg['Hkv']} D={cfg['D']} ctx={cfg['T']} page=16 "
-                               f"sel={wl['W']} pages/row mix={ {int(k): v for k, v in cfg['mix'].items()} }",
+                               f"sel={wl['W']} pages/row mix={ {int(k): v for k, v in cfg['mix'].items()} }"
+                               + (f", {nsets} disjoint page sets rotated" if nsets > 1 else ""),
                    "selected_pages": ab["pages"], "algorithmic_bytes": ab["total"],
                    "bytes_breakdown": {k: ab[k] for k in ("codes", "scales", "meta", "qo")},
                    "pages_per_tag": ab["per_tag"], "pages_per_split": plan.args.pages_per_split,
