@@ -565,8 +565,9 @@ __device__ __forceinline__ void load_tag(const KArgs& a, int raw, int cnt, int s
 template <int QT> constexpr int waves_per_simd() { return QT == IAK_DTYPE_F16 ? IAK_MIN_WAVES_PER_SIMD : 2; }
 
 // One wave per work item. The dependent metadata loads (table entry and count
-// -> tag -> scales) are the wave's prologue; the waves the hardware starts as
-// others finish run their prologue while the rest of the CU streams pages.
+// -> tag) are the wave's prologue, the page scales follow the FP16 pages; the
+// waves the hardware starts as others finish run their prologue while the rest
+// of the CU streams pages.
 template <int D, int QT>
 __global__ __launch_bounds__(64 * IAK_WAVES_PER_BLOCK, waves_per_simd<QT>())
 void paged_decode_kernel(const KArgs a) {
@@ -584,7 +585,6 @@ void paged_decode_kernel(const KArgs a) {
     locate(a, item, sp, start, unit);
     load_entry(a, unit, start, a.chunk, lane, raw, cnt);
     load_tag(a, raw, cnt, start, a.chunk, lane, pid, tag, sp.n);
-    load_page_scales<D>(a, pid, tag, slot);
   }
 
   Wave<D, QF32> w;
@@ -606,6 +606,10 @@ void paged_decode_kernel(const KArgs a) {
         [&](Raw16<D>& r, int p) { load16<D>(r, kp + (int64_t)p * PS * D, vp + (int64_t)p * PS * D, c, g); },
         [&](const Raw16<D>& r, int) { page_fp16(w, r, smul); });
   }
+  // the scales are first needed by the classes below: loaded here, their round
+  // trip overlaps the next class's ring fill instead of preceding the FP16 pages
+  load_page_scales<D>(a, pid, tag, slot);
+
   // ---- one-byte precisions ----
   {
     const uint8_t* kp = reinterpret_cast<const uint8_t*>(a.k_fp8);
