@@ -204,7 +204,7 @@ def build_workload(name: str, device: torch.device, seed: int = 1234, chunk_page
 # WRITE_SIZE runs of this bench, each scaled by what the counter reads for a
 # 1 GiB device copy (--calibrate-copy): profiles/paged_decode_cfg3_hbm_traffic.txt.
 MEASURED_TRAFFIC = {
-    "cfg3": {"bytes": 2_120_189_338 + 13_974_938, "source": "profiles/paged_decode_cfg3_hbm_traffic.txt"},
+    "cfg3": {"bytes": 2_115_644_502 + 13_975_363, "source": "profiles/paged_decode_cfg3_hbm_traffic.txt"},
 }
 
 PAGE_BYTES = {  # K+V code bytes and scale bytes per page (D = 128, fp16 scales, INT4 groups of 32)
