@@ -51,7 +51,7 @@ def _decode_case(seed):
                 q_scale=q_scale, neg=neg)
 
 
-@pytest.mark.parametrize("seed", range(40))
+@pytest.mark.parametrize("seed", range(96))
 def test_decode_random_configs(dev, seed):
     import torch
     from intent_attention import paged_decode
@@ -109,7 +109,7 @@ def _latent_case(rng, B, H, DQK, NP, W, mix):
 MLA_SHAPES = [(64, 64, 0), (128, 128, 0), (256, 256, 0), (512, 512, 0), (576, 512, 0), (576, 64, 512)]
 
 
-@pytest.mark.parametrize("seed", range(16))
+@pytest.mark.parametrize("seed", range(40))
 def test_mla_random_configs(dev, seed):
     import torch
     from intent_attention import LatentPools, mla_paged_decode
@@ -140,7 +140,7 @@ def test_mla_random_configs(dev, seed):
     assert err <= (1e-2 if quant else 2e-3), f"case {c}: max abs err {err:.3e}"
 
 
-@pytest.mark.parametrize("seed", range(24))
+@pytest.mark.parametrize("seed", range(48))
 def test_page_tables_random_configs(dev, seed):
     import torch
     from intent_attention import build_page_tables
