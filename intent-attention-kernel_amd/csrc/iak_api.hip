@@ -101,10 +101,18 @@ iak_status validate(const iak_paged_decode_args* a, Plan* plan) {
   const int W = a->table_width;
   int chunk = a->pages_per_split;
   if (chunk == 0) {
-    // long splits amortise the per-split prologue and partial traffic; shorter
-    // ones only when the grid would otherwise not fill the 256 CUs
+    // long splits amortise the per-split prologue and partial traffic, and
+    // 64-entry splits keep HBM busy from 2048 waves on. Smaller grids are
+    // latency-bound: there the splits shrink until the waves just fit the
+    // waves the GPU holds at once (one round, no tail of late waves), but not
+    // below 8 entries
     chunk = 64;
-    while (chunk > 16 && rows * ((W + chunk - 1) / chunk) < 2048) chunk /= 2;
+    if (rows * ((W + 63) / 64) < 2048) {
+      const long long resident = (long long)IAK_GPU_CUS * 4 * (a->q_dtype == IAK_DTYPE_F16 ? IAK_MIN_WAVES_PER_SIMD : 2);
+      const long long per_row = resident / (rows > 0 ? rows : 1);
+      chunk = per_row > 0 ? (int)((W + per_row - 1) / per_row) : 64;
+      chunk = chunk < 8 ? 8 : (chunk > 64 ? 64 : chunk);
+    }
   }
   int splits = (W + chunk - 1) / chunk;
   if (splits < 1) splits = 1;

@@ -10,6 +10,8 @@
 
 #define IAK_WAVES_PER_BLOCK 4
 #define IAK_MIN_WAVES_PER_SIMD 3
+// compute units of the MI355X / MI350X (gfx950) the split plan sizes grids for
+#define IAK_GPU_CUS 256
 // pages per ring in each precision class loop (one computed, the rest in flight)
 #ifndef IAK_RING_FP16
 #define IAK_RING_FP16 2
