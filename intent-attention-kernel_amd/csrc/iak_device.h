@@ -142,6 +142,11 @@ __device__ __forceinline__ float xsum16_32(float v) {
 }
 
 template <typename T> __device__ __forceinline__ T ld(const T* p) { return *p; }
+// Streaming load (the nontemporal hint): for page data read once per launch.
+// Each such load instruction should cover whole 128-byte lines; a line read
+// in parts by several instructions can be evicted and fetched again between
+// them.
+template <typename T> __device__ __forceinline__ T ld_nt(const T* p) { return __builtin_nontemporal_load(p); }
 
 __device__ __forceinline__ float load_scale(const void* p, int64_t idx, int dtype) {
   if (dtype == IAK_DTYPE_F32) return reinterpret_cast<const float*>(p)[idx];

@@ -18,17 +18,20 @@
 //
 // Per page (16 tokens) and wave, lane = c + 16*g (c, g = lane % 16, lane / 16):
 //   scores  S^T[16 tok x 16 heads] = K[16 tok x D] . Q^T[D x 16 heads]
-//           v_mfma_f32_16x16x32_f16, D/32 k-steps. A operand: lane holds token c,
-//           dims (D/4)g + 8i .. +7 at step i (K dequantised to f16 in registers);
-//           B operand: lane holds head c (zero for c >= G), the same dims.
-//           Result: lane holds head c, tokens 4g .. 4g+3.
+//           v_mfma_f32_16x16x32_f16, D/32 k-steps. A operand: lane holds token
+//           slot c, dims (D/4)g + 8i .. +7 at step i (K dequantised to f16 in
+//           registers); B operand: lane holds head c (zero for c >= G), the
+//           same dims. Result: lane holds head c, token slots 4g .. 4g+3.
+//           Token slot r is token perm16(r) on FP16 and one-byte pages, whose
+//           K reaches this layout through the wave's LDS buffer (the loads
+//           themselves cover whole lines), and token r on INT4 pages.
 //   softmax exp2 domain; the running max per head is shared by the 4 lane groups
 //           (two cross-lane max steps per page) and only moves when a page
 //           exceeds it by more than 8 (2^8 head-room in p), so the accumulator
 //           rescale is rare.
 //   values  O^T[D x 16 heads] += V^T[D x 16 tok] . P^T[16 tok x 16 heads]
 //           v_mfma_f32_16x16x16_f16, D/16 row blocks. A operand: lane holds dim
-//           (D/16)c + mb of tokens 4g..4g+3; B operand: p of head c, tokens
+//           (D/16)c + mb of token slots 4g..4g+3; B operand: p of head c, slots
 //           4g..4g+3 -- exactly the score result layout, converted to f16.
 //           Accumulator: lane holds head c, dims (D/4)g .. (D/4)g + D/4 - 1.
 //   Per-page scalar scales fold into the score multiplier (K) and into p (V);
@@ -47,34 +50,49 @@ namespace iak {
 
 // --------------------------------------------------------------------------- //
 // Raw page data as each lane loads it, per precision and head_dim.
+//
+// FP16 and one-byte pages are read so that every load instruction covers whole
+// 128-byte lines, with the streaming (nontemporal) hint:
+//   K  load i of lane l is the 16 bytes at 1024 i + 16 l of the page; the wave
+//      rewrites them into the MFMA layout through its LDS buffer (k_through_lds);
+//   V  load t of lane (c, g) is token 4t + g, so one instruction reads the four
+//      consecutive rows 4t .. 4t+3.
+// Lane (c, g) therefore holds K of token perm16(c) and V of tokens perm16(4g + t),
+// the same permutation on both sides of the softmax. INT4 pages keep the
+// direct layout (token c; tokens 4g + t) and plain loads: their K loads already
+// cover the whole page, and streaming loads measured slower on them.
 // --------------------------------------------------------------------------- //
 
-template <int D> struct Raw16 {   // FP16: K token c dims (D/4)g..; V tokens 4g+k dims (D/16)c..
+template <int D> struct Raw16 {   // FP16: K chunks 64i + lane; V tokens 4t+g dims (D/16)c..
   u4 k[D / 32];                    // D/4 halves = D/32 u4
   uint32_t v[4][D / 32];           // D/16 halves per token = D/32 dwords
 };
 template <int D> struct Raw8 {    // FP8 / INT8 / INT4_RESIDUAL (one byte per element)
-  uint32_t k[D / 16];              // D/4 bytes
-  uint32_t v[4][D / 64 > 0 ? D / 64 : 1];  // D/16 bytes per token
+  uint32_t k[D / 16];              // D/4 bytes: chunks 64i + lane
+  uint32_t v[4][D / 64 > 0 ? D / 64 : 1];  // D/16 bytes per token 4t+g
 };
-template <int D> struct Raw4 {    // INT4 (half a byte per element)
+template <int D> struct Raw4 {    // INT4 (half a byte per element): K token c, V tokens 4g+t
   uint32_t k[D / 32];              // D/8 bytes
   uint32_t v[4];                   // D/32 bytes per token (<= 4)
 };
 
+// Token of score row / P slot r of FP16 and one-byte pages: perm16(4g + t) =
+// 4t + g.
+__device__ __forceinline__ int perm16(int r) { return 4 * (r & 3) + (r >> 2); }
+
 template <int D> __device__ __forceinline__ void load16(Raw16<D>& r, const _Float16* kp, const _Float16* vp,
                                                        int c, int g) {
-  const u4* kr = reinterpret_cast<const u4*>(kp + c * D + (D / 4) * g);
+  const u4* kr = reinterpret_cast<const u4*>(kp) + (c + 16 * g);
 #pragma unroll
-  for (int i = 0; i < D / 32; ++i) r.k[i] = ld(kr + i);
+  for (int i = 0; i < D / 32; ++i) r.k[i] = ld_nt(kr + 64 * i);
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
-    const _Float16* row = vp + (4 * g + t) * D + (D / 16) * c;
+    const _Float16* row = vp + (4 * t + g) * D + (D / 16) * c;
     if constexpr (D == 128) {
-      u4 x = ld(reinterpret_cast<const u4*>(row));
+      u4 x = ld_nt(reinterpret_cast<const u4*>(row));
       r.v[t][0] = x[0]; r.v[t][1] = x[1]; r.v[t][2] = x[2]; r.v[t][3] = x[3];
     } else {
-      u2 x = ld(reinterpret_cast<const u2*>(row));
+      u2 x = ld_nt(reinterpret_cast<const u2*>(row));
       r.v[t][0] = x[0]; r.v[t][1] = x[1];
     }
   }
@@ -82,20 +100,20 @@ template <int D> __device__ __forceinline__ void load16(Raw16<D>& r, const _Floa
 
 template <int D> __device__ __forceinline__ void load8(Raw8<D>& r, const uint8_t* kp, const uint8_t* vp,
                                                       int c, int g) {
-  const u4* kr = reinterpret_cast<const u4*>(kp + c * D + (D / 4) * g);
+  const u4* kr = reinterpret_cast<const u4*>(kp) + (c + 16 * g);
 #pragma unroll
   for (int i = 0; i < D / 64; ++i) {
-    u4 x = ld(kr + i);
+    u4 x = ld_nt(kr + 64 * i);
     r.k[4 * i + 0] = x[0]; r.k[4 * i + 1] = x[1]; r.k[4 * i + 2] = x[2]; r.k[4 * i + 3] = x[3];
   }
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
-    const uint8_t* row = vp + (4 * g + t) * D + (D / 16) * c;
+    const uint8_t* row = vp + (4 * t + g) * D + (D / 16) * c;
     if constexpr (D == 128) {
-      u2 x = ld(reinterpret_cast<const u2*>(row));
+      u2 x = ld_nt(reinterpret_cast<const u2*>(row));
       r.v[t][0] = x[0]; r.v[t][1] = x[1];
     } else {
-      r.v[t][0] = ld(reinterpret_cast<const uint32_t*>(row));
+      r.v[t][0] = ld_nt(reinterpret_cast<const uint32_t*>(row));
     }
   }
 }
@@ -212,28 +230,74 @@ __device__ __forceinline__ void pv_rows(Wave<D, QF32>& w, const uint32_t (&vt)[4
 // Per-precision page compute
 // --------------------------------------------------------------------------- //
 
+// LDS slot (16-byte units) of chunk `ch` of token row `row` in a wave's K
+// transpose buffer of NC chunks per row, XOR-swizzled so that 16 lanes reading
+// one chunk of 16 different rows, and 16 lanes writing 256 consecutive bytes,
+// each touch every 16-byte bank group once.
+template <int NC> __device__ __forceinline__ int kt_slot(int row, int ch) {
+  constexpr int RPB = 16 / NC;   // rows per 256 bytes
+  return row * NC + (ch ^ ((row / RPB) % NC));
+}
+
+// A wave's K page, loaded as 16-byte chunks 64 i + lane (lane = c + 16 g) of
+// the page, rewritten through its LDS buffer: afterwards lane (c, g) holds the
+// NI chunks NI g .. NI g + NI - 1 of token row perm16(c).
+template <int NC, int NI>
+__device__ __forceinline__ void k_through_lds(u4 (&k)[NI], u4* kt, int c, int g) {
+  const int lane = c + 16 * g;
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int f = 64 * i + lane;
+    kt[kt_slot<NC>(f / NC, f % NC)] = k[i];
+  }
+  const int row = perm16(c);
+#pragma unroll
+  for (int i = 0; i < NI; ++i) k[i] = kt[kt_slot<NC>(row, NI * g + i)];
+}
+
 template <int D, bool QF32>
-__device__ __forceinline__ void page_fp16(Wave<D, QF32>& w, const Raw16<D>& r, float smul) {
+__device__ __forceinline__ void page_fp16(Wave<D, QF32>& w, const Raw16<D>& r, float smul, u4* kt, int c, int g) {
+  u4 k[D / 32];
+#pragma unroll
+  for (int i = 0; i < D / 32; ++i) k[i] = r.k[i];
+  k_through_lds<D / 8, D / 32>(k, kt, c, g);
   h8 ka[D / 32];
 #pragma unroll
-  for (int i = 0; i < D / 32; ++i) ka[i] = __builtin_bit_cast(h8, r.k[i]);
+  for (int i = 0; i < D / 32; ++i) ka[i] = __builtin_bit_cast(h8, k[i]);
   const h4 pb = softmax_step(w, scores(w, ka), smul, 1.0f);
   pv_rows(w, r.v, pb);
+}
+
+// The K dwords of a one-byte page in the MFMA layout (lane (c, g): token row
+// perm16(c), bytes (D/4) g .. (D/4) g + D/4 - 1).
+template <int D> __device__ __forceinline__ void k8_words(const Raw8<D>& r, uint32_t (&kw)[D / 16], u4* kt, int c,
+                                                         int g) {
+  u4 k[D / 64];
+#pragma unroll
+  for (int i = 0; i < D / 64; ++i) k[i] = u4{r.k[4 * i], r.k[4 * i + 1], r.k[4 * i + 2], r.k[4 * i + 3]};
+  k_through_lds<D / 16, D / 64>(k, kt, c, g);
+#pragma unroll
+  for (int i = 0; i < D / 64; ++i) {
+    kw[4 * i] = k[i][0]; kw[4 * i + 1] = k[i][1]; kw[4 * i + 2] = k[i][2]; kw[4 * i + 3] = k[i][3];
+  }
 }
 
 // FP8 / INT8 page: codes convert to f16 exactly; the K page scale is in
 // `smul`, the V page scale `vmul` multiplies p.
 template <int D, bool QF32, int TAG>
-__device__ __forceinline__ void page_byte(Wave<D, QF32>& w, const Raw8<D>& r, float smul, float vmul) {
+__device__ __forceinline__ void page_byte(Wave<D, QF32>& w, const Raw8<D>& r, float smul, float vmul, u4* kt,
+                                          int c, int g) {
+  uint32_t kw[D / 16];
+  k8_words<D>(r, kw, kt, c, g);
   h8 ka[D / 32];
 #pragma unroll
   for (int i = 0; i < D / 32; ++i) {
     uint32_t o[4];
     if constexpr (TAG == IAK_TAG_FP8) {
-      fp8x4_to_f16(r.k[2 * i], o[0], o[1]); fp8x4_to_f16(r.k[2 * i + 1], o[2], o[3]);
+      fp8x4_to_f16(kw[2 * i], o[0], o[1]); fp8x4_to_f16(kw[2 * i + 1], o[2], o[3]);
     } else {
       static_assert(TAG == IAK_TAG_INT8, "page_byte handles FP8 and INT8 pages");
-      i8x4_to_f16(r.k[2 * i], o[0], o[1]); i8x4_to_f16(r.k[2 * i + 1], o[2], o[3]);
+      i8x4_to_f16(kw[2 * i], o[0], o[1]); i8x4_to_f16(kw[2 * i + 1], o[2], o[3]);
     }
     ka[i] = make_h8(o[0], o[1], o[2], o[3]);
   }
@@ -263,7 +327,9 @@ __device__ __forceinline__ void page_byte(Wave<D, QF32>& w, const Raw8<D>& r, fl
 // `ks0, ks1, vs0, vs1`: K base / residual and V base / residual scales.
 template <int D, bool QF32>
 __device__ __forceinline__ void page_int4r(Wave<D, QF32>& w, const Raw8<D>& r, float smul, float ks0, float ks1,
-                                           float vs0, float vs1) {
+                                           float vs0, float vs1, u4* kt, int c, int g) {
+  uint32_t kw[D / 16];
+  k8_words<D>(r, kw, kt, c, g);
   const uint32_t mg = magic_i4();
   f4 sb = {0.f, 0.f, 0.f, 0.f}, sr = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -272,7 +338,7 @@ __device__ __forceinline__ void page_int4r(Wave<D, QF32>& w, const Raw8<D>& r, f
     uint32_t b[4], q16[4];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const uint32_t x = r.k[2 * i + h];
+      const uint32_t x = kw[2 * i + h];
       const uint32_t y01 = __builtin_amdgcn_perm(x, x, 0x01010000u);   // bytes 0, 1 -> 0, 2
       const uint32_t y23 = __builtin_amdgcn_perm(x, x, 0x03030202u);   // bytes 2, 3 -> 0, 2
       b[2 * h] = bits(i4r_base_pair(y01, mg));
@@ -576,6 +642,9 @@ void paged_decode_kernel(const KArgs a) {
   const int c = lane & 15, g = lane >> 4;
   const int item = blockIdx.x * IAK_WAVES_PER_BLOCK + (threadIdx.x >> 6);
   if (item >= a.items) return;
+  // the wave's K transpose buffer: one FP16 page's K (a one-byte page uses half)
+  __shared__ u4 kt_all[IAK_WAVES_PER_BLOCK][PS * D / 8];
+  u4* kt = kt_all[threadIdx.x >> 6];
 
   Split sp;
   int pid, tag;
@@ -595,7 +664,6 @@ void paged_decode_kernel(const KArgs a) {
   load_q<D, QT>(a, sp, w, c, g);
 
   const float smul = a.score_mult;
-  const h2 one = splat2((_Float16)1.0f);
 
   // ---- FP16 pages ----
   {
@@ -604,7 +672,7 @@ void paged_decode_kernel(const KArgs a) {
     class_loop<IAK_RING_FP16, Raw16<D>>(
         __builtin_amdgcn_ballot_w64(tag == IAK_TAG_FP16), pid,
         [&](Raw16<D>& r, int p) { load16<D>(r, kp + (int64_t)p * PS * D, vp + (int64_t)p * PS * D, c, g); },
-        [&](const Raw16<D>& r, int) { page_fp16(w, r, smul); });
+        [&](const Raw16<D>& r, int) { page_fp16(w, r, smul, kt, c, g); });
   }
   // the scales are first needed by the classes below: loaded here, their round
   // trip overlaps the next class's ring fill instead of preceding the FP16 pages
@@ -619,7 +687,7 @@ void paged_decode_kernel(const KArgs a) {
         [&](Raw8<D>& r, int p) { load8<D>(r, kp + (int64_t)p * PS * D, vp + (int64_t)p * PS * D, c, g); },
         [&](const Raw8<D>& r, int idx) {
           const Scales s = read_scales(slot, idx);
-          page_byte<D, QF32, IAK_TAG_FP8>(w, r, smul * u2f(s.s[0]), u2f(s.s[1]));
+          page_byte<D, QF32, IAK_TAG_FP8>(w, r, smul * u2f(s.s[0]), u2f(s.s[1]), kt, c, g);
         });
   }
   {
@@ -630,7 +698,7 @@ void paged_decode_kernel(const KArgs a) {
         [&](Raw8<D>& r, int p) { load8<D>(r, kp + (int64_t)p * PS * D, vp + (int64_t)p * PS * D, c, g); },
         [&](const Raw8<D>& r, int idx) {
           const Scales s = read_scales(slot, idx);
-          page_byte<D, QF32, IAK_TAG_INT8>(w, r, smul * u2f(s.s[0]), u2f(s.s[1]));
+          page_byte<D, QF32, IAK_TAG_INT8>(w, r, smul * u2f(s.s[0]), u2f(s.s[1]), kt, c, g);
         });
   }
   {
@@ -641,7 +709,7 @@ void paged_decode_kernel(const KArgs a) {
         [&](Raw8<D>& r, int p) { load8<D>(r, kp + (int64_t)p * PS * D, vp + (int64_t)p * PS * D, c, g); },
         [&](const Raw8<D>& r, int idx) {
           const Scales s = read_scales(slot, idx);
-          page_int4r(w, r, smul, u2f(s.s[0]), u2f(s.s[1]), u2f(s.s[2]), u2f(s.s[3]));
+          page_int4r(w, r, smul, u2f(s.s[0]), u2f(s.s[1]), u2f(s.s[2]), u2f(s.s[3]), kt, c, g);
         });
   }
   // ---- INT4 pages: lane K dims (D/4)g.. lie in group kg, V dims (D/16)c.. in group vg ----
