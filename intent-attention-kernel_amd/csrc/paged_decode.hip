@@ -556,12 +556,18 @@ __device__ __forceinline__ void load_q(const KArgs& a, const Split& sp, Wave<D, 
   }
 }
 
+// Read-only target of the ring loads issued past the end of a class: one page
+// of any precision (at most PS x 128 x 2 bytes), the same address for every
+// wave, so those loads stay in the L2 instead of fetching a streamed page again.
+static __device__ __attribute__((aligned(4096))) uint8_t pad_page[PS * 128 * 2];
+
 // Walks the pages of one precision class (lanes set in `mask`) through a ring
 // of R register buffers: while one page is computed the next R-1 are in
 // flight. Every step issues exactly one page load -- once the class runs out
-// of pages the last page is loaded again (a cache hit) -- and the loop exits
-// only at its latch, so each buffer stays in its registers and the wait
-// before each compute is a fixed vmcnt: loads are never drained early.
+// of pages the load names page -1, which the load functions point at
+// pad_page -- and the loop exits only at its latch, so each buffer stays in
+// its registers and the wait before each compute is a fixed vmcnt: loads are
+// never drained early.
 template <int R, typename Raw, typename LoadF, typename ComputeF>
 __device__ __forceinline__ void class_loop(uint64_t mask, int pid, LoadF load, ComputeF compute) {
   if (!mask) return;
@@ -571,20 +577,29 @@ __device__ __forceinline__ void class_loop(uint64_t mask, int pid, LoadF load, C
   int last = 0;
 #pragma unroll
   for (int j = 0; j < R; ++j) {
+    const bool real = mask != 0;
     if (mask) last = take(mask);
     idx[j] = last;
-    load(buf[j], __builtin_amdgcn_readlane(pid, last));
+    const int p = __builtin_amdgcn_readlane(pid, last);
+    load(buf[j], real ? p : -1);
   }
   // one exit, at the latch: the R steps of the body always issue their loads
   for (int base = 0; base < n; base += R) {
 #pragma unroll
     for (int j = 0; j < R; ++j) {
       if (base + j < n) compute(buf[j], idx[j]);
+      const bool real = mask != 0;
       if (mask) last = take(mask);
       idx[j] = last;
-      load(buf[j], __builtin_amdgcn_readlane(pid, last));
+      const int p = __builtin_amdgcn_readlane(pid, last);
+      load(buf[j], real ? p : -1);
     }
   }
+}
+
+// Base address of page `p` of a pool with `bytes` per page; pad_page for p < 0.
+template <typename T> __device__ __forceinline__ const T* page_at(const void* pool, int p, int bytes) {
+  return reinterpret_cast<const T*>(p < 0 ? pad_page : reinterpret_cast<const uint8_t*>(pool) + (int64_t)p * bytes);
 }
 
 // Position of work item `item`: split `item % splits` of row
@@ -667,11 +682,11 @@ void paged_decode_kernel(const KArgs a) {
 
   // ---- FP16 pages ----
   {
-    const _Float16* kp = reinterpret_cast<const _Float16*>(a.k_fp16);
-    const _Float16* vp = reinterpret_cast<const _Float16*>(a.v_fp16);
     class_loop<IAK_RING_FP16, Raw16<D>>(
         __builtin_amdgcn_ballot_w64(tag == IAK_TAG_FP16), pid,
-        [&](Raw16<D>& r, int p) { load16<D>(r, kp + (int64_t)p * PS * D, vp + (int64_t)p * PS * D, c, g); },
+        [&](Raw16<D>& r, int p) {
+          load16<D>(r, page_at<_Float16>(a.k_fp16, p, PS * D * 2), page_at<_Float16>(a.v_fp16, p, PS * D * 2), c, g);
+        },
         [&](const Raw16<D>& r, int) { page_fp16(w, r, smul, kt, c, g); });
   }
   // the scales are first needed by the classes below: loaded here, their round
@@ -680,33 +695,33 @@ void paged_decode_kernel(const KArgs a) {
 
   // ---- one-byte precisions ----
   {
-    const uint8_t* kp = reinterpret_cast<const uint8_t*>(a.k_fp8);
-    const uint8_t* vp = reinterpret_cast<const uint8_t*>(a.v_fp8);
     class_loop<IAK_RING_BYTE, Raw8<D>>(
         __builtin_amdgcn_ballot_w64(tag == IAK_TAG_FP8), pid,
-        [&](Raw8<D>& r, int p) { load8<D>(r, kp + (int64_t)p * PS * D, vp + (int64_t)p * PS * D, c, g); },
+        [&](Raw8<D>& r, int p) {
+          load8<D>(r, page_at<uint8_t>(a.k_fp8, p, PS * D), page_at<uint8_t>(a.v_fp8, p, PS * D), c, g);
+        },
         [&](const Raw8<D>& r, int idx) {
           const Scales s = read_scales(slot, idx);
           page_byte<D, QF32, IAK_TAG_FP8>(w, r, smul * u2f(s.s[0]), u2f(s.s[1]), kt, c, g);
         });
   }
   {
-    const uint8_t* kp = reinterpret_cast<const uint8_t*>(a.k_int8);
-    const uint8_t* vp = reinterpret_cast<const uint8_t*>(a.v_int8);
     class_loop<IAK_RING_BYTE, Raw8<D>>(
         __builtin_amdgcn_ballot_w64(tag == IAK_TAG_INT8), pid,
-        [&](Raw8<D>& r, int p) { load8<D>(r, kp + (int64_t)p * PS * D, vp + (int64_t)p * PS * D, c, g); },
+        [&](Raw8<D>& r, int p) {
+          load8<D>(r, page_at<uint8_t>(a.k_int8, p, PS * D), page_at<uint8_t>(a.v_int8, p, PS * D), c, g);
+        },
         [&](const Raw8<D>& r, int idx) {
           const Scales s = read_scales(slot, idx);
           page_byte<D, QF32, IAK_TAG_INT8>(w, r, smul * u2f(s.s[0]), u2f(s.s[1]), kt, c, g);
         });
   }
   {
-    const uint8_t* kp = reinterpret_cast<const uint8_t*>(a.k_int4r);
-    const uint8_t* vp = reinterpret_cast<const uint8_t*>(a.v_int4r);
     class_loop<IAK_RING_BYTE, Raw8<D>>(
         __builtin_amdgcn_ballot_w64(tag == IAK_TAG_INT4_RESIDUAL), pid,
-        [&](Raw8<D>& r, int p) { load8<D>(r, kp + (int64_t)p * PS * D, vp + (int64_t)p * PS * D, c, g); },
+        [&](Raw8<D>& r, int p) {
+          load8<D>(r, page_at<uint8_t>(a.k_int4r, p, PS * D), page_at<uint8_t>(a.v_int4r, p, PS * D), c, g);
+        },
         [&](const Raw8<D>& r, int idx) {
           const Scales s = read_scales(slot, idx);
           page_int4r(w, r, smul, u2f(s.s[0]), u2f(s.s[1]), u2f(s.s[2]), u2f(s.s[3]), kt, c, g);
@@ -714,14 +729,12 @@ void paged_decode_kernel(const KArgs a) {
   }
   // ---- INT4 pages: lane K dims (D/4)g.. lie in group kg, V dims (D/16)c.. in group vg ----
   {
-    const uint8_t* kp = reinterpret_cast<const uint8_t*>(a.k_int4);
-    const uint8_t* vp = reinterpret_cast<const uint8_t*>(a.v_int4);
     const int kg = ((D / 4) * g) / a.int4_group;
     const int vg = ((D / 16) * c) / a.int4_group;
     class_loop<IAK_RING_INT4, Raw4<D>>(
         __builtin_amdgcn_ballot_w64(tag == IAK_TAG_INT4), pid,
         [&](Raw4<D>& r, int p) {
-          load4<D>(r, kp + (int64_t)p * PS * (D / 2), vp + (int64_t)p * PS * (D / 2), c, g);
+          load4<D>(r, page_at<uint8_t>(a.k_int4, p, PS * D / 2), page_at<uint8_t>(a.v_int4, p, PS * D / 2), c, g);
         },
         [&](const Raw4<D>& r, int idx) {
           const Scales s = read_scales(slot, idx);
