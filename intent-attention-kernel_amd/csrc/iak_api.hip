@@ -103,14 +103,14 @@ iak_status validate(const iak_paged_decode_args* a, Plan* plan) {
   if (chunk == 0) {
     // long splits amortise the per-split prologue and partial traffic, and
     // 64-entry splits keep HBM busy from 2048 waves on. Smaller grids are
-    // latency-bound: there the splits shrink until the waves just fit the
-    // waves the GPU holds at once (one round, no tail of late waves), but not
-    // below 8 entries
+    // latency-bound: there the splits shrink until there is one workgroup per
+    // CU (the same work on every CU; a grid of 2 or 3 workgroups per CU, or an
+    // uneven one, measured slower), but not below 8 entries
     chunk = 64;
     if (rows * ((W + 63) / 64) < 2048) {
-      const long long resident = (long long)IAK_GPU_CUS * 4 * (a->q_dtype == IAK_DTYPE_F16 ? IAK_MIN_WAVES_PER_SIMD : 2);
-      const long long per_row = resident / (rows > 0 ? rows : 1);
-      chunk = per_row > 0 ? (int)((W + per_row - 1) / per_row) : 64;
+      const long long want = (long long)IAK_GPU_CUS * IAK_WAVES_PER_BLOCK;   // waves = splits x rows
+      const long long splits_per_row = (want + rows - 1) / (rows > 0 ? rows : 1);
+      chunk = (int)((W + splits_per_row - 1) / splits_per_row);
       chunk = chunk < 8 ? 8 : (chunk > 64 ? 64 : chunk);
     }
   }
