@@ -202,9 +202,11 @@ def build_workload(name: str, device: torch.device, seed: int = 1234, chunk_page
 
 # HBM bytes per decode-kernel launch (reads + writes) from rocprofv3 FETCH_SIZE /
 # WRITE_SIZE runs of this bench, each scaled by what the counter reads for a
-# 1 GiB device copy (--calibrate-copy): profiles/paged_decode_cfg3_hbm_traffic.txt.
+# 1 GiB device copy (--calibrate-copy): profiles/paged_decode_cfg3_hbm_traffic.txt and
+# profiles/paged_decode_cfg4_kernel_stats.txt.
 MEASURED_TRAFFIC = {
-    "cfg3": {"bytes": 2_115_644_502 + 13_975_363, "source": "profiles/paged_decode_cfg3_hbm_traffic.txt"},
+    "cfg3": {"bytes": 2_100_613_077 + 13_874_493, "source": "profiles/paged_decode_cfg3_hbm_traffic.txt"},
+    "cfg4": {"bytes": 189_719_832 + 2_129_920, "source": "profiles/paged_decode_cfg4_kernel_stats.txt"},
 }
 
 PAGE_BYTES = {  # K+V code bytes and scale bytes per page (D = 128, fp16 scales, INT4 groups of 32)
