@@ -147,6 +147,8 @@ template <typename T> __device__ __forceinline__ T ld(const T* p) { return *p; }
 // in parts by several instructions can be evicted and fetched again between
 // them.
 template <typename T> __device__ __forceinline__ T ld_nt(const T* p) { return __builtin_nontemporal_load(p); }
+// Streaming store: for output written once and not read back by this kernel.
+template <typename T> __device__ __forceinline__ void st_nt(T* p, T v) { __builtin_nontemporal_store(v, p); }
 
 __device__ __forceinline__ float load_scale(const void* p, int64_t idx, int dtype) {
   if (dtype == IAK_DTYPE_F32) return reinterpret_cast<const float*>(p)[idx];
