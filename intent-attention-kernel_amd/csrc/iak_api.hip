@@ -346,6 +346,11 @@ static iak_status mla_decode_impl(const iak_mla_decode_args* a, void* workspace,
   m.c16 = a->c_fp16; m.c8f = a->c_fp8; m.c8i = a->c_int8;
   m.s8f = a->c_fp8_scale; m.s8i = a->c_int8_scale; m.sd = a->scale_dtype;
   m.score_mult = a->sm_scale * 1.4426950408889634f;
+  // Compact split partials: each split's context acc / l rounded to float16
+  // (relative error <= 2^-11, 1/128 of an e4m3 code's) when every reachable
+  // page is FP8 / INT8 and the output itself is 16-bit; FP16 pages or a
+  // float32 output keep float32 partials.
+  m.acc16 = (!m.wide && a->out_dtype != IAK_DTYPE_F32) ? 1 : 0;
   if (plan.total > 0) {
     char* ws = static_cast<char*>(workspace);
     m.ws_m = reinterpret_cast<float*>(ws + plan.ws_m);

@@ -167,13 +167,14 @@ __device__ __forceinline__ uint32_t f2u(float x) { return __builtin_bit_cast(uin
 
 // --------------------------------------------------------------------------- //
 // Cross-split merge. Partial slot of split s of head c in row (b, hk):
-// ((b * Hkv + hk) * splits + s) * G + c. WPR waves (1, 2 or 4) share one
+// ((b * Hkv + hk) * splits + s) * G + c; acc is float32, or acc / l as float16
+// (A16: KArgs::acc16). WPR waves (1, 2 or 4) share one
 // (batch, query head): wave part p takes the splits s = p (mod WPR), eight at a
 // time with their loads issued together; the parts agree on the global max
 // and add their sums through LDS. A 256-thread block holds 4 / WPR heads.
 // --------------------------------------------------------------------------- //
 
-template <int D, int WPR>
+template <int D, int WPR, bool A16>
 __global__ __launch_bounds__(256) void splitk_merge_kernel(const KArgs a) {
   static_assert(WPR == 1 || WPR == 2 || WPR == 4, "1, 2 or 4 waves per head");
   constexpr int PER = D / 64;   // dims per lane
@@ -214,17 +215,24 @@ __global__ __launch_bounds__(256) void splitk_merge_kernel(const KArgs a) {
         const int64_t slot = first + (int64_t)s * a.G;
         ms[k] = a.ws_m[slot];
         ls[k] = a.ws_l[slot];
-        const float* ap = a.ws_acc + slot * D + PER * lane;
+        if constexpr (A16) {
+          const _Float16* ap = reinterpret_cast<const _Float16*>(a.ws_acc) + slot * D + PER * lane;
 #pragma unroll
-        for (int j = 0; j < PER; ++j) av[k][j] = ap[j];
+          for (int j = 0; j < PER; ++j) av[k][j] = (float)ap[j];
+        } else {
+          const float* ap = a.ws_acc + slot * D + PER * lane;
+#pragma unroll
+          for (int j = 0; j < PER; ++j) av[k][j] = ap[j];
+        }
       }
 #pragma unroll
       for (int k = 0; k < U; ++k) {
         // 0 for empty splits (m = -inf) and for the clamped reloads past the part's end
         const float wgt = i + k < n ? __builtin_amdgcn_exp2f(ms[k] - M) : 0.f;
         L += wgt * ls[k];
+        const float wa = A16 ? wgt * ls[k] : wgt;   // compact partials hold acc / l
 #pragma unroll
-        for (int j = 0; j < PER; ++j) o[j] += wgt * av[k][j];
+        for (int j = 0; j < PER; ++j) o[j] += wa * av[k][j];
       }
     }
   }
@@ -258,9 +266,15 @@ template <int D> hipError_t launch_merge(const KArgs& k, hipStream_t stream) {
   const int heads = k.B * k.Hq;
   const int wpr = k.splits >= 24 ? 4 : (k.splits >= 12 ? 2 : 1);
   const int blocks = (heads * wpr + 3) / 4;
-  if (wpr == 4) hipLaunchKernelGGL((splitk_merge_kernel<D, 4>), dim3(blocks), dim3(256), 0, stream, k);
-  else if (wpr == 2) hipLaunchKernelGGL((splitk_merge_kernel<D, 2>), dim3(blocks), dim3(256), 0, stream, k);
-  else hipLaunchKernelGGL((splitk_merge_kernel<D, 1>), dim3(blocks), dim3(256), 0, stream, k);
+  if (k.acc16) {
+    if (wpr == 4) hipLaunchKernelGGL((splitk_merge_kernel<D, 4, true>), dim3(blocks), dim3(256), 0, stream, k);
+    else if (wpr == 2) hipLaunchKernelGGL((splitk_merge_kernel<D, 2, true>), dim3(blocks), dim3(256), 0, stream, k);
+    else hipLaunchKernelGGL((splitk_merge_kernel<D, 1, true>), dim3(blocks), dim3(256), 0, stream, k);
+  } else {
+    if (wpr == 4) hipLaunchKernelGGL((splitk_merge_kernel<D, 4, false>), dim3(blocks), dim3(256), 0, stream, k);
+    else if (wpr == 2) hipLaunchKernelGGL((splitk_merge_kernel<D, 2, false>), dim3(blocks), dim3(256), 0, stream, k);
+    else hipLaunchKernelGGL((splitk_merge_kernel<D, 1, false>), dim3(blocks), dim3(256), 0, stream, k);
+  }
   return hipGetLastError();
 }
 

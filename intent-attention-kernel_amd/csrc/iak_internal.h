@@ -56,6 +56,7 @@ struct KArgs {
   float* ws_m;        // [B, Hkv, splits, G]
   float* ws_l;        // [B, Hkv, splits, G]
   float* ws_acc;      // [B, Hkv, splits, G, D]
+  int acc16;          // ws_acc holds acc / l as float16 (the MLA kernel's compact partials)
 };
 
 // ev_begin / ev_end (may be null) are recorded on `stream` around the split
@@ -90,6 +91,7 @@ struct MArgs {
   float* ws_m;        // [B, splits, H]
   float* ws_l;        // [B, splits, H]
   float* ws_acc;      // [B, splits, H, DV]
+  int acc16;          // write acc / l as float16 into ws_acc instead of acc as float32
 };
 
 hipError_t launch_mla_decode(const MArgs& m, hipStream_t stream, hipEvent_t ev_begin = nullptr,

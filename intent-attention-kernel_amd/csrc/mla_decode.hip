@@ -34,8 +34,9 @@
 //             tile through the transposing read ds_read_b64_tr_b16.
 //   One barrier per pair: pair s+1 is staged into the other tile buffer while
 //   pair s is computed. Splits write (m, l, acc) partials merged by
-//   splitk_merge_kernel; a sequence that fits one split writes the output
-//   directly.
+//   splitk_merge_kernel -- acc / l as float16 when every page is quantised and
+//   the output is 16-bit (MArgs::acc16), which halves the partial traffic;
+//   a sequence that fits one split writes the output directly.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -441,9 +442,17 @@ __global__ __launch_bounds__(512, 1) void mla_decode_kernel(const MArgs a) {
         a.ws_m[slot] = sh.mmax[hl];
         a.ws_l[slot] = sh.lsum[hl];
       }
-      float* op = a.ws_acc + slot * DV + c;
+      if (a.acc16) {
+        const float ls = sh.lsum[hl];
+        const float inv = ls > 0.f ? 1.0f / ls : 0.0f;
+        _Float16* op = reinterpret_cast<_Float16*>(a.ws_acc) + slot * DV + c;
 #pragma unroll
-      for (int db = 0; db < C::NDB; ++db) op[16 * db] = acc[db][r];
+        for (int db = 0; db < C::NDB; ++db) op[16 * db] = (_Float16)(acc[db][r] * inv);
+      } else {
+        float* op = a.ws_acc + slot * DV + c;
+#pragma unroll
+        for (int db = 0; db < C::NDB; ++db) op[16 * db] = acc[db][r];
+      }
     }
   }
 }
@@ -460,7 +469,7 @@ hipError_t launch_mla_w(const MArgs& m, hipStream_t stream, hipEvent_t ev_begin,
   KArgs k{};
   k.B = m.B; k.Hq = m.H; k.Hkv = 1; k.G = m.H; k.D = DV; k.splits = m.splits;
   k.out = m.out; k.out_dtype = m.out_dtype; k.osb = m.osb; k.osh = m.osh;
-  k.ws_m = m.ws_m; k.ws_l = m.ws_l; k.ws_acc = m.ws_acc;
+  k.ws_m = m.ws_m; k.ws_l = m.ws_l; k.ws_acc = m.ws_acc; k.acc16 = m.acc16;
   return launch_merge<DV>(k, stream);
 }
 
