@@ -343,13 +343,18 @@ __global__ __launch_bounds__(512, 1) void mla_decode_kernel(const MArgs a) {
       s1 *= a.score_mult * ps1;
       // tokens at or past the bound (the sequence's last visited page), and the
       // second page of a pair past the end
+      // second page of a pair past the end; a wave-uniform test skips the
+      // masking for the usual pair of two whole pages
       const bool live1 = 2 * st + 1 < np;
-      const int64_t lim0 = (int64_t)limit - (int64_t)(start + cur0) * PS - 4 * g;
-      const int64_t lim1 = live1 ? (int64_t)limit - (int64_t)(start + cur1) * PS - 4 * g : 0;
+      const int64_t end0 = (int64_t)(start + cur0 + 1) * PS, end1 = (int64_t)(start + cur1 + 1) * PS;
+      if (!(live1 && end0 <= limit && end1 <= limit)) {
+        const int64_t lim0 = (int64_t)limit - (end0 - PS) - 4 * g;
+        const int64_t lim1 = live1 ? (int64_t)limit - (end1 - PS) - 4 * g : 0;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        if (r >= lim0) s0[r] = -__builtin_inff();
-        if (r >= lim1) s1[r] = -__builtin_inff();
+        for (int r = 0; r < 4; ++r) {
+          if (r >= lim0) s0[r] = -__builtin_inff();
+          if (r >= lim1) s1[r] = -__builtin_inff();
+        }
       }
       const float pm = xmax16_32(fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])),
                                        fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3]))));
