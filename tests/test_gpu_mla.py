@@ -86,6 +86,44 @@ def test_mla_matches_oracle(dev, dqk, dv, voff, pps):
     assert err <= 1e-2, f"max abs err {err:.3e}"
 
 
+@pytest.mark.parametrize("dqk,dv,voff", SHAPES, ids=[f"{a}x{b}+{c}" for a, b, c in SHAPES])
+@pytest.mark.parametrize("out_name", ["float16", "bfloat16"])
+@pytest.mark.parametrize("pps", [0, 5])
+def test_mla_quantised_pools_16bit_out(dev, dqk, dv, voff, out_name, pps):
+    """FP8 / INT8 latent pools without an FP16 pool and a 16-bit output: the
+    split partials are float16 acc / l. Checked against the oracle (1e-2) and
+    against the same call with a float32 output, whose partials are float32 acc:
+    the two differ by the partials' and the output's rounding only."""
+    import torch
+    from intent_attention import LatentPools, mla_paged_decode
+    _say("mla 16-bit out", f"qk={dqk} v={dv} voff={voff} out={out_name} pages_per_split={pps}")
+    mix = {"FP8": .45, "INT8": .45, "SKIP": .1}
+    q, pools, table, counts, tags = _latent_case(700 + dqk + dv + pps, 3, 70, dqk, 40, 37, mix)
+    valid = (counts * 16).astype(np.int32)
+    valid[2] = max(1, valid[2] - 5)
+    t = {k: torch.from_numpy(v).to(dev) for k, v in pools.items()}
+    lp = LatentPools(c_fp8=t["c_fp8"], c_fp8_scale=t["c_fp8_scale"], c_int8=t["c_i8"], c_int8_scale=t["c_i8_scale"])
+    args = (torch.from_numpy(q).to(dev), lp, torch.from_numpy(table).to(dev), torch.from_numpy(counts).to(dev),
+            torch.from_numpy(tags).to(dev))
+    kw = dict(v_dim=dv, v_offset=voff, valid_tokens=torch.from_numpy(valid).to(dev), pages_per_split=pps)
+    got = mla_paged_decode(*args, out_dtype=getattr(torch, out_name), **kw)
+    full = mla_paged_decode(*args, out_dtype=torch.float32, **kw)
+    torch.cuda.synchronize()
+    assert got.dtype == getattr(torch, out_name)
+    got, full = got.float().cpu().numpy(), full.cpu().numpy()
+    ref = M.mla_paged_decode_oracle(q, pools, table, counts, tags, v_dim=dv, v_offset=voff, valid_tokens=valid)
+    assert np.all(np.isfinite(got))
+    err = float(np.abs(got - ref).max())
+    assert err <= 1e-2, f"max abs err {err:.3e}"
+    # one float16 rounding of each partial (half an ulp, <= 2^-11 of a value that
+    # is a convex combination of dequantised latents) plus the output's own rounding
+    half_ulp_out = 2.0 ** -8 if out_name == "bfloat16" else 2.0 ** -11
+    lat_max = 1.1 * float(np.abs(pools["c_fp16"].astype(np.float32)).max())
+    bound = 2.0 ** -11 * lat_max + half_ulp_out * float(np.abs(full).max()) + 1e-6
+    dif = float(np.abs(got - full).max())
+    assert dif <= bound, f"16-bit vs float32 output differ by {dif:.3e} > {bound:.3e}"
+
+
 def test_mla_fp16_pages_and_f32_scales(dev):
     import torch
     from intent_attention import mla_paged_decode
