@@ -80,6 +80,37 @@ def test_paged_decode_matches_oracle(dev, name, seed, B, Hq, Hkv, D, NP, W, mix,
                 assert np.all(got[b, hk * G:(hk + 1) * G] == 0)
 
 
+@pytest.mark.parametrize("pps", [0, 4, 7])
+def test_class_ring_boundaries(dev, pps):
+    """Rows in which every precision class has 0 .. 7 pages (around each class
+    loop's ring depth of 2, 3 or 5), shuffled together: the ring loads past a
+    class's end read a shared pad page and must contribute nothing."""
+    from tests._pools import build_pools
+    _say("ring boundaries", f"pages_per_split={pps}")
+    rng = np.random.default_rng(4242 + pps)
+    names = ["FP16", "FP8", "INT8", "INT4", "INT4_RESIDUAL"]
+    per = 8                                     # physical pages per class
+    tags = np.repeat(np.array([Dm.FP16, Dm.FP8, Dm.INT8, Dm.INT4, Dm.INT4_RESIDUAL], np.int32), per)
+    NP, D, B, Hq, Hkv = len(tags), 128, 2, 8, 4
+    pools = build_pools(rng, NP, D, tags, outliers=0.01)
+    rows = []
+    for r in range(B * Hkv):
+        ids = [k * per + int(x) for k in range(len(names)) for x in rng.integers(0, per, size=(r + 3 * k) % 8)]
+        rng.shuffle(ids)
+        rows.append(ids)
+    W = max(len(x) for x in rows)
+    table = np.zeros((B, Hkv, W), np.int32)
+    counts = np.zeros((B, Hkv), np.int32)
+    for r, ids in enumerate(rows):
+        table.flat[r * W: r * W + len(ids)] = ids
+        counts.flat[r] = len(ids)
+    q = rng.standard_normal((B, Hq, D)).astype(np.float16)
+    got = _run(dev, q, pools, table, counts, tags, pages_per_split=pps)
+    ref = Dm.paged_decode_oracle(q, pools, table, counts, tags)
+    err = float(np.abs(got - ref).max())
+    assert err <= TOL_QUANT, f"max abs err {err:.3e}"
+
+
 @pytest.mark.parametrize("W", [448, 1000])
 def test_many_rows(dev, W):
     """256 (batch, kv head) rows with ragged counts: the automatic plan (64-entry
