@@ -91,17 +91,20 @@ __device__ __forceinline__ h2 i4r_resid16_pair(uint32_t y, uint32_t magic) {
   return as_h2(and_or(y, 0x00F000F0u, magic)) + splat2((_Float16)-1152.0f);   // 1024 + 16 * 8
 }
 
-// Eight packed INT4 codes (element j = nibble j) -> four f16 pairs in element
-// order, multiplied by scale s (`magic` from magic_i4()).
+// Eight packed INT4 codes (element j = nibble j) -> four f16 pairs, multiplied
+// by scale s (`magic` from magic_i4()), in the order the nibble extraction
+// yields them: (e0, e4), (e1, e5), (e2, e6), (e3, e7). An MFMA operand built
+// from them pairs with a Q operand permuted the same way (q_int4_order).
 __device__ __forceinline__ void i4x8_to_f16(uint32_t x, h2 s, uint32_t magic, uint32_t o[4]) {
-  const h2 p04 = nib_pair(x, magic) * s;         // (e0, e4)
-  const h2 p15 = nib_pair(x >> 4, magic) * s;    // (e1, e5)
-  const h2 p26 = nib_pair(x >> 8, magic) * s;    // (e2, e6)
-  const h2 p37 = nib_pair(x >> 12, magic) * s;   // (e3, e7)
-  o[0] = pack_lo(bits(p04), bits(p15));
-  o[1] = pack_lo(bits(p26), bits(p37));
-  o[2] = pack_hi(bits(p04), bits(p15));
-  o[3] = pack_hi(bits(p26), bits(p37));
+  o[0] = bits(nib_pair(x, magic) * s);         // (e0, e4)
+  o[1] = bits(nib_pair(x >> 4, magic) * s);    // (e1, e5)
+  o[2] = bits(nib_pair(x >> 8, magic) * s);    // (e2, e6)
+  o[3] = bits(nib_pair(x >> 12, magic) * s);   // (e3, e7)
+}
+// Eight f16 values in element order -> the order of i4x8_to_f16's output.
+__device__ __forceinline__ h8 q_int4_order(h8 v) {
+  const u4 d = __builtin_bit_cast(u4, v);
+  return make_h8(pack_lo(d[0], d[2]), pack_hi(d[0], d[2]), pack_lo(d[1], d[3]), pack_hi(d[1], d[3]));
 }
 
 // Cross-lane reductions over the lanes {l, l^16, l^32, l^48} with the gfx950

@@ -729,6 +729,13 @@ void paged_decode_kernel(const KArgs a) {
   }
   // ---- INT4 pages: lane K dims (D/4)g.. lie in group kg, V dims (D/16)c.. in group vg ----
   {
+    // the last class: Q takes the element order of the INT4 K operand
+    // (i4x8_to_f16), which saves the K pairs' repacking on every page
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) {
+      w.qhi[i] = q_int4_order(w.qhi[i]);
+      if constexpr (QF32) w.qlo[i] = q_int4_order(w.qlo[i]);
+    }
     const int kg = ((D / 4) * g) / a.int4_group;
     const int vg = ((D / 16) * c) / a.int4_group;
     class_loop<IAK_RING_INT4, Raw4<D>>(
