@@ -245,11 +245,15 @@ template <int NC> __device__ __forceinline__ int kt_slot(int row, int ch) {
 template <int NC, int NI>
 __device__ __forceinline__ void k_through_lds(u4 (&k)[NI], u4* kt, int c, int g) {
   const int lane = c + 16 * g;
+  // wavefront-scope fences: the buffer's previous reads, these writes and the
+  // reads below stay in this order (the lanes exchange data through it)
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
     const int f = 64 * i + lane;
     kt[kt_slot<NC>(f / NC, f % NC)] = k[i];
   }
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   const int row = perm16(c);
 #pragma unroll
   for (int i = 0; i < NI; ++i) k[i] = kt[kt_slot<NC>(row, NI * g + i)];
