@@ -33,6 +33,12 @@ path == dense softmax attention over the gathered pages,
 test_fused_selected_quant_decode.py:142-224), brute force of the textbook
 softmax on tiny inputs, the agreement of the two restatements, and golden
 vectors written by the reference's own function (tests/golden/).
+``dequant_page`` (the FP8 / INT8 / INT4 / INT4_RESIDUAL reconstruction the
+vectorised form and the MLA oracle use) is pinned against the reference's
+fake_quantize_tensor reconstructions (golden g1) on packed pool pages and
+bit-for-bit against the g1-pinned page-granule reconstruction on seeded pools
+of every tag; planted mistakes (tiled group scales, swapped residual scale
+slots, swapped nibbles) fail those checks (tests/test_oracle_decode.py).
 """
 from __future__ import annotations
 
@@ -113,14 +119,27 @@ def dequant_page(pools: Dict, tag: int, pid: int, which: str) -> Optional[np.nda
         codes = Q.unpack_int4(pools[f"{w}_i4"][pid])
         sc = np.asarray(pools[f"{w}_i4_scale"][pid], f32).reshape(-1)
         group = codes.shape[-1] // sc.size
-        return Q._mul(codes.astype(np.float64), np.repeat(sc, group)[None, :], f32).astype(np.float64)
+        return Q._mul(codes.astype(np.float64), _channel_scales(sc, group)[None, :], f32).astype(np.float64)
     if tag == INT4_RESIDUAL:
         q1, q2 = Q.unpack_int4_residual(pools[f"{w}_i4r"][pid])
-        s = np.asarray(pools[f"{w}_i4r_scale"][pid], f32).reshape(-1)
-        base = Q._mul(q1.astype(np.float64), s[0], f32)
-        res = Q._mul(q2.astype(np.float64), s[1], f32)
+        s_base, s_resid = _residual_scales(np.asarray(pools[f"{w}_i4r_scale"][pid], f32).reshape(-1))
+        base = Q._mul(q1.astype(np.float64), s_base, f32)
+        res = Q._mul(q2.astype(np.float64), s_resid, f32)
         return Q._add(base, res, f32).astype(np.float64)
     return None
+
+
+def _channel_scales(group_scales: np.ndarray, group: int) -> np.ndarray:
+    """Scale of every channel: channels ``g*group .. g*group + group - 1`` share
+    group scale g (the group view of intent_quant.py:221-226 reduces over
+    ``group`` consecutive channels)."""
+    return np.repeat(group_scales, group)
+
+
+def _residual_scales(pair: np.ndarray):
+    """(base scale, residual scale) of an INT4_RESIDUAL page's scale slot pair
+    (intent_quant.py:282-307: recon = q1 * s1 + q2 * s2)."""
+    return pair[0], pair[1]
 
 
 def paged_decode_oracle(q, pools: Dict, page_table, page_counts, tags, *,

@@ -192,3 +192,176 @@ def test_mla_paged_oracle_equals_reference_loop():
     rows = np.concatenate([pool[p].astype(np.float64) for p in (3, 0, 11)], 0)
     assert np.abs(got[0] - M.mla_decode_closed_form(q[:1], rows)[0]).max() < 1e-12
     assert np.all(got[1] == 0)
+
+
+# --------------------------------------------------------------------------- #
+# dequant_page: the native-precision reconstruction every mixed-precision
+# parity result rests on (FP8 / INT8 / INT4 group scales / INT4_RESIDUAL)
+# --------------------------------------------------------------------------- #
+
+@pytest.fixture(scope="module")
+def g1(golden_dir):
+    return dict(np.load(os.path.join(golden_dir, "g1_fake_quantize.npz")))
+
+
+def _same(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return a.shape == b.shape and bool(np.all((a == b) | (np.isnan(a) & np.isnan(b))))
+
+
+def _one_page_pools(page, prec, group=32):
+    """Pools holding ``page`` (float16 [rows, D]) as page 0 of ``prec``, K and V alike,
+    in the packed storage dequant_page reads."""
+    from oracle import quant as Q
+    tag = {"FP8": Dm.FP8, "INT8": Dm.INT8, "INT4": Dm.INT4, "INT4_RESIDUAL": Dm.INT4_RESIDUAL}[prec]
+    codes, scales = Q.quantize_page(page, prec, group)
+    pools = {}
+    for w in ("k", "v"):
+        if prec == "FP8":
+            pools[f"{w}_fp8"], pools[f"{w}_fp8_scale"] = codes[None], scales.astype(np.float16)
+        elif prec == "INT8":
+            pools[f"{w}_i8"], pools[f"{w}_i8_scale"] = codes[None], scales.astype(np.float16)
+        elif prec == "INT4":
+            pools[f"{w}_i4"], pools[f"{w}_i4_scale"] = Q.pack_int4(codes)[None], scales[None].astype(np.float16)
+        else:
+            (q1, q2), (s1, s2) = codes, scales
+            pools[f"{w}_i4r"] = Q.pack_int4_residual(q1, q2)[None]
+            pools[f"{w}_i4r_scale"] = np.array([[s1[0], s2[0]]], np.float32)
+    return tag, pools
+
+
+def _golden_page_recon(g1, prec):
+    """The reference's fake_quantize_tensor reconstruction of the 48 x 64 page
+    (g1 x_f16 as one page): the page view for FP8 / INT8 / INT4_RESIDUAL, the
+    32-channel group view for INT4."""
+    if prec == "INT4":
+        return g1["recon_f16_group_INT4"].reshape(48, 32, 2).transpose(0, 2, 1).reshape(48, 64)
+    return g1[f"recon_f16_page_{prec}"].reshape(48, 64)
+
+
+@pytest.mark.parametrize("prec", ["FP8", "INT8", "INT4", "INT4_RESIDUAL"])
+def test_dequant_page_equals_reference_reconstruction(g1, prec):
+    """dequant_page on the packed pool page == what the reference's own
+    fake_quantize_tensor returned for that page (golden g1), for K and V."""
+    page = g1["x_f16"].reshape(48, 64)
+    tag, pools = _one_page_pools(page, prec)
+    want = _golden_page_recon(g1, prec)
+    for w in ("k", "v"):
+        assert _same(Dm.dequant_page(pools, tag, 0, w), want), (prec, w)
+    assert Dm.dequant_page(pools, Dm.SKIP, 0, "k") is None
+    assert Dm.dequant_page({"k_fp16": page[None]}, Dm.FP16, 0, "k").tolist() == page.astype(np.float64).tolist()
+
+
+def _page_mutation_cases(g1):
+    page = g1["x_f16"].reshape(48, 64)
+    # a page whose per-group absmax differs by group, so a wrong group map shows
+    skew = (page.astype(np.float32) * np.where(np.arange(64) < 32, 1.0, 3.0)).astype(np.float16)
+    return page, skew
+
+
+def test_dequant_page_planted_group_map_mistake_fails(g1, monkeypatch):
+    """np.tile instead of np.repeat over the group scales (channel c reads group
+    c mod n instead of c // group) is caught by the golden comparison."""
+    page, skew = _page_mutation_cases(g1)
+    from oracle import quant as Q
+    tag, pools = _one_page_pools(skew, "INT4")
+    codes, scales = Q.quantize_page(skew, "INT4", 32)
+    good = Q.dequantize_page(codes, scales, "INT4", 32)
+    assert _same(Dm.dequant_page(pools, tag, 0, "k"), good)
+    monkeypatch.setattr(Dm, "_channel_scales", lambda sc, group: np.tile(sc, group))
+    assert not _same(Dm.dequant_page(pools, tag, 0, "k"), good)
+    tag, pools = _one_page_pools(page, "INT4")
+    assert not _same(Dm.dequant_page(pools, tag, 0, "k"), _golden_page_recon(g1, "INT4"))
+
+
+def test_dequant_page_planted_residual_slot_swap_fails(g1, monkeypatch):
+    """Reading the INT4_RESIDUAL (base, residual) scale slots the other way
+    round is caught by the golden comparison."""
+    page = g1["x_f16"].reshape(48, 64)
+    tag, pools = _one_page_pools(page, "INT4_RESIDUAL")
+    want = _golden_page_recon(g1, "INT4_RESIDUAL")
+    assert _same(Dm.dequant_page(pools, tag, 0, "v"), want)
+    monkeypatch.setattr(Dm, "_residual_scales", lambda pair: (pair[1], pair[0]))
+    assert not _same(Dm.dequant_page(pools, tag, 0, "v"), want)
+
+
+def test_dequant_page_planted_nibble_order_mistake_fails(g1, monkeypatch):
+    """Unpacking element 2j from the high nibble (and 2j+1 from the low one) is
+    caught by the golden comparison, for INT4 and for INT4_RESIDUAL's base /
+    residual nibbles."""
+    from oracle import quant as Q
+    page = g1["x_f16"].reshape(48, 64)
+    tag4, pools4 = _one_page_pools(page, "INT4")
+    tagr, poolsr = _one_page_pools(page, "INT4_RESIDUAL")
+    real4, realr = Q.unpack_int4, Q.unpack_int4_residual
+
+    def swapped4(p):
+        c = real4(p)
+        out = c.copy()
+        out[..., 0::2], out[..., 1::2] = c[..., 1::2], c[..., 0::2]
+        return out
+
+    monkeypatch.setattr(Q, "unpack_int4", swapped4)
+    monkeypatch.setattr(Q, "unpack_int4_residual", lambda p: realr(p)[::-1])
+    assert not _same(Dm.dequant_page(pools4, tag4, 0, "k"), _golden_page_recon(g1, "INT4"))
+    assert not _same(Dm.dequant_page(poolsr, tagr, 0, "k"), _golden_page_recon(g1, "INT4_RESIDUAL"))
+
+
+@pytest.mark.parametrize("D,group", [(64, 32), (64, 64), (128, 32), (128, 64), (128, 128)])
+@pytest.mark.parametrize("scale_f32", [False, True])
+def test_dequant_page_every_tag_on_built_pools(D, group, scale_f32):
+    """Every page of seeded mixed pools (tests/_pools.build_pools: every tag, K
+    with 8-sigma outliers, one all-zero and one tiny-valued page per tag,
+    float16 or float32 scale storage) reconstructs bit-for-bit as
+    quant.dequantize_page(quant.quantize_page(page)), the g1-pinned
+    page-granule reconstruction; group scales read per channel c // group."""
+    from oracle import quant as Q
+    from tests._pools import build_pools
+    rng = np.random.default_rng(D * 1000 + group + int(scale_f32))
+    names = ["FP16", "FP8", "INT8", "INT4", "INT4_RESIDUAL", "SKIP"]
+    tagv = {"FP16": Dm.FP16, "FP8": Dm.FP8, "INT8": Dm.INT8, "INT4": Dm.INT4,
+            "INT4_RESIDUAL": Dm.INT4_RESIDUAL, "SKIP": Dm.SKIP}
+    tags = np.array([tagv[n] for n in names for _ in range(4)], np.int32)
+    NP = tags.size
+    pools = build_pools(rng, NP, D, tags, outliers=0.01, int4_group=group, scale_f32=scale_f32)
+    # page 1 of each tag all zero, page 2 tiny (float16 subnormal range); every page is
+    # re-quantised below from these sources
+    src = {"k": pools["k_fp16"].copy(), "v": pools["v_fp16"].copy()}
+    for i in range(len(names)):
+        for w in ("k", "v"):
+            src[w][4 * i + 1] = 0
+            src[w][4 * i + 2] = (rng.standard_normal((16, D)) * 1e-5).astype(np.float16)
+    for p in range(NP):
+        t = int(tags[p])
+        for w in ("k", "v"):
+            x = src[w][p]
+            if t == Dm.FP16:
+                pools[f"{w}_fp16"][p] = x
+                want = x.astype(np.float64)
+            elif t == Dm.SKIP:
+                assert Dm.dequant_page(pools, t, p, w) is None
+                continue
+            else:
+                prec = Dm.TAG_NAMES[t]
+                codes, scales = Q.quantize_page(x, prec, group)
+                sdt = np.float32 if scale_f32 else np.float16
+                if t == Dm.FP8:
+                    pools[f"{w}_fp8"][p], pools[f"{w}_fp8_scale"][p] = codes, scales[0]
+                elif t == Dm.INT8:
+                    pools[f"{w}_i8"][p], pools[f"{w}_i8_scale"][p] = codes, scales[0]
+                elif t == Dm.INT4:
+                    pools[f"{w}_i4"][p] = Q.pack_int4(codes)
+                    pools[f"{w}_i4_scale"][p] = scales.astype(sdt)
+                else:
+                    (q1, q2), (s1, s2) = codes, scales
+                    pools[f"{w}_i4r"][p] = Q.pack_int4_residual(q1, q2)
+                    pools[f"{w}_i4r_scale"][p] = (s1[0], s2[0])
+                want = Q.dequantize_page(codes, scales, prec, group)
+            got = Dm.dequant_page(pools, t, p, w)
+            assert _same(got, want), (Dm.TAG_NAMES[t], p, w)
+            if t in (Dm.INT4,) and p % 4 == 0:
+                # closed form: channel c of token r is code[r, c] * scale[c // group]
+                codes = Q.unpack_int4(pools[f"{w}_i4"][p]).astype(np.float64)
+                sc = np.asarray(pools[f"{w}_i4_scale"][p], np.float32)
+                brute = np.array([[np.float32(codes[r, c] * sc[c // group]) for c in range(D)] for r in range(16)])
+                assert _same(got, brute)
