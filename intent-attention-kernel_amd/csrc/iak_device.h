@@ -21,11 +21,27 @@ typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 
 constexpr int PS = 16;
 constexpr float RESCALE_SLACK = 8.0f;      // p <= 2^8 between rescales
-// A page whose V scale exceeds this is folded into p only with p <= 1: its
-// softmax step rescales to the page's own maximum whenever that exceeds the
-// running one (no 2^8 head-room), so p * scale stays within f16 range for every
-// f16 source value (|x| <= 65504, INT4 codes <= 8: scale <= 65504 / 7).
-constexpr float P_SCALE_LIMIT = 255.0f;
+
+// Value exponent. A page's V scale s multiplies the f16 P operand of the value
+// product; on its own p * s leaves f16's normal range for small scales (V
+// codes of tiny values: p * s in the subnormals) and large ones (overflow).
+// Each wave therefore keeps its value accumulator as acc * 2^-E for a
+// wave-uniform exponent E that follows the pages' scale exponents: P holds
+// p * (s * 2^-E), and E moves (the accumulator rescaled by an exact power of
+// two) only when a page's exponent leaves [E - EXP_WINDOW, E + EXP_WINDOW], so
+// s * 2^-E stays in [2^-EXP_WINDOW, 2^(EXP_WINDOW + 1)). The result is acc * 2^E.
+constexpr int EXP_WINDOW = 4;
+constexpr int EXP_LIMIT = 60;              // |E| <= 60: every 2^(E1 - E2) is a finite float
+
+// floor(log2(s)) of a scale, clamped to [-EXP_LIMIT, EXP_LIMIT] (zero and
+// subnormal scales give -EXP_LIMIT, inf / NaN give EXP_LIMIT).
+__device__ __forceinline__ int scale_exp(float s) {
+  const int ef = (int)((__builtin_bit_cast(uint32_t, s) >> 23) & 0xFFu);
+  const int e = ef - 127;
+  return e < -EXP_LIMIT ? -EXP_LIMIT : (e > EXP_LIMIT ? EXP_LIMIT : e);
+}
+// 2^e as a float, for |e| <= 126.
+__device__ __forceinline__ float pow2f(int e) { return __builtin_bit_cast(float, (uint32_t)(e + 127) << 23); }
 constexpr uint32_t MAGIC_I8 = 0x64646464u;  // f16 0x64xx = 1024 + xx
 constexpr uint32_t MAGIC_I4 = 0x64006400u;
 

@@ -16,7 +16,8 @@
 //   ring of page pairs (global_load_lds), SLOTS - 1 steps ahead, and each pair
 //   is staged once per workgroup into one f16 tile [token][dim]; FP8 / INT8
 //   codes convert to f16 exactly while staging, and the page scale folds into
-//   the score multiplier and into P.
+//   the score multiplier and into P (relative to the wave's value exponent E,
+//   as in the paged decode: P = p * s * 2^-E, the value sum is acc * 2^E).
 //   Wave w owns heads 16w .. 16w+15 end to end (its score and value
 //   accumulators live in VGPRs: this file is built with MFMA results in VGPRs,
 //   so the softmax rescale is plain VALU work):
@@ -255,6 +256,7 @@ __global__ __launch_bounds__(512, 1) void mla_decode_kernel(const MArgs a) {
   // per lane: running max and partial denominator of head column c (the
   // partial covers the lane's token rows; summed over g at the end)
   float m = -__builtin_inff(), l = 0.f;
+  int E = 0;   // value exponent (wave-uniform): the value sum is acc * 2^E
   // O tile db: rows = heads 4g .. 4g+3, column = value dim 16 db + c
   f4 acc[C::NDB];
 #pragma unroll
@@ -358,14 +360,18 @@ __global__ __launch_bounds__(512, 1) void mla_decode_kernel(const MArgs a) {
       }
       const float pm = xmax16_32(fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])),
                                        fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3]))));
-      // V scales above P_SCALE_LIMIT are folded into P only with p <= 1
-      const bool tight = fmaxf(ps0, ps1) > P_SCALE_LIMIT;
-      const bool grow = pm > m + (tight ? 0.0f : RESCALE_SLACK);
+      const bool grow = pm > m + RESCALE_SLACK;
       float al = 1.0f;
       if (grow) {
         al = __builtin_amdgcn_exp2f(m - pm);   // 0 on the first pair (m = -inf)
         m = pm;
       }
+      // value exponent: follows the larger page scale of the pair
+      const int e = scale_exp(fmaxf(ps0, ps1));
+      const bool emove = e > E + EXP_WINDOW || e < E - EXP_WINDOW;
+      const float efac = emove ? pow2f(E - e) : 1.0f;
+      if (emove) E = e;
+      const float vm = pow2f(-E);
       f4 p0, p1;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -378,14 +384,14 @@ __global__ __launch_bounds__(512, 1) void mla_decode_kernel(const MArgs a) {
       h8 pa;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        pa[r] = (_Float16)(p0[r] * ps0);
-        pa[4 + r] = (_Float16)(p1[r] * ps1);
+        pa[r] = (_Float16)(p0[r] * (ps0 * vm));
+        pa[4 + r] = (_Float16)(p1[r] * (ps1 * vm));
       }
       // rescale: the O rows are heads 4g + r, whose factor sits in lane 4g + r
-      if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+      if (__builtin_amdgcn_ballot_w64(grow) != 0 || emove) {
         f4 ar;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) ar[r] = __shfl(al, 4 * g + r, 64);
+        for (int r = 0; r < 4; ++r) ar[r] = __shfl(al, 4 * g + r, 64) * efac;
 #pragma unroll
         for (int db = 0; db < C::NDB; ++db) acc[db] *= ar;
       }
@@ -425,6 +431,7 @@ __global__ __launch_bounds__(512, 1) void mla_decode_kernel(const MArgs a) {
     }
   }
   __syncthreads();
+  const float vscale = pow2f(E);
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int hl = 16 * w + 4 * g + r;
@@ -432,7 +439,7 @@ __global__ __launch_bounds__(512, 1) void mla_decode_kernel(const MArgs a) {
     if (h >= a.H) continue;
     if (a.splits == 1) {
       const float ls = sh.lsum[hl];
-      const float inv = ls > 0.f ? 1.0f / ls : 0.0f;
+      const float inv = ls > 0.f ? vscale / ls : 0.0f;
       const int64_t o = (int64_t)b * a.osb + (int64_t)h * a.osh + c;
 #pragma unroll
       for (int db = 0; db < C::NDB; ++db) {
@@ -449,14 +456,14 @@ __global__ __launch_bounds__(512, 1) void mla_decode_kernel(const MArgs a) {
       }
       if (a.acc16) {
         const float ls = sh.lsum[hl];
-        const float inv = ls > 0.f ? 1.0f / ls : 0.0f;
+        const float inv = ls > 0.f ? vscale / ls : 0.0f;
         _Float16* op = reinterpret_cast<_Float16*>(a.ws_acc) + slot * DV + c;
 #pragma unroll
         for (int db = 0; db < C::NDB; ++db) op[16 * db] = (_Float16)(acc[db][r] * inv);
       } else {
         float* op = a.ws_acc + slot * DV + c;
 #pragma unroll
-        for (int db = 0; db < C::NDB; ++db) op[16 * db] = acc[db][r];
+        for (int db = 0; db < C::NDB; ++db) op[16 * db] = acc[db][r] * vscale;
       }
     }
   }

@@ -34,10 +34,11 @@
 //           (D/16)c + mb of token slots 4g..4g+3; B operand: p of head c, slots
 //           4g..4g+3 -- exactly the score result layout, converted to f16.
 //           Accumulator: lane holds head c, dims (D/4)g .. (D/4)g + D/4 - 1.
-//   Per-page scalar scales fold into the score multiplier (K) and into p (V);
-//   INT4 group scales are applied in f16 during dequantisation; INT4_RESIDUAL
-//   pages keep their base and residual codes exact and apply the two scales to
-//   the f32 products (page_int4r).
+//   Per-page scalar scales fold into the score multiplier (K) and into p (V,
+//   relative to the wave's value exponent E: P = p * s * 2^-E, the result is
+//   acc * 2^E); INT4 group scales are applied in f16 during dequantisation;
+//   INT4_RESIDUAL pages keep their base and residual codes exact and apply the
+//   two scales to the f32 products (page_int4r).
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -149,6 +150,7 @@ template <int D, bool QF32> struct Wave {
   f4 acc[D / 16];
   float m;   // running max of head c (exp2 domain), equal in the 4 lane groups
   float l;   // partial denominator over this lane's tokens
+  int E;     // value exponent (wave-uniform): the value sum is acc * 2^E
 };
 
 template <int D, bool QF32>
@@ -163,23 +165,27 @@ __device__ __forceinline__ f4 scores(const Wave<D, QF32>& w, const h8 (&ka)[D / 
 }
 
 // Online-softmax update for one page whose raw scores are `s` (lane: head c,
-// tokens 4g..4g+3); `smul` = softmax scale * log2(e) * K scale. Returns the
-// page's probabilities p (f32, <= 2^8; <= 1 when `tight`, for pages whose V
-// scale exceeds P_SCALE_LIMIT); softmax_step also multiplies them by the V
-// page scale `vmul` (1 when V carries its own scale) into the f16 P operand.
+// tokens 4g..4g+3); `smul` = softmax scale * log2(e) * K scale; `vs` = the V
+// page scale (1 when V carries its own scale). Returns the page's
+// probabilities p (f32, <= 2^8); the V multiplier of the P operand is then
+// vs * 2^-E (value_mult), in [2^-EXP_WINDOW, 2^(EXP_WINDOW + 1)).
 template <int D, bool QF32>
-__device__ __forceinline__ f4 softmax_p(Wave<D, QF32>& w, f4 s, float smul, bool tight = false) {
+__device__ __forceinline__ f4 softmax_p(Wave<D, QF32>& w, f4 s, float smul, float vs) {
   s *= smul;
   float pm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
   pm = xmax16_32(pm);
-  const bool grow = pm > w.m + (tight ? 0.0f : RESCALE_SLACK);
-  if (__builtin_amdgcn_ballot_w64(grow)) {        // wave-uniform, rare after the first page
+  const bool grow = pm > w.m + RESCALE_SLACK;
+  const int e = scale_exp(vs);                    // wave-uniform
+  const bool emove = e > w.E + EXP_WINDOW || e < w.E - EXP_WINDOW;
+  if (__builtin_amdgcn_ballot_w64(grow) || emove) {   // wave-uniform, rare after the first page
     const float mn = grow ? pm : w.m;
     const float alpha = __builtin_amdgcn_exp2f(w.m - mn);   // 0 on the first page (m = -inf)
     w.l *= alpha;
+    const float aacc = emove ? alpha * pow2f(w.E - e) : alpha;
 #pragma unroll
-    for (int mb = 0; mb < D / 16; ++mb) w.acc[mb] *= alpha;
+    for (int mb = 0; mb < D / 16; ++mb) w.acc[mb] *= aacc;
     w.m = mn;
+    if (emove) w.E = e;
   }
   f4 p;
 #pragma unroll
@@ -196,9 +202,15 @@ __device__ __forceinline__ h4 p_operand(f4 p, float vmul) {
   return make_h4(bits(a), bits(b));
 }
 
+// The P multiplier of a V scale `vs` under the wave's value exponent.
+template <int D, bool QF32> __device__ __forceinline__ float value_mult(const Wave<D, QF32>& w, float vs) {
+  return vs * pow2f(-w.E);
+}
+
 template <int D, bool QF32>
-__device__ __forceinline__ h4 softmax_step(Wave<D, QF32>& w, f4 s, float smul, float vmul) {
-  return p_operand(softmax_p(w, s, smul, vmul > P_SCALE_LIMIT), vmul);
+__device__ __forceinline__ h4 softmax_step(Wave<D, QF32>& w, f4 s, float smul, float vs) {
+  const f4 p = softmax_p(w, s, smul, vs);
+  return p_operand(p, value_mult(w, vs));
 }
 
 // V operand of row block mb from four f16-pair rows vt[t][w] = dims (2w, 2w+1)
@@ -287,9 +299,9 @@ template <int D> __device__ __forceinline__ void k8_words(const Raw8<D>& r, uint
 }
 
 // FP8 / INT8 page: codes convert to f16 exactly; the K page scale is in
-// `smul`, the V page scale `vmul` multiplies p.
+// `smul`, the V page scale `vs` multiplies p (relative to the value exponent).
 template <int D, bool QF32, int TAG>
-__device__ __forceinline__ void page_byte(Wave<D, QF32>& w, const Raw8<D>& r, float smul, float vmul, u4* kt,
+__device__ __forceinline__ void page_byte(Wave<D, QF32>& w, const Raw8<D>& r, float smul, float vs, u4* kt,
                                           int c, int g) {
   uint32_t kw[D / 16];
   k8_words<D>(r, kw, kt, c, g);
@@ -305,7 +317,7 @@ __device__ __forceinline__ void page_byte(Wave<D, QF32>& w, const Raw8<D>& r, fl
     }
     ka[i] = make_h8(o[0], o[1], o[2], o[3]);
   }
-  const h4 pb = softmax_step(w, scores(w, ka), smul, vmul);
+  const h4 pb = softmax_step(w, scores(w, ka), smul, vs);
   uint32_t vt[4][D / 32];
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
@@ -362,9 +374,9 @@ __device__ __forceinline__ void page_int4r(Wave<D, QF32>& w, const Raw8<D>& r, f
   f4 s;
 #pragma unroll
   for (int e = 0; e < 4; ++e) s[e] = sb[e] * ks0 + sr[e] * kr16;
-  const float vr16 = vs1 * 0.0625f;
-  const f4 p = softmax_p(w, s, smul, fmaxf(vs0, vr16) > P_SCALE_LIMIT);
-  const h4 pb = p_operand(p, vs0), pr = p_operand(p, vr16);
+  const f4 p = softmax_p(w, s, smul, vs0);
+  const float vm = pow2f(-w.E);
+  const h4 pb = p_operand(p, vs0 * vm), pr = p_operand(p, vs1 * 0.0625f * vm);
   const h8 pop = __builtin_shufflevector(pb, pr, 0, 1, 2, 3, 4, 5, 6, 7);
   // V: r.v[t][j] holds dims (D/16)c + 4j .. +3 of token 4g+t
 #pragma unroll
@@ -483,8 +495,9 @@ __device__ void write_result(const KArgs& a, const Split& sp, Wave<D, QT != IAK_
   const float l = xsum16_32(w.l);
   if (c >= a.G) return;
   const int h = sp.hk * a.G + c;
+  const float vscale = pow2f(w.E);   // the value sum is acc * 2^E
   if (a.splits == 1) {
-    const float inv = l > 0.f ? 1.0f / l : 0.0f;
+    const float inv = l > 0.f ? vscale / l : 0.0f;
     const int64_t base = (int64_t)sp.b * a.osb + (int64_t)h * a.osh + (D / 4) * g;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -514,7 +527,7 @@ __device__ void write_result(const KArgs& a, const Split& sp, Wave<D, QT != IAK_
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
 #pragma unroll
-    for (int mb = 0; mb < D / 16; ++mb) op[(D / 16) * r + mb] = w.acc[mb][r];
+    for (int mb = 0; mb < D / 16; ++mb) op[(D / 16) * r + mb] = w.acc[mb][r] * vscale;
   }
 }
 
@@ -678,6 +691,7 @@ void paged_decode_kernel(const KArgs a) {
   Wave<D, QF32> w;
   w.m = -__builtin_inff();
   w.l = 0.f;
+  w.E = 0;
 #pragma unroll
   for (int mb = 0; mb < D / 16; ++mb) w.acc[mb] = f4{0.f, 0.f, 0.f, 0.f};
   load_q<D, QT>(a, sp, w, c, g);

@@ -19,10 +19,12 @@ TAGS = {"FP16": Dm.FP16, "INT8": Dm.INT8, "SKIP": Dm.SKIP, "FP8": Dm.FP8, "INT4"
 def build_pools(rng: np.random.Generator, num_pages: int, D: int, tags: np.ndarray, *,
                 outliers: float = 0.0, int4_group: int = 32, scale_f32: bool = False, v_scale: float = 1.0):
     """numpy pools dict in the layout ``oracle.decode.dequant_page`` reads
-    (V values N(0, v_scale^2), rounded to float16)."""
+    (V values N(0, v_scale^2), rounded to float16; ``v_scale`` may be one
+    value per page)."""
     PS = 16
     k = rng.standard_normal((num_pages, PS, D)).astype(np.float16)
-    v = (rng.standard_normal((num_pages, PS, D)) * v_scale).astype(np.float16)
+    vsc = np.asarray(v_scale, np.float64).reshape(-1, 1, 1) if np.ndim(v_scale) else v_scale
+    v = (rng.standard_normal((num_pages, PS, D)) * vsc).astype(np.float16)
     if outliers > 0:
         m = rng.random(k.shape) < outliers
         k = np.where(m, (8.0 * np.sign(k.astype(np.float32))).astype(np.float16), k)

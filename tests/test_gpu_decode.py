@@ -153,11 +153,12 @@ def test_q_and_out_dtypes(dev, qdt, odt):
 
 @pytest.mark.parametrize("pps", [0, 16])
 def test_large_value_magnitudes(dev, pps):
-    """V values N(0, 9000^2) (|v| up to ~4e4, inside float16): V page scales
-    exceed what p (up to 2^8 between lazy rescales) times the scale can hold
-    in float16, so those pages take the softmax step with p <= 1. The output
-    matches the oracle to the same relative bar as unit-scale values, with no
-    inf or nan; K stays unit-scale, with outliers to move the running max."""
+    """V values N(0, 9000^2) (|v| up to ~4e4, inside float16): p (up to 2^8
+    between lazy rescales) times such a V page scale (~300) would overflow
+    float16; the kernel's value exponent keeps the P operand in range. The
+    output matches the oracle to the same relative bar as unit-scale values,
+    with no inf or nan; K stays unit-scale, with outliers to move the running
+    max."""
     vs = 9000.0
     _say("large V magnitudes", f"v_scale={vs} pages_per_split={pps}")
     q, pools, table, counts, tags = random_case(
@@ -168,6 +169,59 @@ def test_large_value_magnitudes(dev, pps):
     ref = Dm.paged_decode_oracle(q, pools, table, counts, tags)
     err = np.abs(got - ref).max() / vs
     assert err <= TOL_QUANT, f"max abs err / v_scale {err:.3e}"
+
+
+SMALL_V_MIXES = {"fp8": {"FP8": 1}, "int8": {"INT8": 1}, "int4r": {"INT4_RESIDUAL": 1},
+                 "mixed": {"FP16": .2, "FP8": .2, "INT8": .2, "INT4": .2, "INT4_RESIDUAL": .2}}
+
+
+def _row_rel_err(got, ref):
+    """Worst over (batch, head) rows of max|got - ref| / max|ref| in the row."""
+    d = np.abs(got - ref).max(axis=-1)
+    m = np.abs(ref).max(axis=-1)
+    live = m > 0
+    assert np.all(d[~live] == 0)
+    return float((d[live] / m[live]).max())
+
+
+@pytest.mark.parametrize("vs", [1e-3, 3e-4])
+@pytest.mark.parametrize("mix", list(SMALL_V_MIXES))
+@pytest.mark.parametrize("pps", [0, 7])
+def test_small_value_magnitudes(dev, vs, mix, pps):
+    """V values N(0, vs^2): the V page scales (absmax / 127, ~1e-5) would put
+    p * scale in the float16 subnormals; the kernel's value exponent keeps the
+    P operand normal. Relative bar 2e-3 per row (the output is ~vs)."""
+    _say("small V magnitudes", f"v_scale={vs} mix={mix} pages_per_split={pps}")
+    q, pools, table, counts, tags = random_case(
+        81 + pps, 2, 8, 2, 128, 64, 48, SMALL_V_MIXES[mix], outliers=0.01, v_scale=vs)
+    got = _run(dev, q, pools, table, counts, tags, pages_per_split=pps, out_dtype=__import__("torch").float32)
+    ref = Dm.paged_decode_oracle(q, pools, table, counts, tags)
+    err = _row_rel_err(got, ref)
+    _say(f"  worst row relative error {err:.2e}")
+    assert err <= 2e-3, f"relative err {err:.3e}"
+
+
+@pytest.mark.parametrize("pps", [0, 5])
+def test_value_scales_spanning_binades(dev, pps):
+    """Every page's V drawn at its own magnitude, 10^U(-4, 2.5) (binades -14 ..
+    8), so a split's value exponent moves up and down between pages; every
+    precision. Relative bar 2e-3 per row."""
+    from tests._pools import build_pools
+    _say("V scales spanning binades", f"pages_per_split={pps}")
+    rng = np.random.default_rng(91 + pps)
+    NP, D, B, Hq, Hkv, W = 80, 128, 2, 8, 2, 60
+    names = [Dm.FP16, Dm.FP8, Dm.INT8, Dm.INT4, Dm.INT4_RESIDUAL]
+    tags = np.array([names[i % 5] for i in range(NP)], np.int32)
+    pools = build_pools(rng, NP, D, tags, outliers=0.01, v_scale=10.0 ** rng.uniform(-4, 2.5, NP))
+    table = rng.integers(0, NP, size=(B, Hkv, W)).astype(np.int32)
+    counts = np.full((B, Hkv), W, np.int32)
+    q = rng.standard_normal((B, Hq, D)).astype(np.float16)
+    got = _run(dev, q, pools, table, counts, tags, pages_per_split=pps, out_dtype=__import__("torch").float32)
+    ref = Dm.paged_decode_oracle(q, pools, table, counts, tags)
+    assert np.all(np.isfinite(got))
+    err = _row_rel_err(got, ref)
+    _say(f"  worst row relative error {err:.2e}")
+    assert err <= 2e-3, f"relative err {err:.3e}"
 
 
 def test_misaligned_query_view(dev):

@@ -86,6 +86,34 @@ def test_mla_matches_oracle(dev, dqk, dv, voff, pps):
     assert err <= 1e-2, f"max abs err {err:.3e}"
 
 
+@pytest.mark.parametrize("lat_scale", [1e-3, 3e-4, 300.0])
+@pytest.mark.parametrize("pps", [0, 9])
+def test_mla_small_and_large_latent_magnitudes(dev, lat_scale, pps):
+    """Latents N(0, lat_scale^2) on FP8 / INT8 pages: page scales of ~1e-5
+    (small) would put p * scale in the float16 subnormals and ~10 (large)
+    times p up to 2^8 near its top; the value exponent keeps P normal.
+    Relative bar 2e-3 per (sequence, head)."""
+    import torch
+    from intent_attention import mla_paged_decode
+    _say("mla latent magnitudes", f"lat_scale={lat_scale} pages_per_split={pps}")
+    mix = {"FP8": .45, "INT8": .45, "SKIP": .1}
+    q, pools, table, counts, tags = _latent_case(910 + pps, 3, 70, 576, 40, 37, mix, lat_scale=lat_scale,
+                                                 q_scale=1.0 / lat_scale)
+    got = mla_paged_decode(torch.from_numpy(q.astype(np.float32)).to(dev), _device_pools(pools, dev),
+                           torch.from_numpy(table).to(dev), torch.from_numpy(counts).to(dev),
+                           torch.from_numpy(tags).to(dev), v_dim=512, pages_per_split=pps,
+                           out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    got = got.cpu().numpy()
+    ref = M.mla_paged_decode_oracle(q.astype(np.float32), pools, table, counts, tags, v_dim=512)
+    assert np.all(np.isfinite(got))
+    d = np.abs(got - ref).max(axis=-1)
+    m = np.abs(ref).max(axis=-1)
+    err = float((d / m).max())
+    _say(f"  worst relative error {err:.2e}")
+    assert err <= 2e-3, f"relative err {err:.3e}"
+
+
 @pytest.mark.parametrize("dqk,dv,voff", SHAPES, ids=[f"{a}x{b}+{c}" for a, b, c in SHAPES])
 @pytest.mark.parametrize("out_name", ["float16", "bfloat16"])
 @pytest.mark.parametrize("pps", [0, 5])
@@ -147,10 +175,10 @@ def test_mla_fp16_pages_and_f32_scales(dev):
 
 def test_mla_large_latent_magnitudes(dev):
     """Latent values N(0, 9000^2) (|c| up to ~4e4, inside float16) with queries
-    scaled by 1/9000: INT8 page scales exceed what p (up to 2^8 between lazy
-    rescales) times the scale can hold in float16, so those pairs take the
-    softmax step with p <= 1. Same relative bar as unit-scale latents, no inf
-    or nan."""
+    scaled by 1/9000: p (up to 2^8 between lazy rescales) times such an INT8
+    page scale (~300) would overflow float16; the kernel's value exponent keeps
+    the P operand in range. Same relative bar as unit-scale latents, no inf or
+    nan."""
     import torch
     from intent_attention import mla_paged_decode
     ls = 9000.0
