@@ -70,6 +70,80 @@ CONFIGS = {
 }
 
 
+# cfg1 (the reference's CPU-runnable case): batch 1,
+# 8 query / 8 KV heads, head_dim 64, 1024 tokens = 64 pages of 16; the router
+# selects 32 pages (0-3 ALWAYS, 56-63 RECENT, 20 drawn from 4-55 as ATTEND);
+# selected pages alternate FP16 / INT8 by ascending page id (even rank FP16),
+# INT8 with per-page, per-head absmax scales.
+CFG1 = dict(B=1, H=8, D=64, T=1024, pages=64, always=4, recent=8, attend=20)
+
+
+class _PagePlan:
+    """Duck-typed quantizer: a fixed precision per block name (the
+    alternating plan cfg1 states; the router only calls
+    assign_block_precision)."""
+
+    def __init__(self, plan):
+        self.plan = plan
+
+    def assign_block_precision(self, block):
+        from intent_attention import QuantPolicy
+        return QuantPolicy(self.plan[block.name])
+
+
+def build_cfg1(device: torch.device, seed: int = 1):
+    """cfg1 through the reference's routing path on the product API:
+    BlockLayout (one block per page) -> BlockRouter.route_layout ->
+    routing_to_kernel_metadata -> metadata_to_kernel_tensors, then the pools
+    the fused entry point reads. Physical pages are head-major: page (h, p) is
+    h * 64 + p, so the broadcast logical table is offset by h * 64 per head."""
+    from intent_attention import (BlockLayout, BlockPolicy, BlockRouter, FusedDecodeConfig, KVPrecision,
+                                  RouterConfig, SemanticBlock, metadata_to_kernel_tensors,
+                                  routing_to_kernel_metadata)
+    # the fused module's variant (float16 arithmetic and scales), fused_selected_quant_decode.py:521-542
+    from intent_attention.fused_selected_quant_decode import fake_int8_pages_from_fp16
+    c = CFG1
+    B, H, D, P = c["B"], c["H"], c["D"], c["pages"]
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, H, 1, D, generator=g).half()
+    k = torch.randn(H * P, PS, D, generator=g).half()
+    v = torch.randn(H * P, PS, D, generator=g).half()
+    mid = (torch.randperm(P - c["always"] - c["recent"], generator=g)[:c["attend"]] + c["always"]).sort().values
+    pages = list(range(c["always"])) + [int(p) for p in mid] + list(range(P - c["recent"], P))
+    rank = {p: i for i, p in enumerate(pages)}
+    blocks, plan = [], {}
+    for p in range(P):
+        if p < c["always"]:
+            pol = BlockPolicy.ALWAYS
+        elif p >= P - c["recent"]:
+            pol = BlockPolicy.RECENT
+        elif p in rank:
+            pol = BlockPolicy.ATTEND
+        else:
+            pol = BlockPolicy.SKIP
+        blocks.append(SemanticBlock(f"p{p}", p * PS, (p + 1) * PS, pol, 0.9 if pol == BlockPolicy.ATTEND else None))
+        plan[f"p{p}"] = (KVPrecision.SKIP if p not in rank else
+                         (KVPrecision.FP16 if rank[p] % 2 == 0 else KVPrecision.INT8))
+    router = BlockRouter(RouterConfig(top_k_blocks=c["attend"]), quantizer=_PagePlan(plan))
+    routed = router.route_layout(BlockLayout(blocks), c["T"])
+    meta = routing_to_kernel_metadata(routed, PS)
+    cfg = FusedDecodeConfig(page_size=PS, head_dim=D, max_selected_pages=len(pages))
+    table, prec, counts = metadata_to_kernel_tensors(meta, P, B, H, cfg, device=device)
+    table = (table + (torch.arange(H, device=device, dtype=torch.int32) * P)[None, :, None]).contiguous()
+    prec = prec.repeat(H).contiguous()
+    k, v, q = k.to(device), v.to(device), q.to(device)
+    k8, ks = fake_int8_pages_from_fp16(k)
+    v8, vs = fake_int8_pages_from_fp16(v)
+    return dict(name="cfg1", cfg=cfg, q=q, k16=k, v16=v, k8=k8, v8=v8, ks=ks, vs=vs, table=table, prec=prec,
+                counts=counts, pages=pages, meta=meta, plan=plan, layout_blocks=blocks)
+
+
+def cfg1_args(wl):
+    """Positional arguments of fused_selected_quant_decode for a cfg1 workload."""
+    return (wl["q"], wl["k16"], wl["v16"], wl["k8"], wl["v8"], wl["ks"], wl["vs"], wl["table"], wl["prec"],
+            wl["counts"], wl["cfg"])
+
+
 # --------------------------------------------------------------------------- #
 # Quantisation of synthetic pages (reference arithmetic, torch ops on device)
 # --------------------------------------------------------------------------- #

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define IAK_ABI_VERSION 1
+#define IAK_ABI_VERSION 2
 
 typedef enum {
   IAK_OK = 0,
@@ -73,7 +73,11 @@ enum { IAK_DTYPE_F16 = 0, IAK_DTYPE_F32 = 1, IAK_DTYPE_BF16 = 2 };
  *                h*G .. h*G+G-1 (G = num_q_heads / num_kv_heads) share it.
  *   page_counts  [batch, num_kv_heads] int32; entries are clamped to [0, table_width].
  *   page_tags    [num_pages] int32 caller tags, translated by tag_map[tag] to a native tag;
- *                tags outside [0, 8) and map entries outside the enum contribute nothing.
+ *                map entries outside the enum contribute nothing.
+ *   map_other_tags  0: caller tags outside [0, 8) contribute nothing (the fused
+ *                reference's `else: continue`, fused_selected_quant_decode.py:316-317);
+ *                1: they take tag_map[7] (the sibling API reads every tag but FP16
+ *                and SKIP through its INT8 pool, triton_intent_quant_attention.py:281-307).
  *   negative_ids 0: an id < 0 is an invalid page (contributes nothing);
  *                1: an id in [-num_pages, 0) means id + num_pages (torch indexing).
  *                Ids outside the pool always contribute nothing.
@@ -91,6 +95,10 @@ enum { IAK_DTYPE_F16 = 0, IAK_DTYPE_F32 = 1, IAK_DTYPE_BF16 = 2 };
  *
  *   sm_scale     softmax scale (the reference uses 1/sqrt(head_dim), :323).
  *   pages_per_split  pages one wave reduces before the cross-split merge; 0 = automatic.
+ *   valid_tokens [batch, num_kv_heads] int32 or NULL: token t of table entry e of row
+ *                (b, h) exists only if e * page_size + t < valid_tokens[b, h] (a ragged
+ *                last page); entries wholly past the bound contribute nothing. The page
+ *                memory of tokens past the bound is still read and must hold finite values.
  */
 typedef struct {
   int32_t batch, num_q_heads, num_kv_heads, head_dim, page_size, table_width;
@@ -118,6 +126,8 @@ typedef struct {
 
   float sm_scale;
   int32_t pages_per_split;
+  int32_t map_other_tags;
+  const int32_t* valid_tokens;
 } iak_paged_decode_args;
 
 /* ABI version of the loaded library (IAK_ABI_VERSION). */

@@ -61,6 +61,8 @@ iak_status validate(const iak_paged_decode_args* a, Plan* plan) {
   if (!std::isfinite(a->sm_scale)) return fail(IAK_EINVAL, "sm_scale is not finite");
   if (a->pages_per_split < 0 || a->pages_per_split > 64)
     return fail(IAK_EINVAL, "pages_per_split %d outside [0, 64]", a->pages_per_split);
+  if (a->map_other_tags != 0 && a->map_other_tags != 1)
+    return fail(IAK_EINVAL, "map_other_tags must be 0 or 1, got %d", a->map_other_tags);
   const long long rows = (long long)a->batch * a->num_kv_heads;
   if (rows > 0) {
     if (!a->q || !a->out) return fail(IAK_EINVAL, "q/out is NULL");
@@ -70,6 +72,7 @@ iak_status validate(const iak_paged_decode_args* a, Plan* plan) {
       return fail(IAK_EINVAL, "q must be 16-byte aligned with strides that are multiples of %d elements", qvec);
     if (!a->page_table || !a->page_counts) return fail(IAK_EINVAL, "page_table/page_counts is NULL");
     if (a->num_pages > 0 && !a->page_tags) return fail(IAK_EINVAL, "page_tags is NULL");
+    if (reinterpret_cast<uintptr_t>(a->valid_tokens) & 3u) return fail(IAK_EINVAL, "valid_tokens must be 4-byte aligned");
   }
   // every native precision reachable through the tag map needs its pools
   for (int t = 0; t < 8; ++t) {
@@ -277,7 +280,9 @@ static iak_status paged_decode_impl(const iak_paged_decode_args* a, void* worksp
     map |= (uint64_t)n << (8 * t);
   }
   k.tagmap = map;
+  k.other_tag = a->map_other_tags ? (int)((map >> 56) & 0xFFu) : IAK_TAG_SKIP;
   k.neg_wrap = a->negative_ids != 0;
+  k.valid = a->valid_tokens;
   k.k_fp16 = a->k_fp16; k.v_fp16 = a->v_fp16; k.k_fp8 = a->k_fp8; k.v_fp8 = a->v_fp8;
   k.k_int8 = a->k_int8; k.v_int8 = a->v_int8; k.k_int4 = a->k_int4; k.v_int4 = a->v_int4;
   k.k_int4r = a->k_int4r; k.v_int4r = a->v_int4r;

@@ -39,7 +39,9 @@ struct KArgs {
   const int32_t* counts;
   const int32_t* tags;
   uint64_t tagmap;   // byte t = native tag of caller tag t
+  int other_tag;     // native tag of caller tags outside [0, 8)
   int neg_wrap;
+  const int32_t* valid;   // [B, Hkv] token bound per row, may be null
 
   const void* k_fp16; const void* v_fp16;
   const void* k_fp8; const void* v_fp8;

@@ -151,6 +151,8 @@ template <int D, bool QF32> struct Wave {
   float m;   // running max of head c (exp2 domain), equal in the 4 lane groups
   float l;   // partial denominator over this lane's tokens
   int E;     // value exponent (wave-uniform): the value sum is acc * 2^E
+  int lim;   // tokens of the current page that exist (< PS on a ragged last page; wave-uniform)
+  int g;     // this lane's group (lane / 16)
 };
 
 template <int D, bool QF32>
@@ -170,8 +172,18 @@ __device__ __forceinline__ f4 scores(const Wave<D, QF32>& w, const h8 (&ka)[D / 
 // probabilities p (f32, <= 2^8); the V multiplier of the P operand is then
 // vs * 2^-E (value_mult), in [2^-EXP_WINDOW, 2^(EXP_WINDOW + 1)).
 template <int D, bool QF32>
-__device__ __forceinline__ f4 softmax_p(Wave<D, QF32>& w, f4 s, float smul, float vs) {
+__device__ __forceinline__ f4 softmax_p(Wave<D, QF32>& w, f4 s, float smul, float vs, bool perm = true) {
   s *= smul;
+  if (w.lim < PS) {
+    // ragged page: score slot r of lane group g is token perm16(4g + r) = 4r + g
+    // (`perm`: FP16 and one-byte pages) or 4g + r (INT4 pages); tokens at or
+    // past `lim` are left out (the page's first token always exists)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int tok = perm ? 4 * r + w.g : 4 * w.g + r;
+      if (tok >= w.lim) s[r] = -__builtin_inff();
+    }
+  }
   float pm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
   pm = xmax16_32(pm);
   const bool grow = pm > w.m + RESCALE_SLACK;
@@ -208,8 +220,8 @@ template <int D, bool QF32> __device__ __forceinline__ float value_mult(const Wa
 }
 
 template <int D, bool QF32>
-__device__ __forceinline__ h4 softmax_step(Wave<D, QF32>& w, f4 s, float smul, float vs) {
-  const f4 p = softmax_p(w, s, smul, vs);
+__device__ __forceinline__ h4 softmax_step(Wave<D, QF32>& w, f4 s, float smul, float vs, bool perm = true) {
+  const f4 p = softmax_p(w, s, smul, vs, perm);
   return p_operand(p, value_mult(w, vs));
 }
 
@@ -401,7 +413,7 @@ __device__ __forceinline__ void page_int4(Wave<D, QF32>& w, const Raw4<D>& r, fl
     i4x8_to_f16(r.k[i], ks, mg, o);
     ka[i] = make_h8(o[0], o[1], o[2], o[3]);
   }
-  const h4 pb = softmax_step(w, scores(w, ka), smul, 1.0f);
+  const h4 pb = softmax_step(w, scores(w, ka), smul, 1.0f, false);
   // V: tokens (0,1) and (2,3) interleaved per 16 bits, then one nibble per dim
   // gives the (t0, t1) and (t2, t3) halves of the A operand of that dim directly.
   h4 va[D / 16];
@@ -630,29 +642,35 @@ __device__ __forceinline__ void locate(const KArgs& a, int item, Split& sp, int&
 }
 
 // First metadata stage of an item: lane i loads table entry start + i (bounded
-// by the table width, so it needs no count) and the row's page count.
+// by the table width, so it needs no count), the row's page count and token
+// bound.
 __device__ __forceinline__ void load_entry(const KArgs& a, int unit, int start, int len, int lane, int& raw,
-                                           int& cnt) {
+                                           int& cnt, int& bnd) {
   raw = -1;
   if (lane < len && start + lane < a.W) raw = a.table[(int64_t)unit * a.W + start + lane];
   cnt = a.counts[unit];
+  bnd = a.valid ? a.valid[unit] : 0x7FFFFFFF;
 }
 
-// Second stage: drop entries at or past the row's count, validate the page id
-// (wrapping negative ids when asked) and load its tag through the tag map.
-__device__ __forceinline__ void load_tag(const KArgs& a, int raw, int cnt, int start, int len, int lane,
-                                         int& pid, int& tag, int& n) {
+// Second stage: drop entries at or past the row's count or wholly past its
+// token bound, validate the page id (wrapping negative ids when asked) and load
+// its tag through the tag map (caller tags outside [0, 8) take other_tag).
+// `lim`: tokens of the lane's entry that exist (PS unless the bound cuts it).
+__device__ __forceinline__ void load_tag(const KArgs& a, int raw, int cnt, int bnd, int start, int len, int lane,
+                                         int& pid, int& tag, int& n, int& lim) {
   cnt = cnt < 0 ? 0 : (cnt > a.W ? a.W : cnt);
   n = cnt - start < len ? cnt - start : len;
   if (n < 0) n = 0;
   pid = -1;
   tag = IAK_TAG_SKIP;
-  if (lane < n) {
+  const int64_t left = (int64_t)bnd - (int64_t)(start + lane) * PS;
+  lim = left < 0 ? 0 : (left > PS ? PS : (int)left);
+  if (lane < n && lim > 0) {
     int p = raw;
     if (a.neg_wrap && p < 0 && (int64_t)p >= -a.NP) p = (int)((int64_t)p + a.NP);
     if (p >= 0 && (int64_t)p < a.NP) {
       const int t = a.tags[p];
-      tag = (t >= 0 && t < 8) ? (int)((a.tagmap >> (8 * t)) & 0xFFu) : IAK_TAG_SKIP;
+      tag = (t >= 0 && t < 8) ? (int)((a.tagmap >> (8 * t)) & 0xFFu) : a.other_tag;
       pid = p;
     }
   }
@@ -679,19 +697,23 @@ void paged_decode_kernel(const KArgs a) {
   u4* kt = kt_all[threadIdx.x >> 6];
 
   Split sp;
-  int pid, tag;
+  int pid, tag, lim;
   uint32_t slot[4];
   {
-    int start, unit, raw, cnt;
+    int start, unit, raw, cnt, bnd;
     locate(a, item, sp, start, unit);
-    load_entry(a, unit, start, a.chunk, lane, raw, cnt);
-    load_tag(a, raw, cnt, start, a.chunk, lane, pid, tag, sp.n);
+    load_entry(a, unit, start, a.chunk, lane, raw, cnt, bnd);
+    load_tag(a, raw, cnt, bnd, start, a.chunk, lane, pid, tag, sp.n, lim);
   }
 
   Wave<D, QF32> w;
   w.m = -__builtin_inff();
   w.l = 0.f;
   w.E = 0;
+  w.lim = PS;
+  w.g = g;
+  // tokens of the page of lane idx that exist
+  auto page_lim = [&](int idx) { return __builtin_amdgcn_readlane(lim, idx); };
 #pragma unroll
   for (int mb = 0; mb < D / 16; ++mb) w.acc[mb] = f4{0.f, 0.f, 0.f, 0.f};
   load_q<D, QT>(a, sp, w, c, g);
@@ -705,7 +727,10 @@ void paged_decode_kernel(const KArgs a) {
         [&](Raw16<D>& r, int p) {
           load16<D>(r, page_at<_Float16>(a.k_fp16, p, PS * D * 2), page_at<_Float16>(a.v_fp16, p, PS * D * 2), c, g);
         },
-        [&](const Raw16<D>& r, int) { page_fp16(w, r, smul, kt, c, g); });
+        [&](const Raw16<D>& r, int idx) {
+          w.lim = page_lim(idx);
+          page_fp16(w, r, smul, kt, c, g);
+        });
   }
   // the scales are first needed by the classes below: loaded here, their round
   // trip overlaps the next class's ring fill instead of preceding the FP16 pages
@@ -720,6 +745,7 @@ void paged_decode_kernel(const KArgs a) {
         },
         [&](const Raw8<D>& r, int idx) {
           const Scales s = read_scales(slot, idx);
+          w.lim = page_lim(idx);
           page_byte<D, QF32, IAK_TAG_FP8>(w, r, smul * u2f(s.s[0]), u2f(s.s[1]), kt, c, g);
         });
   }
@@ -731,6 +757,7 @@ void paged_decode_kernel(const KArgs a) {
         },
         [&](const Raw8<D>& r, int idx) {
           const Scales s = read_scales(slot, idx);
+          w.lim = page_lim(idx);
           page_byte<D, QF32, IAK_TAG_INT8>(w, r, smul * u2f(s.s[0]), u2f(s.s[1]), kt, c, g);
         });
   }
@@ -742,6 +769,7 @@ void paged_decode_kernel(const KArgs a) {
         },
         [&](const Raw8<D>& r, int idx) {
           const Scales s = read_scales(slot, idx);
+          w.lim = page_lim(idx);
           page_int4r(w, r, smul, u2f(s.s[0]), u2f(s.s[1]), u2f(s.s[2]), u2f(s.s[3]), kt, c, g);
         });
   }
@@ -763,6 +791,7 @@ void paged_decode_kernel(const KArgs a) {
         },
         [&](const Raw4<D>& r, int idx) {
           const Scales s = read_scales(slot, idx);
+          w.lim = page_lim(idx);
           page_int4(w, r, smul, group_scale(s.s[0], s.s[1], kg), group_scale(s.s[2], s.s[3], vg));
         });
   }

@@ -14,7 +14,7 @@ from typing import Optional
 _HERE = os.path.dirname(os.path.abspath(__file__))
 # IAK_LIBRARY selects another build of the same ABI (e.g. a tuning variant)
 LIB_PATH = os.environ.get("IAK_LIBRARY") or os.path.join(_HERE, "libiak.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 IAK_OK, IAK_EINVAL, IAK_ENOTSUP, IAK_EHIP = 0, 1, 2, 3
 
@@ -48,6 +48,8 @@ class PagedDecodeArgs(ctypes.Structure):
         ("k_int4r_scale", c_void_p), ("v_int4r_scale", c_void_p),
         ("sm_scale", c_float),
         ("pages_per_split", c_i32),
+        ("map_other_tags", c_i32),
+        ("valid_tokens", c_void_p),
     ]
 
 

@@ -115,18 +115,24 @@ def paged_decode(q: torch.Tensor, pools: PagePools, page_table: torch.Tensor, pa
                  page_tags: torch.Tensor, *, tag_map: Optional[Sequence[int]] = None,
                  negative_ids: bool = False, sm_scale: Optional[float] = None,
                  out: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None,
-                 pages_per_split: int = 0) -> torch.Tensor:
+                 pages_per_split: int = 0, map_other_tags: bool = False,
+                 valid_tokens: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Selected-page decode attention on the GPU.
 
     q [B, Hq, D] (f16 / f32 / bf16, any strides with unit last stride);
     page_table [B, Hkv, W] int32; page_counts [B, Hkv] int32; page_tags [NP]
     int32 caller tags mapped through ``tag_map`` (8 entries of IAK_TAG_*);
     the default maps each native tag whose pools are present to itself and
-    every other tag to SKIP (contributes nothing). Query head h uses row
-    h // (Hq // Hkv). Returns out [B, Hq, D].
+    every other tag to SKIP (contributes nothing). Caller tags outside
+    [0, 8) contribute nothing, or take ``tag_map[7]`` with
+    ``map_other_tags``. Query head h uses row h // (Hq // Hkv).
+    ``valid_tokens`` [B, Hkv] int32 (optional): token t of table entry e of a
+    row exists only if e * 16 + t < valid_tokens[row] (a ragged last page).
+    Returns out [B, Hq, D].
     """
     plan = make_plan(q, pools, page_table, page_counts, page_tags, tag_map=tag_map, negative_ids=negative_ids,
-                     sm_scale=sm_scale, out=out, out_dtype=out_dtype, pages_per_split=pages_per_split)
+                     sm_scale=sm_scale, out=out, out_dtype=out_dtype, pages_per_split=pages_per_split,
+                     map_other_tags=map_other_tags, valid_tokens=valid_tokens)
     plan.run()
     return plan.out
 
@@ -135,7 +141,8 @@ def make_plan(q: torch.Tensor, pools: PagePools, page_table: torch.Tensor, page_
               page_tags: torch.Tensor, *, tag_map: Optional[Sequence[int]] = None,
               negative_ids: bool = False, sm_scale: Optional[float] = None,
               out: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None,
-              pages_per_split: int = 0) -> "DecodePlan":
+              pages_per_split: int = 0, map_other_tags: bool = False,
+              valid_tokens: Optional[torch.Tensor] = None) -> "DecodePlan":
     """Validate the arguments of ``paged_decode`` once; the returned plan
     re-launches the decode on the same tensors with ``run()``."""
     if q.dim() != 3:
@@ -151,7 +158,13 @@ def make_plan(q: torch.Tensor, pools: PagePools, page_table: torch.Tensor, page_
     if page_tags.dim() != 1:
         raise ValueError(f"page_precision must have shape [num_pages], got {tuple(page_tags.shape)}")
     NP = int(page_tags.shape[0])
-    dev = require_device(q, page_table, page_counts, page_tags, *pools.tensors().values())
+    extra = () if valid_tokens is None else (valid_tokens,)
+    dev = require_device(q, page_table, page_counts, page_tags, *extra, *pools.tensors().values())
+    if valid_tokens is not None:
+        if tuple(valid_tokens.shape) != (B, Hkv) or valid_tokens.dtype != torch.int32:
+            raise ValueError(f"valid_tokens must be int32 [{B}, {Hkv}], got {tuple(valid_tokens.shape)} "
+                             f"{valid_tokens.dtype}")
+        valid_tokens = valid_tokens.contiguous()
     for name, t in (("page_table", page_table), ("page_counts", page_counts), ("page_precision", page_tags)):
         if t.dtype != torch.int32:
             raise ValueError(f"{name} must be int32, got {t.dtype}")
@@ -223,8 +236,10 @@ def make_plan(q: torch.Tensor, pools: PagePools, page_table: torch.Tensor, page_
     a.int4_group = grp
     a.sm_scale = (1.0 / math.sqrt(D)) if sm_scale is None else float(sm_scale)
     a.pages_per_split = int(pages_per_split)
+    a.map_other_tags = 1 if map_other_tags else 0
+    a.valid_tokens = _ptr(valid_tokens)
 
-    return DecodePlan(a, dev, out, keep=(q, page_table, page_counts, page_tags, pools))
+    return DecodePlan(a, dev, out, keep=(q, page_table, page_counts, page_tags, valid_tokens, pools))
 
 
 class DecodePlan:

@@ -1,0 +1,116 @@
+"""``intent_quant_attention_reference`` of the reference
+(intent_quant_attention.py:20-119) with its attention on the HIP decode.
+
+Semantics kept from the reference, step for step:
+
+* ``causal=True`` raises NotImplementedError (:29-35); the layout is
+  validated against ``k.size(-2)`` (:37-38); no selected block gives
+  ``zeros_like(q)`` (:40-45);
+* each selected block (layout order) takes ``quantizer.assign_block_precision``
+  and is fake-quantised with ``fake_quantize_tensor`` at the reference's
+  granule: one scale per channel over the block's ``[..., T_blk, D]`` slice
+  (:56-75). A block whose precision is SKIP contributes zero K/V rows, which
+  take softmax mass like any other row;
+* the reconstructions are concatenated in block order (torch's type promotion:
+  float16 FP16 blocks next to float32 quantised ones give float32) and
+  attended densely (:82-85); a query dtype that differs from the
+  concatenation's raises the RuntimeError of the reference's matmul;
+* ``return_debug`` returns the same dictionary keys and values: byte
+  estimates, per-block precision and reconstruction MSE, and the output's
+  error against attention over the unquantised selected tokens (:87-118).
+
+The fake quantisation runs as torch ops on the input's device (the product
+``intent_quant.fake_quantize_tensor``, the reference's arithmetic); the
+attention is ``reference.dense_attention`` on libiak's paged decode kernel.
+Device tensors only: host tensors raise RuntimeError.
+"""
+from __future__ import annotations
+
+from typing import Any, Dict, List
+
+import torch
+
+from .block_metadata import BlockLayout
+from .decode_core import require_device
+from .intent_quant import IntentQuantizer, KVPrecision, QuantPolicy, compute_quant_error, \
+    fake_dequantize_tensor, fake_quantize_tensor
+from .reference import dense_attention
+
+
+def _empty_debug(layout: BlockLayout, kv_tokens: int) -> Dict[str, Any]:
+    """Debug dictionary of a layout that selects nothing (:120-133)."""
+    return {
+        "selected_block_names": [], "selected_tokens": 0, "precision_by_block": {},
+        "estimated_fp16_bytes": 0, "estimated_quant_bytes": 0, "bytes_saved_pct": 0.0,
+        "reconstruction_mse_k": {}, "reconstruction_mse_v": {},
+        "output_mse_vs_fp16_selected": 0.0, "output_cosine_vs_fp16_selected": 1.0,
+        "output_max_abs_error_vs_fp16_selected": 0.0,
+    }
+
+
+def intent_quant_attention_reference(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layout: BlockLayout,
+                                     quantizer: IntentQuantizer, causal: bool = False,
+                                     return_debug: bool = False) -> Any:
+    """Fake-quant -> dequant -> dense attention over the layout's selected blocks."""
+    if causal:
+        raise NotImplementedError(
+            "Causal IntentQuant attention requires explicit query_positions "
+            "because selected KV indices are in original context coordinates. "
+            "The current CPU reference supports non-causal selected-block "
+            "attention only.")
+    require_device(q, k, v, what="IntentQuant attention")
+    kv_tokens = k.size(-2)
+    layout.validate(kv_tokens)
+    blocks = layout.selected_blocks()
+    if not blocks:
+        out = torch.zeros_like(q)
+        return (out, _empty_debug(layout, kv_tokens)) if return_debug else out
+
+    head_dim = q.size(-1)
+    precision_by_block: Dict[str, str] = {}
+    k_parts: List[torch.Tensor] = []
+    v_parts: List[torch.Tensor] = []
+    k_err: Dict[str, float] = {}
+    v_err: Dict[str, float] = {}
+    fp16_bytes = 0
+    quant_bytes = 0
+    for block in blocks:
+        bk = k[..., block.start:block.end, :].contiguous()
+        bv = v[..., block.start:block.end, :].contiguous()
+        n = block.end - block.start
+        policy: QuantPolicy = quantizer.assign_block_precision(block)
+        precision_by_block[block.name] = policy.precision.value
+        fp16_bytes += 2 * n * head_dim * 2
+        quant_bytes += int(round(2 * n * head_dim * policy.estimated_bytes_per_value))
+        kq, kmeta = fake_quantize_tensor(bk, policy.precision)
+        vq, vmeta = fake_quantize_tensor(bv, policy.precision)
+        kd, vd = fake_dequantize_tensor(kq, kmeta), fake_dequantize_tensor(vq, vmeta)
+        k_parts.append(kd)
+        v_parts.append(vd)
+        if policy.precision != KVPrecision.SKIP:
+            k_err[block.name] = compute_quant_error(bk, kd)["mse"]
+            v_err[block.name] = compute_quant_error(bv, vd)["mse"]
+
+    output = dense_attention(q, torch.cat(k_parts, dim=-2), torch.cat(v_parts, dim=-2), causal=False)
+    if not return_debug:
+        return output
+
+    sel_k = torch.cat([k[..., b.start:b.end, :].contiguous() for b in blocks], dim=-2)
+    sel_v = torch.cat([v[..., b.start:b.end, :].contiguous() for b in blocks], dim=-2)
+    fp16_out = dense_attention(q, sel_k, sel_v, causal=False)
+    err = compute_quant_error(fp16_out, output)
+    saved = (1.0 - quant_bytes / max(fp16_bytes, 1)) * 100.0 if fp16_bytes > 0 else 0.0
+    debug: Dict[str, Any] = {
+        "selected_block_names": [b.name for b in blocks],
+        "selected_tokens": layout.selected_token_count(),
+        "precision_by_block": precision_by_block,
+        "estimated_fp16_bytes": fp16_bytes,
+        "estimated_quant_bytes": quant_bytes,
+        "bytes_saved_pct": round(saved, 2),
+        "reconstruction_mse_k": k_err,
+        "reconstruction_mse_v": v_err,
+        "output_mse_vs_fp16_selected": err["mse"],
+        "output_cosine_vs_fp16_selected": err["cosine_similarity"],
+        "output_max_abs_error_vs_fp16_selected": err["max_abs_error"],
+    }
+    return output, debug

@@ -11,9 +11,10 @@ uses Triton (the module that keeps the reference's import path,
 ``triton_intent_quant_attention``, re-exports these names).
 
 Semantics kept from the reference kernel (:255-335): q [B, H, D] in, output
-of q's dtype; tag 0 reads the FP16 pool, tags 1-4 (FP8, INT8, INT4,
-INT4_RESIDUAL) read the INT8 pool with the per-page scale unless native pools
-for them are passed; tag 5 (SKIP), a negative page id or any other tag
+of q's dtype; tag 0 reads the FP16 pool; every other tag but 5 (SKIP) -- 1-4
+(FP8, INT8, INT4, INT4_RESIDUAL), 6, 7, negative or larger tags -- reads the
+INT8 pool with the per-page scale (:281-307), except that tags 1, 3 and 4
+read their native pools when those are passed; tag 5 or a negative page id
 contributes nothing; a row with nothing visited gives 0.
 """
 from __future__ import annotations
@@ -148,8 +149,9 @@ def intent_quant_decode_attention_triton(
 
     pools = PagePools(k_fp16=k_pages_fp16, v_fp16=v_pages_fp16, k_int8=k_pages_i8, v_int8=v_pages_i8,
                       k_int8_scale=k_i8_scales, v_int8_scale=v_i8_scales)
-    # caller tag -> native tag: 1..4 read INT8 unless a native pool is given
-    tag_map = [N.TAG_FP16, N.TAG_INT8, N.TAG_INT8, N.TAG_INT8, N.TAG_INT8, N.TAG_SKIP, N.TAG_SKIP, N.TAG_SKIP]
+    # caller tag -> native tag: all but 0 and 5 read INT8 (tags outside [0, 8) take
+    # slot 7's) unless a native pool is given for 1, 3 or 4
+    tag_map = [N.TAG_FP16, N.TAG_INT8, N.TAG_INT8, N.TAG_INT8, N.TAG_INT8, N.TAG_SKIP, N.TAG_INT8, N.TAG_INT8]
     if native_pools is not None:
         for name in ("k_fp8", "v_fp8", "k_fp8_scale", "v_fp8_scale", "k_int4", "v_int4", "k_int4_scale",
                      "v_int4_scale", "int4_group", "k_int4r", "v_int4r", "k_int4r_scale", "v_int4r_scale"):
@@ -160,7 +162,7 @@ def intent_quant_decode_attention_triton(
                 tag_map[int(caller)] = native
     return paged_decode(q, pools, page_ids, page_count, page_precision, tag_map=tag_map,
                         negative_ids=False, sm_scale=1.0 / math.sqrt(dim), out=out,
-                        pages_per_split=pages_per_split)
+                        pages_per_split=pages_per_split, map_other_tags=True)
 
 
 def fake_int8_pages_from_fp16(pages: torch.Tensor, *, eps: float = 1e-6) -> Tuple[torch.Tensor, torch.Tensor]:

@@ -7,8 +7,8 @@ latent rows of the pages listed in a 1-D ``page_table`` shared by the batch
 (page ``p`` = rows ``p*page_size .. (p+1)*page_size - 1`` of ``C [T, d_c]``),
 softmax scale ``1/sqrt(d_c)``, and the context is projected by ``W_VO_fused``;
 zeros when the table is empty. The selected rows are gathered in table order
-into 16-row pages of float16 (any ``page_size``; a ragged last page is bounded
-by the kernel's token count), ``d_c`` is zero-padded to a supported width
+into 16-row pages of float16 (any ``page_size``; the last page of ``C`` may be
+shorter, and the gathered rows are bounded by the kernel's token count), ``d_c`` is zero-padded to a supported width
 (64, 128, 256, 512 or 576), and the projection is one float32 GEMM. Host
 tensors raise RuntimeError: there is no CPU path in this package.
 """
@@ -50,11 +50,14 @@ def mla_latent_context(q_absorb: torch.Tensor, C: torch.Tensor, page_table: torc
     n_sel = ids.numel()
     if n_sel == 0:
         return torch.zeros(batch, q_len, d_c, dtype=torch.float32, device=dev)
-    n_src = C.shape[0] // page_size
+    # page p is rows p*page_size .. (p+1)*page_size - 1 of C, the last page of
+    # C possibly shorter (the reference slices C[p*ps:(p+1)*ps])
+    n_src = (C.shape[0] + page_size - 1) // page_size
     if int(ids.min()) < 0 or int(ids.max()) >= n_src:
         raise ValueError(f"page ids must lie in [0, {n_src})")
     width = next(w for w in _WIDTHS if w >= d_c)
     rows = (ids[:, None] * page_size + torch.arange(page_size, device=dev)).reshape(-1)
+    rows = rows[rows < C.shape[0]]
     T = rows.numel()
     n16 = (T + 15) // 16
     lat = torch.zeros(n16 * 16, width, dtype=torch.float16, device=dev)

@@ -144,7 +144,7 @@ def _residual_scales(pair: np.ndarray):
 
 def paged_decode_oracle(q, pools: Dict, page_table, page_counts, tags, *,
                         sm_scale: Optional[float] = None, dtype=np.float64,
-                        neg_ids_wrap: bool = False):
+                        neg_ids_wrap: bool = False, valid_tokens=None):
     """Vectorised selected-page decode with GQA and native precisions.
 
     ``q`` [B, Hq, D]; ``page_table`` [B, Hkv, W]; ``page_counts`` [B, Hkv];
@@ -152,7 +152,11 @@ def paged_decode_oracle(q, pools: Dict, page_table, page_counts, tags, *,
     softmax scale defaults to 1/sqrt(D) (reference :323). With
     ``neg_ids_wrap`` a page id in [-NP, 0) means ``id + NP`` (torch indexing
     in the fused reference); otherwise negative ids are invalid (the sibling
-    Triton API, triton_intent_quant_attention.py:280).
+    Triton API, triton_intent_quant_attention.py:280). ``valid_tokens``
+    [B, Hkv] (this build's extension for a ragged last page): token t of
+    table entry e exists only if ``e * PS + t < valid_tokens[b, hk]``.
+    Pinned by: brute-force softmax over explicit token lists
+    (tests/test_oracle_decode.py).
     """
     q = np.asarray(q)
     B, Hq, D = q.shape
@@ -164,6 +168,7 @@ def paged_decode_oracle(q, pools: Dict, page_table, page_counts, tags, *,
     for b in range(B):
         for hk in range(Hkv):
             n = min(int(page_counts[b, hk]), W)
+            bound = None if valid_tokens is None else int(valid_tokens[b, hk])
             ks, vs = [], []
             for p in range(n):
                 pid = int(page_table[b, hk, p])
@@ -174,8 +179,11 @@ def paged_decode_oracle(q, pools: Dict, page_table, page_counts, tags, *,
                 k = dequant_page(pools, int(tags[pid]), pid, "k")
                 if k is None:
                     continue
-                ks.append(k)
-                vs.append(dequant_page(pools, int(tags[pid]), pid, "v"))
+                keep = k.shape[0] if bound is None else max(0, min(k.shape[0], bound - p * k.shape[0]))
+                if keep == 0:
+                    continue
+                ks.append(k[:keep])
+                vs.append(dequant_page(pools, int(tags[pid]), pid, "v")[:keep])
             if not ks:
                 continue
             K = np.concatenate(ks, 0).astype(dtype)

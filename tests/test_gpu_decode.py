@@ -354,7 +354,9 @@ def test_fused_api_reference_test_facts(dev):
 
 
 def test_sibling_api_triton_numbering(dev):
-    """intent_quant_decode_attention_triton: tags 0 FP16, 1-4 read the INT8 pool, 5 / id<0 invalid."""
+    """intent_quant_decode_attention_triton: tag 0 FP16; 5 or an id < 0 invalid;
+    every other tag -- 1-4, 6, 7, negative, 8 and above -- reads the INT8 pool
+    (triton_intent_quant_attention.py:281-307)."""
     import torch
     from intent_attention import (IntentQuantKernelConfig, TritonKVPrecision, intent_quant_decode_attention_triton,
                                   make_page_tables_from_selected_pages)
@@ -362,11 +364,15 @@ def test_sibling_api_triton_numbering(dev):
     rng = np.random.default_rng(9)
     B, H, D, NP = 2, 4, 64, 12
     q, pools, table, counts, tags = random_case(51, B, H, H, D, NP, 8, {"FP16": .5, "INT8": .5}, scale_f32=True)
-    ttags = np.where(tags == Dm.FP16, 0, rng.choice([1, 2, 3, 4], size=NP)).astype(np.int32)
+    ttags = np.where(tags == Dm.FP16, 0, rng.choice([1, 2, 3, 4, 6, 7, -3, 9, 1 << 20], size=NP)).astype(np.int32)
     ttags[0] = int(TritonKVPrecision.SKIP)
-    sel = torch.tensor([0, 3, 5, 7, 2, 11], dtype=torch.int32)
-    ids, cnt = make_page_tables_from_selected_pages(sel, B, H, max_selected_pages=8)
-    cfg = IntentQuantKernelConfig(page_size=16, head_dim=D, max_selected_pages=8)
+    sel = torch.tensor([0, 3, 5, 7, 2, 11, 1, 4, 6, 8], dtype=torch.int32)
+    quant_sel = [p for p in sel.tolist()[1:] if tags[p] != Dm.FP16]
+    assert len(quant_sel) >= 3
+    for p, t in zip(quant_sel, (6, -3, 1 << 20, 7, 9)):
+        ttags[p] = t                           # tags outside the numbering on selected pages
+    ids, cnt = make_page_tables_from_selected_pages(sel, B, H, max_selected_pages=12)
+    cfg = IntentQuantKernelConfig(page_size=16, head_dim=D, max_selected_pages=12)
     t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)  # noqa: E731
     out = intent_quant_decode_attention_triton(
         t(q), t(pools["k_fp16"]), t(pools["v_fp16"]), t(pools["k_i8"]), t(pools["v_i8"]),

@@ -365,3 +365,35 @@ def test_dequant_page_every_tag_on_built_pools(D, group, scale_f32):
                 sc = np.asarray(pools[f"{w}_i4_scale"][p], np.float32)
                 brute = np.array([[np.float32(codes[r, c] * sc[c // group]) for c in range(D)] for r in range(16)])
                 assert _same(got, brute)
+
+
+def test_valid_tokens_bound_equals_brute_force():
+    """paged_decode_oracle with a per-row token bound (a ragged last page) ==
+    the textbook softmax over the explicit list of (entry, token) pairs the
+    bound keeps; a bound at a page boundary equals truncating the count."""
+    rng = np.random.default_rng(17)
+    B, Hq, Hkv, D, PS, NP, W = 2, 4, 2, 16, 16, 9, 6
+    pools = {"k_fp16": rng.standard_normal((NP, PS, D)).astype(np.float16),
+             "v_fp16": rng.standard_normal((NP, PS, D)).astype(np.float16)}
+    tags = np.array([0, 0, 2, 0, 0, 0, 0, 0, 0], np.int32)
+    table = rng.integers(0, NP, size=(B, Hkv, W)).astype(np.int32)
+    counts = np.array([[6, 4], [5, 6]], np.int32)
+    bound = np.array([[83, 16], [0, 95]], np.int32)
+    q = rng.standard_normal((B, Hq, D)).astype(np.float16)
+    out = Dm.paged_decode_oracle(q, pools, table, counts, tags, valid_tokens=bound)
+    for b in range(B):
+        for h in range(Hq):
+            hk = h // 2
+            toks = [(int(table[b, hk, e]), t) for e in range(counts[b, hk]) for t in range(PS)
+                    if tags[table[b, hk, e]] != 2 and e * PS + t < bound[b, hk]]
+            if not toks:
+                assert np.all(out[b, h] == 0)
+                continue
+            s = np.array([float(np.dot(q[b, h].astype(np.float64), pools["k_fp16"][p, t].astype(np.float64)))
+                          for p, t in toks]) / math.sqrt(D)
+            w = np.exp(s - s.max())
+            ref = (w[:, None] * np.array([pools["v_fp16"][p, t] for p, t in toks], np.float64)).sum(0) / w.sum()
+            assert np.allclose(out[b, h], ref, rtol=0, atol=1e-12)
+    full = Dm.paged_decode_oracle(q, pools, table, np.minimum(counts, 1), tags)
+    cut = Dm.paged_decode_oracle(q, pools, table, counts, tags, valid_tokens=np.full((B, Hkv), 16))
+    assert np.array_equal(full, cut)
