@@ -156,6 +156,22 @@ iak_status iak_paged_decode(const iak_paged_decode_args* args, void* workspace,
 iak_status iak_paged_decode_timed(const iak_paged_decode_args* args, void* workspace,
                                   size_t workspace_bytes, void* stream, void* ev_begin, void* ev_end);
 
+/* Maximum split-K partial bytes iak_paged_decode_noalloc serves from its
+ * library-owned scratch (what iak_paged_decode_workspace reports for the same
+ * arguments). */
+#define IAK_NOALLOC_SCRATCH_BYTES (16u << 20)
+
+/* iak_paged_decode without a caller workspace and without any allocation: the
+ * split-K partials live in a library-owned device array of
+ * IAK_NOALLOC_SCRATCH_BYTES (one per GPU, held until the process ends).
+ * Arguments whose partials need more return IAK_EINVAL. Every call on a GPU
+ * shares that GPU's array, so calls that overlap on one GPU (concurrent
+ * streams or threads) race; calls ordered on one stream do not. No
+ * counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). */
+iak_status iak_paged_decode_noalloc(const iak_paged_decode_args* args, void* stream);
+
 /*
  * MLA latent decode: every query head attends to one shared compressed KV
  * (latent rows of qk_dim values; dims v_offset .. v_offset + v_dim - 1 of a

@@ -6,6 +6,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 #include "iak.h"
 #include "iak_internal.h"
@@ -226,6 +227,42 @@ iak_status validate_mla(const iak_mla_decode_args* a, MPlan* plan) {
 
 }  // namespace
 
+// Split-K partials of iak_paged_decode_noalloc: a library-owned device array
+// (each GPU holds its own copy). In host code `scratch` names a host-side
+// stand-in, not device memory: kernels get the device address that
+// hipGetSymbolAddress returns for the current GPU (scratch_address).
+static __device__ __align__(256) unsigned char scratch[IAK_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[MAX_DEVICES] = {};
+
+// Device address of `scratch` on GPU `dev`, looked up once per device (with
+// that device current) and kept.
+iak_status scratch_address(int dev, void** out) {
+  if (dev < 0 || dev >= MAX_DEVICES) return fail(IAK_EINVAL, "device %d outside [0, %d)", dev, MAX_DEVICES);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    int cur = -1;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return fail(IAK_EHIP, "hipGetDevice failed: %s", hipGetErrorString(e));
+    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess)
+      return fail(IAK_EHIP, "hipSetDevice(%d) failed: %s", dev, hipGetErrorString(e));
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) (void)hipSetDevice(cur);
+    if (e != hipSuccess || !p)
+      return fail(IAK_EHIP, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return IAK_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 int iak_abi_version(void) { return IAK_ABI_VERSION; }
@@ -312,6 +349,27 @@ iak_status iak_paged_decode(const iak_paged_decode_args* a, void* workspace, siz
 iak_status iak_paged_decode_timed(const iak_paged_decode_args* a, void* workspace, size_t workspace_bytes,
                                   void* stream, void* ev_begin, void* ev_end) {
   return paged_decode_impl(a, workspace, workspace_bytes, stream, ev_begin, ev_end);
+}
+
+iak_status iak_paged_decode_noalloc(const iak_paged_decode_args* a, void* stream) {
+  Plan plan;
+  const iak_status st = validate(a, &plan);
+  if (st != IAK_OK) return st;
+  if (plan.total > IAK_NOALLOC_SCRATCH_BYTES)
+    return fail(IAK_EINVAL,
+                "split-K partials of %zu bytes exceed the %zu-byte no-alloc scratch; use iak_paged_decode with a "
+                "caller workspace (or fewer splits: pages_per_split)",
+                plan.total, (size_t)IAK_NOALLOC_SCRATCH_BYTES);
+  if ((long long)a->batch * a->num_kv_heads == 0) return IAK_OK;
+  void* ws = nullptr;
+  if (plan.total > 0) {
+    int dev = -1;
+    const hipError_t e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &dev);
+    if (e != hipSuccess) return fail(IAK_EHIP, "hipStreamGetDevice failed: %s", hipGetErrorString(e));
+    const iak_status s2 = scratch_address(dev, &ws);
+    if (s2 != IAK_OK) return s2;
+  }
+  return paged_decode_impl(a, ws, plan.total, stream, nullptr, nullptr);
 }
 
 iak_status iak_mla_decode_workspace(const iak_mla_decode_args* args, size_t* bytes) {

@@ -103,7 +103,9 @@ class PageTableArgs(ctypes.Structure):
 EXPORTED = ("iak_abi_version", "iak_status_string", "iak_last_error",
             "iak_paged_decode_workspace", "iak_paged_decode",
             "iak_mla_decode_workspace", "iak_mla_decode", "iak_quantize_pages",
-            "iak_build_page_tables", "iak_paged_decode_timed", "iak_mla_decode_timed")
+            "iak_build_page_tables", "iak_paged_decode_timed", "iak_mla_decode_timed",
+            "iak_paged_decode_noalloc")
+NOALLOC_SCRATCH_BYTES = 16 << 20   # IAK_NOALLOC_SCRATCH_BYTES
 
 _lib: Optional[ctypes.CDLL] = None
 _load_error: Optional[str] = None
@@ -147,6 +149,8 @@ def load() -> ctypes.CDLL:
     lib.iak_mla_decode_timed.restype = ctypes.c_int
     lib.iak_mla_decode_timed.argtypes = [ctypes.POINTER(MlaDecodeArgs), c_void_p, ctypes.c_size_t, c_void_p,
                                          c_void_p, c_void_p]
+    lib.iak_paged_decode_noalloc.restype = ctypes.c_int
+    lib.iak_paged_decode_noalloc.argtypes = [ctypes.POINTER(PagedDecodeArgs), c_void_p]
     lib.iak_build_page_tables.restype = ctypes.c_int
     lib.iak_build_page_tables.argtypes = [ctypes.POINTER(PageTableArgs), c_void_p]
     ver = lib.iak_abi_version()
@@ -183,6 +187,11 @@ def paged_decode(args: PagedDecodeArgs, workspace_ptr: int, workspace_size: int,
     else:
         check(load().iak_paged_decode_timed(ctypes.byref(args), workspace_ptr or None, workspace_size,
                                             stream or None, events[0] or None, events[1] or None))
+
+
+def paged_decode_noalloc(args: PagedDecodeArgs, stream: int) -> None:
+    """iak_paged_decode_noalloc: the split-K partials in the library's own scratch."""
+    check(load().iak_paged_decode_noalloc(ctypes.byref(args), stream or None))
 
 
 def mla_workspace_bytes(args: MlaDecodeArgs) -> int:
