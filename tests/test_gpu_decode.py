@@ -224,6 +224,34 @@ def test_value_scales_spanning_binades(dev, pps):
     assert err <= 2e-3, f"relative err {err:.3e}"
 
 
+@pytest.mark.parametrize("mix", ["FP16", "FP8", "INT8", "INT4", "INT4_RESIDUAL", "all"])
+@pytest.mark.parametrize("pps", [0, 5])
+def test_valid_tokens_ragged_rows(dev, mix, pps):
+    """A per-row token bound: tokens of table entry e at or past
+    valid_tokens - 16 e are left out (a ragged last page), entries wholly past
+    it contribute nothing; every precision class (INT4 pages hold tokens in
+    direct order in the score layout, the others permuted), bounds 0 ..
+    16 * count + 5."""
+    import torch
+    from intent_attention import paged_decode
+    _say("valid_tokens", f"mix={mix} pages_per_split={pps}")
+    m = ({"FP16": .2, "FP8": .2, "INT8": .2, "INT4": .2, "INT4_RESIDUAL": .2} if mix == "all" else {mix: 1})
+    B, Hq, Hkv, D, NP, W = 3, 8, 4, 128, 40, 23
+    q, pools, table, counts, tags = random_case(300 + pps + len(mix), B, Hq, Hkv, D, NP, W, m, outliers=0.01)
+    rng = np.random.default_rng(5 + pps)
+    bound = (rng.integers(0, 16 * counts + 6)).astype(np.int32)
+    bound.flat[1] = 0
+    bound.flat[2] = 16 * int(counts.flat[2])          # exactly at a page boundary
+    bound.flat[3] = 16 * int(counts.flat[3]) - 15     # one token of the last page
+    got = _run(dev, q, pools, table, counts, tags, pages_per_split=pps, out_dtype=torch.float32,
+               valid_tokens=torch.from_numpy(bound).to(dev))
+    ref = Dm.paged_decode_oracle(q, pools, table, counts, tags, valid_tokens=bound)
+    err = float(np.abs(got - ref).max())
+    assert err <= (TOL_FP16 if mix == "FP16" else TOL_QUANT), f"max abs err {err:.3e}"
+    G = Hq // Hkv
+    assert np.all(got.reshape(B, Hkv, G, D)[np.unravel_index(1, (B, Hkv))] == 0)
+
+
 def test_misaligned_query_view(dev):
     """A query view 2 bytes past an aligned address (the kernel reads 16-byte
     query vectors) is copied to an aligned buffer by the host layer; the
