@@ -277,11 +277,37 @@ def build_workload(name: str, device: torch.device, seed: int = 1234, chunk_page
 # HBM bytes per decode-kernel launch (reads + writes) from rocprofv3 FETCH_SIZE /
 # WRITE_SIZE runs of this bench, each scaled by what the counter reads for a
 # 1 GiB device copy (--calibrate-copy): profiles/paged_decode_cfg3_hbm_traffic.txt and
-# profiles/paged_decode_cfg4_kernel_stats.txt.
+# profiles/paged_decode_cfg4_kernel_stats.txt. Each figure holds the digest of the
+# decode kernel's sources it was measured on (kernel_source_digest); a build whose
+# sources differ reports traffic null (stale) until the counters are run again.
 MEASURED_TRAFFIC = {
-    "cfg3": {"bytes": 2_100_613_077 + 13_874_493, "source": "profiles/paged_decode_cfg3_hbm_traffic.txt"},
-    "cfg4": {"bytes": 189_719_832 + 2_129_920, "source": "profiles/paged_decode_cfg4_kernel_stats.txt"},
+    "cfg3": {"bytes": 2_101_251_482 + 13_853_491, "src": "b1a3ae648395e56b",
+             "source": "profiles/paged_decode_cfg3_hbm_traffic.txt"},
+    "cfg4": {"bytes": 189_766_042 + 2_129_920, "src": "b1a3ae648395e56b",
+             "source": "profiles/paged_decode_cfg4_kernel_stats.txt"},
 }
+KERNEL_SOURCES = ("paged_decode.hip", "iak_device.h", "iak_internal.h")
+
+
+def kernel_source_digest() -> str:
+    """sha256 (first 16 hex digits) of the decode kernel's source files."""
+    import hashlib
+    h = hashlib.sha256()
+    for f in KERNEL_SOURCES:
+        with open(os.path.join(ROOT, "intent-attention-kernel_amd", "csrc", f), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
+def measured_traffic(config: str):
+    """(bytes per launch or None, note) for a config under the current kernel sources."""
+    m = MEASURED_TRAFFIC.get(config)
+    if m is None:
+        return None, None
+    if m["src"] != kernel_source_digest():
+        return None, f"stale: {m['source']} was measured on kernel sources {m['src']}, not {kernel_source_digest()}"
+    return m["bytes"], m["source"]
+
 
 PAGE_BYTES = {  # K+V code bytes and scale bytes per page (D = 128, fp16 scales, INT4 groups of 32)
     TAG_FP16: (2 * PS * 128 * 2, 0), TAG_FP8: (2 * PS * 128, 2 * 2), TAG_INT8: (2 * PS * 128, 2 * 2),
@@ -313,46 +339,68 @@ def flops(wl) -> float:
 # CPU baseline: the oracle on a bounded sample of rows
 # --------------------------------------------------------------------------- #
 
-def cpu_baseline(wl, rows: int, budget_s: float = 20.0) -> dict:
-    from threadpoolctl import threadpool_limits
+CPU_BUDGET_S = 8.0      # seconds of oracle work per CPU leg (one thread, then all cores)
+CPU_WORKERS_MAX = 16    # host cores of the GPU box's share
 
-    from oracle.decode import paged_decode_oracle
-    cfg = wl["cfg"]
-    B, Hkv, G, D = cfg["B"], cfg["Hkv"], cfg["Hq"] // cfg["Hkv"], cfg["D"]
-    total_rows = B * Hkv
-    table = wl["table"].reshape(total_rows, -1)
-    pick = list(range(0, total_rows, max(1, total_rows // rows)))[:rows]
-    ids = table[pick].flatten()
-    uniq, inv = torch.unique(ids, return_inverse=True)
-    p = wl["pools"]
 
-    def host(t):
-        return None if t is None else t[uniq.long()].cpu().numpy()
+def cpu_info() -> dict:
+    """Host CPU model (lscpu, else /proc/cpuinfo), cores this process may use,
+    and the worker count of the all-core leg."""
+    import subprocess
+    model = None
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        model = next((ln.split(":", 1)[1].strip() for ln in out.splitlines() if ln.startswith("Model name")), None)
+    except (OSError, subprocess.SubprocessError):
+        pass
+    if model is None and os.path.exists("/proc/cpuinfo"):
+        model = next((ln.split(":", 1)[1].strip() for ln in open("/proc/cpuinfo") if ln.startswith("model name")),
+                     None)
+    avail = len(os.sched_getaffinity(0))
+    return {"cpu_model": model, "cores_available": avail, "workers": min(CPU_WORKERS_MAX, avail)}
 
-    pools = {"k_fp16": host(p.k_fp16), "v_fp16": host(p.v_fp16)}
-    for nm, src in (("fp8", "fp8"), ("i8", "int8"), ("i4", "int4"), ("i4r", "int4r")):
-        for w in ("k", "v"):
-            if getattr(p, f"{w}_{src}") is not None:
-                pools[f"{w}_{nm}"] = host(getattr(p, f"{w}_{src}"))
-                pools[f"{w}_{nm}_scale"] = host(getattr(p, f"{w}_{src}_scale"))
-    tags = wl["tags"][uniq.long()].cpu().numpy()
-    tbl = inv.reshape(len(pick), 1, -1).cpu().numpy().astype(np.int32)
-    cnt = wl["counts"].reshape(total_rows)[pick].reshape(len(pick), 1).cpu().numpy()
-    q = wl["q"].reshape(B, Hkv, G, D).reshape(total_rows, G, D)[pick].cpu().numpy()
-    done, t0 = 0, time.perf_counter()
-    with threadpool_limits(limits=1):
-        for i in range(len(pick)):
-            paged_decode_oracle(q[i:i + 1], pools, tbl[i:i + 1], cnt[i:i + 1], tags, dtype=np.float32)
-            done += 1
-            if time.perf_counter() - t0 > budget_s:
-                break
-    dt = time.perf_counter() - t0
-    step_s = dt * total_rows / done
-    ab = algorithmic_bytes(wl)["total"]
-    return {"value": ab / step_s / 1e9, "unit": "GB/s", "us_per_step": step_s * 1e6, "cores": 1,
-            "kind": "port",
-            "sample": f"oracle.decode.paged_decode_oracle (numpy float32, 1 thread) on {done} of "
-                      f"{total_rows} (batch, kv-head) rows of {wl['name']}, {dt:.1f} s, scaled to the full step"}
+
+def run_cpu_jobs(job: str, *extra, budget_s: float = CPU_BUDGET_S) -> dict:
+    """The oracle's CPU job in a child process (python -m oracle.baseline),
+    started before this process touches the GPU: one thread, then one job per
+    core at once. Returns its JSON plus cpu_info()."""
+    import subprocess
+    info = cpu_info()
+    cmd = [sys.executable, "-m", "oracle.baseline", job, *map(str, extra), "--workers", str(info["workers"]),
+           "--budget", str(budget_s)]
+    r = subprocess.run(cmd, cwd=ROOT, capture_output=True, text=True, timeout=4 * budget_s + 180)
+    if r.returncode != 0:
+        raise RuntimeError(f"CPU baseline job {job} failed ({r.returncode}): {r.stderr[-2000:]}")
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    res.update(info)
+    return res
+
+
+def cpu_baseline_entry(raw: dict, unit: str, per_unit_value, step_units: int, sample: str, **extra) -> dict:
+    """bench.py's cpu_baseline object from a run_cpu_jobs result: ``value`` is
+    the all-core figure (``cores`` = workers used), ``threads_1`` the
+    one-thread one; ``per_unit_value(units_per_s)`` converts a job rate into
+    the leg's unit and a step takes ``step_units`` units."""
+    one = raw["threads_1"]["units_per_s"]
+    allc = raw.get("threads_all", raw["threads_1"])["units_per_s"]
+    workers = raw.get("threads_all", {}).get("workers", 1)
+    out = {"value": round(per_unit_value(allc), 4), "unit": unit, "cores": workers, "kind": "port",
+           "us_per_step": round(step_units / allc * 1e6, 1),
+           "threads_1": {"value": round(per_unit_value(one), 4), "us_per_step": round(step_units / one * 1e6, 1)},
+           "cpu_model": raw["cpu_model"], "cores_available": raw["cores_available"],
+           "sample": sample}
+    out.update(extra)
+    return out
+
+
+def cpu_baseline_decode(name: str, raw: dict, step_bytes: int, rows: int) -> dict:
+    return cpu_baseline_entry(
+        raw, "GB/s", lambda ups: step_bytes * ups / rows / 1e9, rows,
+        f"oracle.decode.paged_decode_oracle (numpy float32, one BLAS thread per process) on synthetic "
+        f"{name} rows (random codes of the configuration's shapes and precision mix); one thread "
+        f"{raw['threads_1']['units']} rows in {raw['threads_1']['seconds']:.1f} s, all cores "
+        f"{raw.get('threads_all', {}).get('units', 0)} rows in {raw.get('threads_all', {}).get('seconds', 0):.1f} s "
+        f"over {raw['workers']} processes; scaled to the {rows}-row step")
 
 
 # --------------------------------------------------------------------------- #
@@ -418,35 +466,18 @@ def mla_step_cost(wl) -> dict:
     return dict(flop=flop, bytes=codes + scales + qo, tokens=toks)
 
 
-def mla_cpu_baseline(wl, seqs: int = 4, budget_s: float = 20.0) -> dict:
-    from threadpoolctl import threadpool_limits
-
-    from oracle.mla import mla_paged_decode_oracle
+def mla_cpu_baseline(wl, raw: dict) -> dict:
     cfg = wl["cfg"]
-    p = wl["pools"]
-    table = wl["tables"][0]
-    done, t0 = 0, time.perf_counter()
-    with threadpool_limits(limits=1):
-        for b in range(min(seqs, cfg["B"])):
-            ids = table[b].long()
-            uniq, inv = torch.unique(ids, return_inverse=True)
-            pools = {"c_fp8": p.c_fp8[uniq].cpu().numpy(), "c_fp8_scale": p.c_fp8_scale[uniq].cpu().numpy(),
-                     "c_i8": p.c_int8[uniq].cpu().numpy(), "c_i8_scale": p.c_int8_scale[uniq].cpu().numpy()}
-            tags = wl["tags"][uniq].cpu().numpy()
-            mla_paged_decode_oracle(wl["q"][b:b + 1].cpu().numpy(), pools, inv[None].cpu().numpy().astype(np.int32),
-                                    np.array([wl["W"]]), tags, v_dim=cfg["DV"])
-            done += 1
-            if time.perf_counter() - t0 > budget_s:
-                break
-    dt = time.perf_counter() - t0
-    step_s = dt * cfg["B"] / done
-    return {"value": mla_step_cost(wl)["flop"] / step_s / 1e12, "unit": "TFLOP/s", "us_per_step": step_s * 1e6,
-            "cores": 1, "kind": "port",
-            "sample": f"oracle.mla.mla_paged_decode_oracle (numpy float64, 1 thread) on {done} of {cfg['B']} "
-                      f"sequences of {wl['name']}, {dt:.1f} s, scaled to the full step"}
+    flop = mla_step_cost(wl)["flop"]
+    return cpu_baseline_entry(
+        raw, "TFLOP/s", lambda ups: flop * ups / cfg["B"] / 1e12, cfg["B"],
+        f"oracle.mla.mla_paged_decode_oracle (numpy float64, one BLAS thread per process) on synthetic cfg5 "
+        f"sequences (128 heads, 512 FP8 / INT8 latent pages); one thread {raw['threads_1']['units']} sequences "
+        f"in {raw['threads_1']['seconds']:.1f} s, all cores {raw.get('threads_all', {}).get('units', 0)} over "
+        f"{raw['workers']} processes; scaled to the {cfg['B']}-sequence step")
 
 
-def run_mla(args) -> None:
+def run_mla(args, cpu=None) -> None:
     from intent_attention.mla_core import make_mla_plan
     dev = torch.device("cuda:0")
     t_build = time.perf_counter()
@@ -501,8 +532,8 @@ def run_mla(args) -> None:
                      "step_frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
                      "hbm_gbps": round(cost["bytes"] / (kernel_ms * 1e-3) / 1e9, 1)},
     }
-    if not args.no_cpu_baseline:
-        res["cpu_baseline"] = mla_cpu_baseline(wl)
+    if cpu is not None:
+        res["cpu_baseline"] = mla_cpu_baseline(wl, cpu)
     print(json.dumps(res), flush=True)
 
 
@@ -554,28 +585,18 @@ def quantize_step_bytes(wl) -> int:
     return total
 
 
-def quantize_cpu_baseline(wl, budget_s: float = 12.0) -> dict:
-    from oracle import quant as Q
-    names = {TAG_FP8: "FP8", TAG_INT8: "INT8", TAG_INT4: "INT4"}
-    host = [(j["tag"], j["src"][:512].cpu().numpy()) for j in wl["jobs"]]
-    done_pages, done_bytes, t0 = 0, 0, time.perf_counter()
-    i = 0
-    while time.perf_counter() - t0 < budget_s and i < 512:
-        for tag, x in host:                     # round robin over the K/V x precision jobs
-            cb, sb = QUANT_OUT_BYTES[tag]
-            Q.quantize_page(x[i], names[tag], 32)
-            done_pages += 1
-            done_bytes += PS * wl["cfg"]["D"] * 2 + 4 + cb + sb
-        i += 1
-    dt = time.perf_counter() - t0
-    rate = done_bytes / dt
-    return {"value": round(rate / 1e9, 4), "unit": "GB/s", "us_per_step": round(quantize_step_bytes(wl) / rate * 1e6),
-            "cores": 1, "kind": "port",
-            "sample": f"oracle.quant.quantize_page (numpy, 1 thread) on {done_pages} pages (round robin over the "
-                      f"6 K/V x precision jobs), {dt:.1f} s, scaled to the full step"}
+def quantize_cpu_baseline(wl, raw: dict) -> dict:
+    pages = sum(j["src"].shape[0] for j in wl["jobs"])
+    step_bytes = quantize_step_bytes(wl)
+    return cpu_baseline_entry(
+        raw, "GB/s", lambda ups: step_bytes * ups / pages / 1e9, pages,
+        f"oracle.quant.quantize_page (numpy, one thread per process) on float16 pages round robin over the "
+        f"FP8 / INT8 / INT4 jobs; one thread {raw['threads_1']['units']} pages in "
+        f"{raw['threads_1']['seconds']:.1f} s, all cores {raw.get('threads_all', {}).get('units', 0)} over "
+        f"{raw['workers']} processes; scaled to the {pages}-page step")
 
 
-def run_quantize(args) -> None:
+def run_quantize(args, cpu=None) -> None:
     from intent_attention import _native as N
     dev = torch.device("cuda:0")
     t_build = time.perf_counter()
@@ -611,8 +632,8 @@ def run_quantize(args) -> None:
                       "algorithmic_bytes": ab},
            "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None}}
-    if not args.no_cpu_baseline:
-        out["cpu_baseline"] = quantize_cpu_baseline(wl)
+    if cpu is not None:
+        out["cpu_baseline"] = quantize_cpu_baseline(wl, cpu)
     print(json.dumps(out), flush=True)
 
 
@@ -630,7 +651,9 @@ TABLE_CONFIGS = {
 }
 
 
-def build_table_workload(name: str, device: torch.device, seed: int = 7):
+def table_routing(name: str, seed: int = 7):
+    """Host part of the cfg3-tables workload: per sequence the routed spans
+    (start, end, tag), and the block table [B * Hkv, pages] (numpy only)."""
     cfg = TABLE_CONFIGS[name]
     B, Hkv, T = cfg["B"], cfg["Hkv"], cfg["T"]
     P = T // PS
@@ -652,7 +675,13 @@ def build_table_workload(name: str, device: torch.device, seed: int = 7):
             got += e - s
         lists.append(spans)
     NP = B * Hkv * P
-    bt = torch.from_numpy(rng.permutation(NP).astype(np.int32).reshape(B * Hkv, P)).to(device)
+    return lists, NP, P, rng.permutation(NP).astype(np.int32).reshape(B * Hkv, P)
+
+
+def build_table_workload(name: str, device: torch.device, seed: int = 7):
+    cfg = TABLE_CONFIGS[name]
+    lists, NP, P, bt_host = table_routing(name, seed)
+    bt = torch.from_numpy(bt_host).to(device)
     offs, beg, end, tag = [0], [], [], []
     for spans in lists:
         for s, e, t in spans:
@@ -674,9 +703,8 @@ def table_step_bytes(wl, pairs: int) -> int:
             + R * cfg["W"] * 4 + R * 4 + wl["NP"] * 4)          # page table, counts, precision out
 
 
-def run_tables(args) -> None:
+def run_tables(args, cpu=None) -> None:
     from intent_attention import _native as N
-    from oracle import policy as Pol
     dev = torch.device("cuda:0")
     wl = build_table_workload(args.config, dev)
     cfg = wl["cfg"]
@@ -702,14 +730,6 @@ def run_tables(args) -> None:
         N.build_page_tables(a, torch.cuda.current_stream(dev).cuda_stream)
     torch.cuda.synchronize()
     res = _time_steps(graph.replay, args, stream)
-    # every replay must give the CPU restatement's tables (checked on 16 rows)
-    rows = list(range(0, R, R // 16))
-    want = Pol.build_page_tables_oracle(wl["lists"], R, cfg["W"], PS, wl["NP"], rows_per_seq=1,
-                                        rows_per_list=cfg["Hkv"], block_table=wl["block_table"].cpu().numpy())
-    got_t, got_c = table.cpu().numpy(), counts.cpu().numpy()
-    if not (np.array_equal(got_t[rows], want[0][rows]) and np.array_equal(got_c, want[2])
-            and np.array_equal(prec.cpu().numpy(), want[1])):
-        raise SystemExit("page tables differ from the CPU restatement")
     pairs = int(sum(min(wl["P"] - 1, (e - 1) // PS) - s // PS + 1 for spans in wl["lists"] for s, e, _ in spans))
     ab = table_step_bytes(wl, pairs * cfg["Hkv"])
     ms = res["ms"]
@@ -725,18 +745,13 @@ def run_tables(args) -> None:
                       "algorithmic_bytes": ab},
            "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None}}
-    if not args.no_cpu_baseline:
-        bt_host = wl["block_table"].cpu().numpy()
-        reps, t0 = 0, time.perf_counter()
-        while reps < 3 or time.perf_counter() - t0 < 10.0:
-            Pol.build_page_tables_oracle(wl["lists"], R, cfg["W"], PS, wl["NP"], rows_per_seq=1,
-                                         rows_per_list=cfg["Hkv"], block_table=bt_host)
-            reps += 1
-        dt = time.perf_counter() - t0
-        out["cpu_baseline"] = {"value": round(dt / reps * 1e6, 1), "unit": "us", "cores": 1, "kind": "port",
-                               "sample": f"oracle.policy.build_page_tables_oracle (Python loops as the reference's "
-                                         f"routing_to_kernel_metadata + metadata_to_kernel_tensors, 1 thread), the "
-                                         f"full step {reps} times in {dt:.1f} s"}
+    if cpu is not None:
+        out["cpu_baseline"] = cpu_baseline_entry(
+            cpu, "us", lambda ups: 1e6 / ups, 1,
+            f"oracle.policy.build_page_tables_oracle (Python loops as the reference's routing_to_kernel_metadata "
+            f"+ metadata_to_kernel_tensors, one thread per process), the full step: one thread "
+            f"{cpu['threads_1']['units']} in {cpu['threads_1']['seconds']:.1f} s, all cores "
+            f"{cpu.get('threads_all', {}).get('units', 0)} over {cpu['workers']} processes (independent steps)")
     print(json.dumps(out), flush=True)
 
 
@@ -776,15 +791,92 @@ def _time_steps(step, args, stream) -> dict:
 
 # --------------------------------------------------------------------------- #
 
+def cpu_jobs_for(config: str):
+    """(job, extra args) of the oracle CPU job that mirrors a leg."""
+    if config in CONFIGS and config != "tiny":
+        return "decode", (config,)
+    if config in MLA_CONFIGS:
+        return "mla", ()
+    if config in QUANT_CONFIGS:
+        return "quantize", ()
+    if config == "cfg1":
+        return "cfg1", ("loop",)
+    return None, ()
+
+
+def run_cfg1(args, cpu=None, cfg1_paths=None) -> None:
+    """cfg1: the reference's CPU-runnable shape on the
+    GPU. A step is one fused_selected_quant_decode over the routed pages, timed
+    as the validated plan's launch (the call the Python entry point makes after
+    its argument checks) and as the whole Python call."""
+    from intent_attention import fused_selected_quant_decode
+    from intent_attention.decode_core import PagePools, make_plan
+    from intent_attention.fused_selected_quant_decode import _tag_map
+    dev = torch.device("cuda:0")
+    wl = build_cfg1(dev)
+    c = CFG1
+    pools = PagePools(k_fp16=wl["k16"], v_fp16=wl["v16"], k_int8=wl["k8"], v_int8=wl["v8"], k_int8_scale=wl["ks"],
+                      v_int8_scale=wl["vs"])
+    out = torch.empty((c["B"], c["H"], 1, c["D"]), dtype=torch.float16, device=dev)
+    plan = make_plan(wl["q"][:, :, 0, :], pools, wl["table"], wl["counts"], wl["prec"], tag_map=_tag_map(pools),
+                     negative_ids=True, sm_scale=1.0 / math.sqrt(c["D"]), out=out[:, :, 0, :])
+    stream = torch.cuda.current_stream(dev)
+    res = _time_steps(plan.run, args, stream)
+    api = _time_steps(lambda: fused_selected_quant_decode(*cfg1_args(wl)), args, stream)
+    kev = kernel_events(args.steps, stream)
+    for k in kev:
+        plan.run(events=k)
+    torch.cuda.synchronize()
+    kernel_ms = sum(b.elapsed_time(e) for b, e in kev) / args.steps
+    n_sel = len(wl["pages"])
+    n_int8 = n_sel // 2
+    # K+V codes of every (head, selected page), INT8 scales, table entries and tags, counts, Q and O
+    ab = (c["H"] * ((n_sel - n_int8) * 2 * PS * c["D"] * 2 + n_int8 * (2 * PS * c["D"] + 2 * 2))
+          + c["H"] * n_sel * (4 + 4) + c["H"] * 4 + 2 * c["B"] * c["H"] * c["D"] * 2)
+    ms = res["ms"]
+    out_json = {
+        "metric": METRIC, "value": round(ab / (ms * 1e-3) / 1e9, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5), "us_per_step": round(ms * 1e3, 2),
+        "us_per_step_p10_p50_p90": res["spread"],
+        "api_us_per_step": round(api["ms"] * 1e3, 2),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+        "data": "synthetic (seeded N(0,1) float16 Q/K/V; INT8 pages by the fused fake_int8_pages_from_fp16)",
+        "config": {"workload": "cfg1: B=1 H=8/8 D=64 ctx=1024 (64 pages), 32 selected by BlockRouter (4 ALWAYS, "
+                               "8 RECENT, 20 ATTEND), FP16/INT8 alternating by page id, "
+                               "routing_to_kernel_metadata -> metadata_to_kernel_tensors -> "
+                               "fused_selected_quant_decode",
+                   "selected_pages": c["H"] * n_sel, "algorithmic_bytes": ab,
+                   "selected_page_ids": wl["meta"]["selected_page_ids"]},
+        "roofline": {"bound": "hbm", "achieved": round(ab / (kernel_ms * 1e-3) / 1e9, 2), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(ab / (kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 5),
+                     "traffic": None, "kernel": "paged_decode_kernel", "kernel_us": round(kernel_ms * 1e3, 2),
+                     "note": "latency-bound: 64 waves read 1.4 MB; the step is launch and dependent-load latency"},
+    }
+    if cpu is not None:
+        out_json["cpu_baseline"] = cpu_baseline_entry(
+            cpu, "GB/s", lambda ups: ab * ups / 1e9, 1,
+            f"oracle.decode.fused_decode_reference_loop (the reference's per-(b, h, page) loop, numpy float32, one "
+            f"thread per process) on synthetic cfg1 inputs; one thread {cpu['threads_1']['units']} steps in "
+            f"{cpu['threads_1']['seconds']:.1f} s, all cores {cpu.get('threads_all', {}).get('units', 0)} steps "
+            f"over {cpu['workers']} processes (independent steps)",
+            paths_1_thread=cfg1_paths,
+            published_reference_cpu_us=19454.0,
+            published_reference_shape="docs/results_cpu.md:63-69: B=1 H=8 D=64, 16 of 64 pages selected, all FP16, "
+                                      "unstated CPU")
+    print(json.dumps(out_json), flush=True)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="cfg3",
-                    choices=sorted(CONFIGS) + sorted(MLA_CONFIGS) + sorted(QUANT_CONFIGS) + sorted(TABLE_CONFIGS))
+                    choices=sorted(CONFIGS) + ["cfg1"] + sorted(MLA_CONFIGS) + sorted(QUANT_CONFIGS)
+                    + sorted(TABLE_CONFIGS))
     ap.add_argument("--pages-per-split", type=int, default=0)
-    ap.add_argument("--cpu-rows", type=int, default=192, help="rows of the step the CPU baseline times")
+    ap.add_argument("--cpu-budget", type=float, default=CPU_BUDGET_S,
+                    help="seconds of oracle work per CPU-baseline leg (one thread, then all cores)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="after the timed steps, run a plain device copy of MIB MiB (read + write "
@@ -796,15 +888,48 @@ def main() -> None:
               file=sys.stderr)
         sys.exit(2)
 
+    # the CPU baseline runs first, in a child process, before this process touches the GPU
+    cpu, cfg1_paths = None, None
+    if not args.no_cpu_baseline:
+        t0 = time.perf_counter()
+        if args.config in TABLE_CONFIGS:
+            import tempfile
+            lists, NP, P, bt = table_routing(args.config)
+            cfg = TABLE_CONFIGS[args.config]
+            spec = os.path.join(tempfile.mkdtemp(prefix="iak_bench_"), "tables.npz")
+            np.savez(spec, lists=np.array(json.dumps(lists)), R=cfg["B"] * cfg["Hkv"], W=cfg["W"], PS=PS, NP=NP,
+                     Hkv=cfg["Hkv"], block_table=bt)
+            cpu = run_cpu_jobs("tables", spec, budget_s=args.cpu_budget)
+        else:
+            job, extra = cpu_jobs_for(args.config)
+            if job is not None:
+                cpu = run_cpu_jobs(job, *extra, budget_s=args.cpu_budget)
+        if args.config == "cfg1":
+            import subprocess
+            r = subprocess.run([sys.executable, "-c", "import json; from oracle.baseline import cfg1_protocol; "
+                                "print(json.dumps(cfg1_protocol()))"], cwd=ROOT, capture_output=True, text=True,
+                               timeout=300)
+            if r.returncode != 0:
+                raise RuntimeError(f"cfg1 CPU protocol failed: {r.stderr[-2000:]}")
+            cfg1_paths = json.loads(r.stdout.strip().splitlines()[-1])
+        print(f"[bench] CPU baseline in {time.perf_counter() - t0:.1f}s", file=sys.stderr, flush=True)
+
+    if args.config == "cfg1":
+        run_cfg1(args, cpu, cfg1_paths)
+        return
     if args.config in MLA_CONFIGS:
-        run_mla(args)
+        run_mla(args, cpu)
         return
     if args.config in QUANT_CONFIGS:
-        run_quantize(args)
+        run_quantize(args, cpu)
         return
     if args.config in TABLE_CONFIGS:
-        run_tables(args)
+        run_tables(args, cpu)
         return
+    run_decode(args, cpu)
+
+
+def run_decode(args, cpu=None) -> None:
     from intent_attention.decode_core import make_plan
     dev = torch.device("cuda:0")
     t_build = time.perf_counter()
@@ -874,12 +999,12 @@ def main() -> None:
                    "gflop": round(flops(wl) / 1e9, 3)},
         "roofline": {"bound": "hbm", "achieved": round(kernel_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(kernel_gbps / HBM_PEAK_GBPS, 4),
-                     "traffic": MEASURED_TRAFFIC.get(args.config, {}).get("bytes"),
+                     "traffic": measured_traffic(args.config)[0],
                      "kernel": "paged_decode_kernel", "kernel_us": round(kernel_ms * 1e3, 2),
                      "kernel_bytes": kernel_bytes, "step_frac": round(achieved / HBM_PEAK_GBPS, 4)},
     }
     if args.config in MEASURED_TRAFFIC:
-        res["roofline"]["traffic_source"] = MEASURED_TRAFFIC[args.config]["source"]
+        res["roofline"]["traffic_source"] = measured_traffic(args.config)[1]
     if args.calibrate_copy:
         n = args.calibrate_copy * (1 << 20)
         src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
@@ -889,8 +1014,9 @@ def main() -> None:
             dst.copy_(src)
         torch.cuda.synchronize()
         res["copy_calibration_bytes"] = n
-    if not args.no_cpu_baseline:
-        res["cpu_baseline"] = cpu_baseline(wl, args.cpu_rows)
+    if cpu is not None:
+        rows = cfg["B"] * cfg["Hkv"]
+        res["cpu_baseline"] = cpu_baseline_decode(args.config, cpu, ab["total"], rows)
     print(json.dumps(res), flush=True)
 
 

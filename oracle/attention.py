@@ -43,7 +43,7 @@ def dense_attention(q, k, v, exact: bool = True):
     if not exact and not (q.dtype == k.dtype == v.dtype):
         raise RuntimeError(
             f"expected m1 and m2 to have the same dtype, but got: {q.dtype} != {k.dtype}")
-    dt = np.float64 if exact else q.dtype
+    dt = np.float64 if exact else q.dtype.type
     scale = 1.0 / math.sqrt(q.shape[-1])
     s = np.matmul(q.astype(dt), np.swapaxes(k.astype(dt), -2, -1)) * dt(scale)
     s = s - s.max(axis=-1, keepdims=True)
