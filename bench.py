@@ -755,6 +755,91 @@ def run_tables(args, cpu=None) -> None:
     print(json.dumps(out), flush=True)
 
 
+# --------------------------------------------------------------------------- #
+# KV memory manager transcoding (transcode): iak_transcode_pages on the cfg3
+# pool shape. A step demotes a quarter of the pool's pages (random slots) from
+# the FP16 pool to the INT8 pool, then promotes them back: the manager's
+# demote_cold_pages / promote_hot_pages, one launch each.
+
+TRANSCODE_CONFIGS = {
+    "transcode": dict(pool=32 * 8 * 4096, pages=262144, elems=PS * 128),
+}
+
+
+def transcode_page_bytes(elems: int) -> dict:
+    """Algorithmic bytes per page: demote reads the float16 page and its slot id
+    and writes the codes and the float32 scale; promote reads the codes, the
+    scale and the slot id and writes the float16 page."""
+    return {"demote": elems * 2 + 4 + elems + 4, "promote": elems + 4 + 4 + elems * 2}
+
+
+def run_transcode(args, cpu=None) -> None:
+    from intent_attention import _native as N
+    dev = torch.device("cuda:0")
+    cfg = TRANSCODE_CONFIGS[args.config]
+    NP, n, E = cfg["pool"], cfg["pages"], cfg["elems"]
+    t_build = time.perf_counter()
+    g = torch.Generator(device=dev).manual_seed(5)
+    fp16 = torch.empty((NP, E), dtype=torch.float16, device=dev)
+    for lo in range(0, NP, 65536):
+        fp16[lo:lo + 65536] = torch.randn((min(65536, NP - lo), E), generator=g, device=dev).half()
+    int8 = torch.zeros((NP, E), dtype=torch.int8, device=dev)
+    scales = torch.ones(NP, dtype=torch.float32, device=dev)
+    slots = torch.randperm(NP, generator=torch.Generator().manual_seed(6))[:n].to(torch.int32).to(dev)
+    torch.cuda.synchronize()
+    print(f"[bench] built {args.config} in {time.perf_counter() - t_build:.1f}s", file=sys.stderr, flush=True)
+    stream = torch.cuda.current_stream(dev)
+    argv = {}
+    for name, mode in (("demote", N.TRANSCODE_DEMOTE_INT8), ("promote", N.TRANSCODE_PROMOTE_FP16)):
+        a = N.TranscodeArgs()
+        a.num_pages, a.page_elems, a.mode, a.pages, a.pool_pages = n, E, mode, slots.data_ptr(), NP
+        a.fp16, a.int8, a.scales = fp16.data_ptr(), int8.data_ptr(), scales.data_ptr()
+        argv[name] = a
+
+    def step(ev=None):
+        for i, name in enumerate(("demote", "promote")):
+            if ev is not None:
+                ev[i][0].record(stream)
+            N.transcode_pages(argv[name], stream.cuda_stream)
+            if ev is not None:
+                ev[i][1].record(stream)
+
+    res = _time_steps(step, args, stream)
+    evs = [kernel_events(2, stream) for _ in range(args.steps)]
+    for ev in evs:
+        step(ev)
+    torch.cuda.synchronize()
+    per_page = transcode_page_bytes(E)
+    kern = {}
+    for i, name in enumerate(("demote", "promote")):
+        us = sum(ev[i][0].elapsed_time(ev[i][1]) for ev in evs) / args.steps * 1e3
+        kern[name] = {"us": round(us, 2), "GBps": round(per_page[name] * n / (us * 1e-6) / 1e9, 1),
+                      "algorithmic_bytes": per_page[name] * n}
+    ab = (per_page["demote"] + per_page["promote"]) * n
+    ms = res["ms"]
+    gbps = ab / (ms * 1e-3) / 1e9
+    dom = max(kern, key=lambda k: kern[k]["us"])
+    out = {"metric": "KV page transcoding GB/s (demote FP16 -> INT8, then promote INT8 -> FP16)",
+           "value": round(gbps, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": round(ms, 5), "us_per_step": round(ms * 1e3, 2),
+           "us_per_step_p10_p50_p90": res["spread"], "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "f16<->i8",
+           "data": "synthetic (seeded float16 N(0,1) pages)",
+           "config": {"workload": f"{args.config}: {n} random slots of a {NP}-page pool of 16x128 float16 pages "
+                                  f"demoted to INT8 and promoted back (2 launches per step)",
+                      "algorithmic_bytes": ab, "kernels": kern},
+           "roofline": {"bound": "hbm", "achieved": kern[dom]["GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                        "frac": round(kern[dom]["GBps"] / HBM_PEAK_GBPS, 4), "traffic": None,
+                        "kernel": f"transcode_{dom}_kernel", "kernel_us": kern[dom]["us"]}}
+    if cpu is not None:
+        out["cpu_baseline"] = cpu_baseline_entry(
+            cpu, "GB/s", lambda ups: (per_page["demote"] + per_page["promote"]) * ups / 1e9, n,
+            f"oracle.memory.demote_int8 + promote_fp16 (numpy, one thread per process) on 16x128 float16 pages; "
+            f"one thread {cpu['threads_1']['units']} pages in {cpu['threads_1']['seconds']:.1f} s, all cores "
+            f"{cpu.get('threads_all', {}).get('units', 0)} over {cpu['workers']} processes")
+    print(json.dumps(out), flush=True)
+
+
 def kernel_events(n: int, stream) -> list:
     """n pairs of timing events, each recorded once so its HIP event exists
     (torch creates events lazily); the library re-records them around the split
@@ -801,6 +886,8 @@ def cpu_jobs_for(config: str):
         return "quantize", ()
     if config == "cfg1":
         return "cfg1", ("loop",)
+    if config in TRANSCODE_CONFIGS:
+        return "transcode", ()
     return None, ()
 
 
@@ -873,7 +960,7 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="cfg3",
                     choices=sorted(CONFIGS) + ["cfg1"] + sorted(MLA_CONFIGS) + sorted(QUANT_CONFIGS)
-                    + sorted(TABLE_CONFIGS))
+                    + sorted(TABLE_CONFIGS) + sorted(TRANSCODE_CONFIGS))
     ap.add_argument("--pages-per-split", type=int, default=0)
     ap.add_argument("--cpu-budget", type=float, default=CPU_BUDGET_S,
                     help="seconds of oracle work per CPU-baseline leg (one thread, then all cores)")
@@ -925,6 +1012,9 @@ def main() -> None:
         return
     if args.config in TABLE_CONFIGS:
         run_tables(args, cpu)
+        return
+    if args.config in TRANSCODE_CONFIGS:
+        run_transcode(args, cpu)
         return
     run_decode(args, cpu)
 

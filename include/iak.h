@@ -25,6 +25,10 @@
  *   iak_build_page_tables       routing_to_kernel_metadata() block_router.py:383-421 (page ids: selected_page_ids
  *                               :283-296) followed by metadata_to_kernel_tensors()
  *                               fused_selected_quant_decode.py:344-400 (the loop :394-398)
+ *   iak_transcode_pages         KVMemoryManager FP16 <-> INT8 page transcoding: write_page's INT8 branch
+ *                               kv_memory_manager.py:233-252, _read_page_data :286-296, set_page_format
+ *                               :268-284 (demote_cold_pages :350-362, promote_hot_pages :364-377)
+ *   iak_prefetch_pages          launch_prefetch_pages() prefetch.py:183-261 (its Triton kernel :111-170)
  *   iak_status_string           (no counterpart: the reference raises ValueError/RuntimeError in Python)
  */
 #ifndef IAK_H
@@ -299,6 +303,59 @@ typedef struct {
 
 /* Build page tables; async on `stream`. */
 iak_status iak_build_page_tables(const iak_page_table_args* args, void* stream);
+
+/*
+ * KV memory manager page transcoding with the manager's arithmetic
+ * (kv_memory_manager.py): pages of page_elems values (page_size x head_dim,
+ * a multiple of 8) in two pools indexed by slot, fp16 [pool_pages,
+ * page_elems] and int8 [pool_pages, page_elems], with one float32 scale per
+ * slot. Page p is slot pages[p] (or p when pages is NULL); slots outside
+ * [0, pool_pages) are skipped.
+ *   IAK_TRANSCODE_DEMOTE_INT8: fp16 -> int8 codes and scales:
+ *       scale = max|x| / 127 (1.0 for an all-zero page or one holding a NaN),
+ *       code = clamp(round(float16(x / scale)), -128, 127) (round half to even);
+ *   IAK_TRANSCODE_PROMOTE_FP16: int8 codes and scales -> fp16: float16(code * scale).
+ * The float32 scale is what the reference's float arithmetic uses of its
+ * Python float scale, so both directions are bit-exact to it. The fp16 pool
+ * must be 16-byte aligned, the int8 pool 8-byte aligned. A slot listed twice
+ * in one call is transcoded twice, concurrently (the result of a race).
+ */
+enum { IAK_TRANSCODE_DEMOTE_INT8 = 0, IAK_TRANSCODE_PROMOTE_FP16 = 1 };
+
+typedef struct {
+  int32_t num_pages;
+  int32_t page_elems;
+  int32_t mode;
+  const int32_t* pages;         /* [num_pages] slots, or NULL */
+  int64_t pool_pages;
+  void* fp16;                   /* float16 [pool_pages, page_elems] */
+  void* int8;                   /* int8 [pool_pages, page_elems] */
+  float* scales;                /* float32 [pool_pages] */
+} iak_transcode_args;
+
+/* Transcode pages between the FP16 and INT8 pools; async on `stream`. */
+iak_status iak_transcode_pages(const iak_transcode_args* args, void* stream);
+
+/*
+ * Page warm-up: reads the K and V rows of pages page_ids[0 .. num_ids-1]
+ * (pages of page_size tokens; tokens at or past kv_len skipped) of every
+ * (batch, head) of k, v [batch, heads, kv_len, head_dim] (16-bit elements,
+ * element strides, unit last stride) with cached loads, so a following decode
+ * finds them in the L2 / Infinity Cache. Correctness-neutral. The words read
+ * are folded into checksum [batch * heads * num_ids * 4] (one per wave:
+ * element i of a page enters as value << (16 (i & 1)), XOR-folded).
+ */
+typedef struct {
+  int32_t batch, heads, kv_len, head_dim, page_size, num_ids;
+  const int32_t* page_ids;
+  const void* k; const void* v;
+  int64_t k_stride_b, k_stride_h, k_stride_t;
+  int64_t v_stride_b, v_stride_h, v_stride_t;
+  uint32_t* checksum;
+} iak_prefetch_args;
+
+/* Warm pages into the caches; async on `stream`. */
+iak_status iak_prefetch_pages(const iak_prefetch_args* args, void* stream);
 
 #ifdef __cplusplus
 }

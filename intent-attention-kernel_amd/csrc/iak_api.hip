@@ -471,6 +471,41 @@ iak_status iak_quantize_pages(const iak_quantize_args* a, void* stream) {
   return IAK_OK;
 }
 
+iak_status iak_transcode_pages(const iak_transcode_args* a, void* stream) {
+  if (!a) return fail(IAK_EINVAL, "args is NULL");
+  if (a->num_pages < 0 || a->pool_pages < 0) return fail(IAK_EINVAL, "negative page count");
+  if (a->mode != IAK_TRANSCODE_DEMOTE_INT8 && a->mode != IAK_TRANSCODE_PROMOTE_FP16)
+    return fail(IAK_EINVAL, "unknown transcode mode %d", a->mode);
+  if (a->page_elems <= 0 || a->page_elems % 8 != 0)
+    return fail(IAK_ENOTSUP, "page_elems %d must be a positive multiple of 8", a->page_elems);
+  if (a->num_pages == 0) return IAK_OK;
+  if (!a->fp16 || !a->int8 || !a->scales) return fail(IAK_EINVAL, "fp16/int8/scales is NULL");
+  if (!aligned16(a->fp16) || (reinterpret_cast<uintptr_t>(a->int8) & 7u) ||
+      (reinterpret_cast<uintptr_t>(a->scales) & 3u) || (reinterpret_cast<uintptr_t>(a->pages) & 3u))
+    return fail(IAK_EINVAL, "the fp16 pool must be 16-byte aligned, the int8 pool 8-byte aligned, scales and "
+                "pages 4-byte aligned");
+  if (!a->pages && a->num_pages > a->pool_pages)
+    return fail(IAK_EINVAL, "num_pages %d exceeds pool_pages %lld without a slot list", a->num_pages,
+                (long long)a->pool_pages);
+  const hipError_t e = iak::launch_transcode(*a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(IAK_EHIP, "kernel launch failed: %s", hipGetErrorString(e));
+  return IAK_OK;
+}
+
+iak_status iak_prefetch_pages(const iak_prefetch_args* a, void* stream) {
+  if (!a) return fail(IAK_EINVAL, "args is NULL");
+  if (a->batch < 0 || a->heads < 0 || a->kv_len < 0 || a->num_ids < 0 || a->head_dim <= 0 || a->page_size <= 0)
+    return fail(IAK_EINVAL, "negative size or non-positive head_dim / page_size");
+  if ((long long)a->batch * a->heads > 65535) return fail(IAK_ENOTSUP, "batch * heads above 65535");
+  if (a->num_ids == 0 || a->batch == 0 || a->heads == 0) return IAK_OK;
+  if (!a->page_ids || !a->k || !a->v || !a->checksum) return fail(IAK_EINVAL, "page_ids/k/v/checksum is NULL");
+  if ((reinterpret_cast<uintptr_t>(a->k) | reinterpret_cast<uintptr_t>(a->v)) & 1u)
+    return fail(IAK_EINVAL, "k/v must be 2-byte aligned");
+  const hipError_t e = iak::launch_prefetch(*a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(IAK_EHIP, "kernel launch failed: %s", hipGetErrorString(e));
+  return IAK_OK;
+}
+
 iak_status iak_build_page_tables(const iak_page_table_args* a, void* stream) {
   if (!a) return fail(IAK_EINVAL, "args is NULL");
   if (a->num_rows < 0 || a->table_width < 0 || a->num_pages < 0)

@@ -103,6 +103,10 @@ hipError_t launch_quantize_pages(const iak_quantize_args& a, hipStream_t stream)
 
 hipError_t launch_page_tables(const iak_page_table_args& a, hipStream_t stream);
 
+hipError_t launch_transcode(const iak_transcode_args& a, hipStream_t stream);
+
+hipError_t launch_prefetch(const iak_prefetch_args& a, hipStream_t stream);
+
 }  // namespace iak
 
 #endif

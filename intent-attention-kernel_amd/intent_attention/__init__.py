@@ -46,6 +46,8 @@ from .mla_core import LatentPools, mla_paged_decode
 from .triton_mla_decode import mla_decode_triton
 from .quantize import fake_int8_pages_device, quantize_pages
 from .page_tables import build_page_tables, routing_to_kernel_tensors
+from .kv_memory_manager import KVMemoryManager, PageFormatPolicy, PageState, PageStorageFormat
+from .prefetch import BlockPrefetcher, get_prefetch_stream, get_prefetcher, launch_prefetch_pages, reset_prefetcher
 
 __all__ = [
     "SELECTED_POLICIES", "BlockLayout", "BlockPolicy", "SemanticBlock",
@@ -64,4 +66,6 @@ __all__ = [
     "LatentPools", "mla_paged_decode", "mla_decode_triton",
     "quantize_pages", "fake_int8_pages_device",
     "build_page_tables", "routing_to_kernel_tensors",
+    "KVMemoryManager", "PageFormatPolicy", "PageState", "PageStorageFormat",
+    "BlockPrefetcher", "get_prefetch_stream", "get_prefetcher", "launch_prefetch_pages", "reset_prefetcher",
 ]

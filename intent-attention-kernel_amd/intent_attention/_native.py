@@ -100,11 +100,37 @@ class PageTableArgs(ctypes.Structure):
     ]
 
 
+TRANSCODE_DEMOTE_INT8, TRANSCODE_PROMOTE_FP16 = 0, 1
+
+
+class TranscodeArgs(ctypes.Structure):
+    """Mirror of ``iak_transcode_args`` (include/iak.h)."""
+
+    _fields_ = [
+        ("num_pages", c_i32), ("page_elems", c_i32), ("mode", c_i32),
+        ("pages", c_void_p), ("pool_pages", c_i64),
+        ("fp16", c_void_p), ("int8", c_void_p), ("scales", c_void_p),
+    ]
+
+
+class PrefetchArgs(ctypes.Structure):
+    """Mirror of ``iak_prefetch_args`` (include/iak.h)."""
+
+    _fields_ = [
+        ("batch", c_i32), ("heads", c_i32), ("kv_len", c_i32), ("head_dim", c_i32), ("page_size", c_i32),
+        ("num_ids", c_i32),
+        ("page_ids", c_void_p), ("k", c_void_p), ("v", c_void_p),
+        ("k_stride_b", c_i64), ("k_stride_h", c_i64), ("k_stride_t", c_i64),
+        ("v_stride_b", c_i64), ("v_stride_h", c_i64), ("v_stride_t", c_i64),
+        ("checksum", c_void_p),
+    ]
+
+
 EXPORTED = ("iak_abi_version", "iak_status_string", "iak_last_error",
             "iak_paged_decode_workspace", "iak_paged_decode",
             "iak_mla_decode_workspace", "iak_mla_decode", "iak_quantize_pages",
             "iak_build_page_tables", "iak_paged_decode_timed", "iak_mla_decode_timed",
-            "iak_paged_decode_noalloc")
+            "iak_paged_decode_noalloc", "iak_transcode_pages", "iak_prefetch_pages")
 NOALLOC_SCRATCH_BYTES = 16 << 20   # IAK_NOALLOC_SCRATCH_BYTES
 
 _lib: Optional[ctypes.CDLL] = None
@@ -151,6 +177,10 @@ def load() -> ctypes.CDLL:
                                          c_void_p, c_void_p]
     lib.iak_paged_decode_noalloc.restype = ctypes.c_int
     lib.iak_paged_decode_noalloc.argtypes = [ctypes.POINTER(PagedDecodeArgs), c_void_p]
+    lib.iak_transcode_pages.restype = ctypes.c_int
+    lib.iak_transcode_pages.argtypes = [ctypes.POINTER(TranscodeArgs), c_void_p]
+    lib.iak_prefetch_pages.restype = ctypes.c_int
+    lib.iak_prefetch_pages.argtypes = [ctypes.POINTER(PrefetchArgs), c_void_p]
     lib.iak_build_page_tables.restype = ctypes.c_int
     lib.iak_build_page_tables.argtypes = [ctypes.POINTER(PageTableArgs), c_void_p]
     ver = lib.iak_abi_version()
@@ -212,6 +242,14 @@ def mla_decode(args: MlaDecodeArgs, workspace_ptr: int, workspace_size: int, str
 
 def quantize_pages(args: QuantizeArgs, stream: int) -> None:
     check(load().iak_quantize_pages(ctypes.byref(args), stream or None))
+
+
+def transcode_pages(args: TranscodeArgs, stream: int) -> None:
+    check(load().iak_transcode_pages(ctypes.byref(args), stream or None))
+
+
+def prefetch_pages(args: PrefetchArgs, stream: int) -> None:
+    check(load().iak_prefetch_pages(ctypes.byref(args), stream or None))
 
 
 def build_page_tables(args: PageTableArgs, stream: int) -> None:

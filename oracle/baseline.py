@@ -10,7 +10,7 @@ processes (the all-core figure: independent units decoded concurrently).
 
 Jobs return ``(units, seconds)``. Units: one (batch, KV head) row of a decode
 configuration, one MLA sequence of cfg5, one page of the quantise-on-write
-leg, one step of cfg1.
+leg, one step of cfg1, one page demoted and promoted for the transcoding leg.
 """
 from __future__ import annotations
 
@@ -120,6 +120,22 @@ def quantize_job(seed: int, budget_s: float, D: int = 128) -> Tuple[int, float]:
     return done, time.perf_counter() - t0
 
 
+def transcode_job(seed: int, budget_s: float, D: int = 128) -> Tuple[int, float]:
+    """Pages of the KV memory manager's transcoding leg: one unit is a 16 x D
+    float16 page demoted to INT8 (memory.demote_int8) and promoted back
+    (memory.promote_fp16)."""
+    from . import memory as M
+    rng = np.random.default_rng(seed)
+    pages = rng.standard_normal((64, 16, D)).astype(np.float16)
+    done, t0 = 0, time.perf_counter()
+    with _limit_threads():
+        while done == 0 or time.perf_counter() - t0 < budget_s:
+            codes, s = M.demote_int8(pages[done % 64])
+            M.promote_fp16(codes, s)
+            done += 1
+    return done, time.perf_counter() - t0
+
+
 def _cfg1_pages(rng):
     return sorted([0, 1, 2, 3] + [int(p) for p in rng.permutation(52)[:20] + 4] + list(range(56, 64)))
 
@@ -199,7 +215,8 @@ def tables_job(spec_path: str, seed: int, budget_s: float) -> Tuple[int, float]:
     return done, time.perf_counter() - t0
 
 
-JOBS = {"decode": decode_job, "mla": mla_job, "quantize": quantize_job, "cfg1": cfg1_job, "tables": tables_job}
+JOBS = {"decode": decode_job, "mla": mla_job, "quantize": quantize_job, "cfg1": cfg1_job, "tables": tables_job,
+        "transcode": transcode_job}
 
 
 def _run(args):

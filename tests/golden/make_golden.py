@@ -10,7 +10,8 @@ inputs, exactly the functions whose results nothing else pins: the
 float16/float32 arithmetic of ``fake_quantize_tensor`` (G1), router metadata
 on odd layouts (G2), ``fused_selected_quant_decode_reference`` and both
 ``fake_int8_pages_from_fp16`` variants (G3), ``intent_quant_attention_reference``
-(G4) and ``_mla_decode_cpu`` (G5). The fixtures hold inputs and outputs only.
+(G4), ``_mla_decode_cpu`` (G5) and the KV memory manager's INT8 page
+transcoding (G6). The fixtures hold inputs and outputs only.
 """
 from __future__ import annotations
 
@@ -32,6 +33,7 @@ from intent_attention import intent_quant as iq                                 
 from intent_attention import intent_quant_attention as iqa                         # noqa: E402
 from intent_attention import triton_intent_quant_attention as tiq                  # noqa: E402
 from intent_attention import triton_mla_decode as tmd                              # noqa: E402
+from intent_attention import kv_memory_manager as kvm                              # noqa: E402
 
 
 def _np(t: torch.Tensor) -> np.ndarray:
@@ -253,8 +255,45 @@ def g5() -> None:
           page_size=np.array(ps), out=_np(out), out_empty=_np(out_empty))
 
 
+# --------------------------------------------------------------------------- #
+# G6: KVMemoryManager INT8 transcoding (write_page, _read_page_data, set_page_format)
+# --------------------------------------------------------------------------- #
+
+def g6() -> None:
+    g = torch.Generator().manual_seed(6006)
+    out = {}
+    for si, (ps, d) in enumerate(((16, 64), (16, 128), (8, 48))):
+        n = 7
+        pages = torch.randn(n, ps, d, generator=g)
+        pages[1] *= 1e-3                           # small values
+        pages[2, 0, 0] = 60000.0                   # near the top of float16
+        pages[3] = 0.0                             # all zero: scale 1.0
+        pages[4] = torch.round(pages[4] * 8) / 8   # exact eighths: ties after scaling
+        pages[5] *= 3e-6                           # float16 subnormals
+        pages[6] = torch.round(pages[6] * 127) / 127 * 3.0
+        x16 = pages.half()
+        mgr = kvm.KVMemoryManager(num_pages=n, page_size=ps, head_dim=d)
+        ids = mgr.allocate_pages("blk", "ATTEND", n, score=0.1)   # attend_low_format: INT8
+        codes, scales, promoted, codes2, scales2, fp16_back = [], [], [], [], [], []
+        for i, pid in enumerate(ids):
+            mgr.write_page(pid, x16[i])                              # demote (write as INT8)
+            st = mgr.pages[pid]
+            codes.append(_np(st.kv_int8.clone()))
+            scales.append(st.kv_int8_scale)
+            promoted.append(_np(mgr._read_page_data(pid)))          # promote arithmetic
+            mgr.set_page_format(pid, kvm.PageStorageFormat.FP16)     # INT8 -> FP16 transcode
+            fp16_back.append(_np(mgr.pages[pid].kv_fp16.clone()))
+            mgr.set_page_format(pid, kvm.PageStorageFormat.INT8)     # FP16 -> INT8 transcode
+            codes2.append(_np(mgr.pages[pid].kv_int8.clone()))
+            scales2.append(mgr.pages[pid].kv_int8_scale)
+        out.update({f"s{si}_x": _np(x16), f"s{si}_codes": np.stack(codes), f"s{si}_scale": np.array(scales),
+                    f"s{si}_promoted": np.stack(promoted), f"s{si}_fp16_back": np.stack(fp16_back),
+                    f"s{si}_codes2": np.stack(codes2), f"s{si}_scale2": np.array(scales2)})
+    _save("g6_kv_transcode.npz", **out)
+
+
 if __name__ == "__main__":
     torch.set_num_threads(1)
-    which = sys.argv[1:] or ["g1", "g2", "g3", "g4", "g5"]
+    which = sys.argv[1:] or ["g1", "g2", "g3", "g4", "g5", "g6"]
     for w in which:
         globals()[w]()

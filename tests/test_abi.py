@@ -37,6 +37,8 @@ def test_library_exports_every_declared_symbol():
 @pytest.mark.parametrize("cname,pyname", [("iak_paged_decode_args", "PagedDecodeArgs"),
                                           ("iak_mla_decode_args", "MlaDecodeArgs"),
                                           ("iak_quantize_args", "QuantizeArgs"),
+                                          ("iak_transcode_args", "TranscodeArgs"),
+                                          ("iak_prefetch_args", "PrefetchArgs"),
                                           ("iak_page_table_args", "PageTableArgs")])
 def test_ctypes_struct_matches_c_layout(cname, pyname):
     from intent_attention import _native as N
