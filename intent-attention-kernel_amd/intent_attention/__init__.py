@@ -48,6 +48,13 @@ from .quantize import fake_int8_pages_device, quantize_pages
 from .page_tables import build_page_tables, routing_to_kernel_tensors
 from .kv_memory_manager import KVMemoryManager, PageFormatPolicy, PageState, PageStorageFormat
 from .prefetch import BlockPrefetcher, get_prefetch_stream, get_prefetcher, launch_prefetch_pages, reset_prefetcher
+from .triton_adaptive_format_attention import (
+    AdaptiveFormatKernelConfig,
+    AdaptivePageFormat,
+    adaptive_format_decode_attention_reference_dispatch,
+    adaptive_format_decode_attention_triton,
+    make_adaptive_page_tables,
+)
 
 __all__ = [
     "SELECTED_POLICIES", "BlockLayout", "BlockPolicy", "SemanticBlock",
@@ -68,4 +75,6 @@ __all__ = [
     "build_page_tables", "routing_to_kernel_tensors",
     "KVMemoryManager", "PageFormatPolicy", "PageState", "PageStorageFormat",
     "BlockPrefetcher", "get_prefetch_stream", "get_prefetcher", "launch_prefetch_pages", "reset_prefetcher",
+    "AdaptiveFormatKernelConfig", "AdaptivePageFormat", "adaptive_format_decode_attention_reference_dispatch",
+    "adaptive_format_decode_attention_triton", "make_adaptive_page_tables",
 ]
