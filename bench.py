@@ -281,9 +281,9 @@ def build_workload(name: str, device: torch.device, seed: int = 1234, chunk_page
 # decode kernel's sources it was measured on (kernel_source_digest); a build whose
 # sources differ reports traffic null (stale) until the counters are run again.
 MEASURED_TRAFFIC = {
-    "cfg3": {"bytes": 2_101_251_482 + 13_853_491, "src": "b1a3ae648395e56b",
+    "cfg3": {"bytes": 2_105_201_844 + 4_456_448, "src": "fbd947793aa59b0a",
              "source": "profiles/paged_decode_cfg3_hbm_traffic.txt"},
-    "cfg4": {"bytes": 189_766_042 + 2_129_920, "src": "b1a3ae648395e56b",
+    "cfg4": {"bytes": 189_782_836 + 2_129_920, "src": "fbd947793aa59b0a",
              "source": "profiles/paged_decode_cfg4_kernel_stats.txt"},
 }
 KERNEL_SOURCES = ("paged_decode.hip", "iak_device.h", "iak_internal.h")
@@ -965,6 +965,8 @@ def main() -> None:
     ap.add_argument("--cpu-budget", type=float, default=CPU_BUDGET_S,
                     help="seconds of oracle work per CPU-baseline leg (one thread, then all cores)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--merge", choices=("auto", "kernel", "in-kernel"), default="auto",
+                    help="decode legs: where the split partials are merged (auto: the library's choice)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="after the timed steps, run a plain device copy of MIB MiB (read + write "
                          "MIB MiB each): the reference point that scales rocprof FETCH_SIZE/WRITE_SIZE")
@@ -1030,9 +1032,13 @@ def run_decode(args, cpu=None) -> None:
     cfg = wl["cfg"]
     out = torch.empty((cfg["B"], cfg["Hq"], cfg["D"]), dtype=torch.float16, device=dev)
     # one plan per page table; step i runs table i % sets
+    merge = {"auto": None, "kernel": False, "in-kernel": True}[args.merge]
     plans = [make_plan(wl["q"], wl["pools"], t, wl["counts"], wl["tags"], out=out,
-                       pages_per_split=args.pages_per_split) for t in wl["tables"]]
+                       pages_per_split=args.pages_per_split, merge_in_kernel=merge) for t in wl["tables"]]
     plan = plans[0]
+    from intent_attention import _native as N
+    split_plan = N.plan_info(plan.args)
+    fused = split_plan["merge_in_kernel"]
     nsets = len(plans)
     stream = torch.cuda.current_stream(dev)
     for i in range(args.warmup):
@@ -1067,8 +1073,9 @@ def run_decode(args, cpu=None) -> None:
         ab[key] = int(round(sum(x[key] for x in abs_) / nsets))
     ab["per_tag"] = {k: int(round(sum(x["per_tag"][k] for x in abs_) / nsets)) for k in abs_[0]["per_tag"]}
     achieved = ab["total"] / (ms * 1e-3) / 1e9
-    # the split kernel moves every algorithmic byte but the output, which the merge writes
-    kernel_bytes = ab["total"] - ab["qo"] // 2
+    # the split kernel moves every algorithmic byte but the output, which the
+    # merge kernel writes (unless the decode kernel merges itself)
+    kernel_bytes = ab["total"] - (0 if fused else ab["qo"] // 2)
     kernel_gbps = kernel_bytes / (kernel_ms * 1e-3) / 1e9
     med = per[len(per) // 2]
     res = {
@@ -1085,7 +1092,9 @@ def run_decode(args, cpu=None) -> None:
                                + (f", {nsets} disjoint page sets rotated" if nsets > 1 else ""),
                    "selected_pages": ab["pages"], "algorithmic_bytes": ab["total"],
                    "bytes_breakdown": {k: ab[k] for k in ("codes", "scales", "meta", "qo")},
-                   "pages_per_tag": ab["per_tag"], "pages_per_split": plan.args.pages_per_split,
+                   "pages_per_tag": ab["per_tag"], "pages_per_split": split_plan["pages_per_split"],
+                   "splits_per_row": split_plan["splits"],
+                   "merge": "in the decode kernel" if fused else "merge kernel",
                    "gflop": round(flops(wl) / 1e9, 3)},
         "roofline": {"bound": "hbm", "achieved": round(kernel_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(kernel_gbps / HBM_PEAK_GBPS, 4),

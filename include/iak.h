@@ -3,7 +3,8 @@
  * (libiak.so). Plain pointers, sizes and status codes; no torch or HIP types.
  *
  * Ownership: the caller owns every buffer (inputs, output, workspace). The
- * library keeps no global state and allocates nothing; calls are asynchronous
+ * library allocates nothing and keeps no state between calls, apart from the
+ * static per-GPU scratch of iak_paged_decode_noalloc; calls are asynchronous
  * on the caller's HIP stream and never synchronise the host.
  *
  * Reference interfaces these entry points replace (paths relative to the
@@ -13,6 +14,7 @@
  *                               and intent_quant_decode_attention_triton()
  *                                                                      triton_intent_quant_attention.py:342-457
  *   iak_paged_decode_workspace  (no counterpart: sizes the split-K partial buffer the caller allocates)
+ *   iak_paged_decode_plan       (no counterpart: the split plan the library chooses for a call)
  *   iak_paged_decode_timed,     (no counterpart: the same calls with HIP events around the split
  *   iak_mla_decode_timed         kernel, for timing it apart from the merge)
  *   iak_mla_decode              mla_decode_triton() / _mla_decode_cpu()    triton_mla_decode.py:110-186
@@ -41,7 +43,10 @@
 extern "C" {
 #endif
 
-#define IAK_ABI_VERSION 2
+#define IAK_ABI_VERSION 3
+
+/* Grid size from which merge_in_kernel = 2 merges inside the decode kernel. */
+#define IAK_MERGE_IN_KERNEL_MIN_WORKGROUPS 1024
 
 typedef enum {
   IAK_OK = 0,
@@ -103,6 +108,17 @@ enum { IAK_DTYPE_F16 = 0, IAK_DTYPE_F32 = 1, IAK_DTYPE_BF16 = 2 };
  *                (b, h) exists only if e * page_size + t < valid_tokens[b, h] (a ragged
  *                last page); entries wholly past the bound contribute nothing. The page
  *                memory of tokens past the bound is still read and must hold finite values.
+ *   merge_in_kernel  0: a merge kernel combines the split partials after the decode kernel.
+ *                1: the decode kernel merges them itself. 2: automatic -- in-kernel for grids
+ *                of at least IAK_MERGE_IN_KERNEL_MIN_WORKGROUPS workgroups (where the merges
+ *                overlap other workgroups' page streaming), else the merge kernel. In-kernel,
+ *                the four waves of a workgroup
+ *                reduce four consecutive splits of one row (the split count is rounded up
+ *                to a multiple of four) and combine them in LDS into one partial; the
+ *                workgroup that arrives last at the row's arrival counter merges the row's
+ *                partials into the output. The counters live at the end of the workspace:
+ *                they must be zero before a workspace's first use, and every call leaves
+ *                them zero (iak_paged_decode_noalloc ignores this field).
  */
 typedef struct {
   int32_t batch, num_q_heads, num_kv_heads, head_dim, page_size, table_width;
@@ -132,6 +148,7 @@ typedef struct {
   int32_t pages_per_split;
   int32_t map_other_tags;
   const int32_t* valid_tokens;
+  int32_t merge_in_kernel;
 } iak_paged_decode_args;
 
 /* ABI version of the loaded library (IAK_ABI_VERSION). */
@@ -146,6 +163,16 @@ const char* iak_last_error(void);
 /* Bytes of device workspace iak_paged_decode needs for these arguments
  * (0 when the whole reduction fits one split). */
 iak_status iak_paged_decode_workspace(const iak_paged_decode_args* args, size_t* bytes);
+
+/* The split plan iak_paged_decode uses for these arguments. No counterpart in
+ * the reference (its Triton kernel has one program per (batch, head)). */
+typedef struct {
+  int32_t splits;            /* splits per (batch, kv head) row (1: no merge) */
+  int32_t pages_per_split;   /* table entries per split */
+  int32_t merge_in_kernel;   /* 1: the decode kernel merges the splits itself */
+  size_t workspace_bytes;    /* = iak_paged_decode_workspace */
+} iak_paged_decode_plan_info;
+iak_status iak_paged_decode_plan(const iak_paged_decode_args* args, iak_paged_decode_plan_info* info);
 
 /* Selected-page mixed-precision decode attention, split-K over pages with an
  * LSE merge. `workspace` must hold iak_paged_decode_workspace() bytes (may be

@@ -41,7 +41,8 @@ size_t round_up(size_t x) { return (x + WS_ALIGN - 1) / WS_ALIGN * WS_ALIGN; }
 
 struct Plan {
   int G, splits, chunk;
-  size_t ws_m, ws_l, ws_acc, total;   // byte offsets / total
+  bool fused;                                 // the decode kernel merges (merge_in_kernel)
+  size_t ws_m, ws_l, ws_acc, ws_cnt, total;   // byte offsets / total
 };
 
 iak_status validate(const iak_paged_decode_args* a, Plan* plan) {
@@ -126,19 +127,34 @@ iak_status validate(const iak_paged_decode_args* a, Plan* plan) {
   }
   int splits = (W + chunk - 1) / chunk;
   if (splits < 1) splits = 1;
+  // in-kernel merge: a workgroup's four waves take four splits of one row, so
+  // the row's split count becomes a multiple of four (trailing splits may be
+  // empty: they read no entry)
+  // (automatic: only for grids of many workgroups, where each row's merge
+  // overlaps other workgroups' page streaming; its three dependent memory
+  // round trips otherwise lengthen the tail: cfg3, 1,792 workgroups, 337.6 ->
+  // 333.9 us per step; cfg2, 512, unchanged; cfg4, 256, 42.4 -> 43.0 us)
+  bool fused = a->merge_in_kernel != 0 && splits > 1;
+  if (fused && a->merge_in_kernel == 2)
+    fused = rows * (long long)((splits + 3) / 4) >= IAK_MERGE_IN_KERNEL_MIN_WORKGROUPS;
+  if (fused) splits = (splits + 3) / 4 * 4;
   if (rows * (long long)splits > 0x7FFFFFFFLL) return fail(IAK_EINVAL, "too many splits");
   plan->G = G;
   plan->splits = splits;
   plan->chunk = chunk;
-  // workspace: the split partials (m, l, acc); none when one split covers a row
+  plan->fused = fused;
+  // workspace: the split partials (m, l, acc), one per split or, in-kernel,
+  // one per workgroup, then the rows' arrival counters; none when one split
+  // covers a row
   if (splits == 1) {
-    plan->ws_m = plan->ws_l = plan->ws_acc = plan->total = 0;
+    plan->ws_m = plan->ws_l = plan->ws_acc = plan->ws_cnt = plan->total = 0;
   } else {
-    const size_t slots = (size_t)rows * splits * G;
+    const size_t slots = (size_t)rows * (fused ? splits / 4 : splits) * G;
     plan->ws_m = 0;
     plan->ws_l = round_up(slots * sizeof(float));
     plan->ws_acc = plan->ws_l + round_up(slots * sizeof(float));
-    plan->total = plan->ws_acc + round_up(slots * a->head_dim * sizeof(float));
+    plan->ws_cnt = plan->ws_acc + round_up(slots * a->head_dim * sizeof(float));
+    plan->total = plan->ws_cnt + (fused ? round_up((size_t)rows * sizeof(int32_t)) : 0);
   }
   return IAK_OK;
 }
@@ -288,6 +304,18 @@ iak_status iak_paged_decode_workspace(const iak_paged_decode_args* args, size_t*
   return IAK_OK;
 }
 
+iak_status iak_paged_decode_plan(const iak_paged_decode_args* args, iak_paged_decode_plan_info* info) {
+  if (!info) return fail(IAK_EINVAL, "info is NULL");
+  Plan plan;
+  const iak_status st = validate(args, &plan);
+  if (st != IAK_OK) return st;
+  info->splits = plan.splits;
+  info->pages_per_split = plan.chunk;
+  info->merge_in_kernel = plan.fused ? 1 : 0;
+  info->workspace_bytes = plan.total;
+  return IAK_OK;
+}
+
 static iak_status paged_decode_impl(const iak_paged_decode_args* a, void* workspace, size_t workspace_bytes,
                                     void* stream, void* ev_begin, void* ev_end) {
   Plan plan;
@@ -334,6 +362,10 @@ static iak_status paged_decode_impl(const iak_paged_decode_args* a, void* worksp
     k.ws_m = reinterpret_cast<float*>(ws + plan.ws_m);
     k.ws_l = reinterpret_cast<float*>(ws + plan.ws_l);
     k.ws_acc = reinterpret_cast<float*>(ws + plan.ws_acc);
+    if (plan.fused) {
+      k.fused = 1;
+      k.counters = reinterpret_cast<int32_t*>(ws + plan.ws_cnt);
+    }
   }
   const hipError_t e = iak::launch_paged_decode(k, static_cast<hipStream_t>(stream),
                                                 static_cast<hipEvent_t>(ev_begin), static_cast<hipEvent_t>(ev_end));
@@ -351,7 +383,12 @@ iak_status iak_paged_decode_timed(const iak_paged_decode_args* a, void* workspac
   return paged_decode_impl(a, workspace, workspace_bytes, stream, ev_begin, ev_end);
 }
 
-iak_status iak_paged_decode_noalloc(const iak_paged_decode_args* a, void* stream) {
+iak_status iak_paged_decode_noalloc(const iak_paged_decode_args* args, void* stream) {
+  if (!args) return fail(IAK_EINVAL, "args is NULL");
+  // the scratch array holds split partials only: the merge kernel combines them
+  iak_paged_decode_args local = *args;
+  local.merge_in_kernel = 0;
+  const iak_paged_decode_args* a = &local;
   Plan plan;
   const iak_status st = validate(a, &plan);
   if (st != IAK_OK) return st;

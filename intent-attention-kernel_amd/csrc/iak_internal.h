@@ -59,6 +59,11 @@ struct KArgs {
   float* ws_l;        // [B, Hkv, splits, G]
   float* ws_acc;      // [B, Hkv, splits, G, D]
   int acc16;          // ws_acc holds acc / l as float16 (the MLA kernel's compact partials)
+
+  // merge inside the decode kernel: the partials are per workgroup (4 splits),
+  // [B, Hkv, splits / 4, G] and [.., D]; counters [B * Hkv] arrivals per row
+  int fused;
+  int32_t* counters;
 };
 
 // ev_begin / ev_end (may be null) are recorded on `stream` around the split

@@ -543,6 +543,112 @@ __device__ void write_result(const KArgs& a, const Split& sp, Wave<D, QT != IAK_
   }
 }
 
+// In-kernel merge (KArgs::fused). The workgroup's four waves hold splits
+// 4j .. 4j+3 of one row (the plan makes the split count a multiple of four).
+// Each wave puts its (m, l, acc * 2^E) per head into the LDS, the workgroup
+// combines the four with the log-sum-exp rule into the row's partial j, and
+// the workgroup that arrives last at the row's counter merges the row's
+// splits / 4 partials into the output, then resets the counter for the next
+// call.
+// Visibility across the XCDs (each has its own L2): the partials are written
+// and read with agent-scope atomic stores and loads, which the L2 writes
+// through to memory and re-reads from it (the sc1 scope bit), and the stores
+// are acknowledged (s_waitcnt vmcnt(0)) before the barrier that precedes the
+// arrival. No agent-scope fence is used: its release half writes back the
+// whole L2 (buffer_wbl2), which took the cfg3 decode from 333 to 645 us.
+// `red`: LDS [4 waves][16 heads][D] floats (the K transpose buffers, done with).
+template <int D, int QT>
+__device__ void merge_in_kernel(const KArgs& a, const Split& sp, const Wave<D, QT != IAK_DTYPE_F16>& w, int c,
+                                int g, float* red, int wv) {
+  __shared__ float red_m[IAK_WAVES_PER_BLOCK][16], red_l[IAK_WAVES_PER_BLOCK][16];
+  __shared__ int last;
+  constexpr int WR = 16 * D;   // floats per wave
+  const float l = xsum16_32(w.l);
+  // this wave's K transpose reads are done before its region is overwritten
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  if (c < a.G) {
+    if (g == 0) { red_m[wv][c] = w.m; red_l[wv][c] = l; }
+    const float vscale = pow2f(w.E);   // the value sum is acc * 2^E
+    float* mine = red + wv * WR + c * D + (D / 4) * g;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+#pragma unroll
+      for (int mb = 0; mb < D / 16; ++mb) mine[(D / 16) * r + mb] = w.acc[mb][r] * vscale;
+    }
+  }
+  __syncthreads();
+
+  const int t = threadIdx.x;
+  const int GD = a.G * D;
+  const int nwg = a.splits >> 2, j = sp.split >> 2;
+  const int64_t row = (int64_t)sp.b * a.Hkv + sp.hk;
+  const int64_t first = row * nwg * a.G;   // partial slot of (row, 0, head 0)
+  for (int o = t; o < GD; o += 64 * IAK_WAVES_PER_BLOCK) {
+    const int h = o / D;
+    float M = -__builtin_inff();
+#pragma unroll
+    for (int k = 0; k < IAK_WAVES_PER_BLOCK; ++k) M = fmaxf(M, red_m[k][h]);
+    float L = 0.f, A = 0.f;
+    if (M > -__builtin_inff()) {
+#pragma unroll
+      for (int k = 0; k < IAK_WAVES_PER_BLOCK; ++k) {
+        const float wt = __builtin_amdgcn_exp2f(red_m[k][h] - M);   // 0 for an empty split (m = -inf)
+        L += wt * red_l[k][h];
+        A += wt * red[k * WR + o];
+      }
+    }
+    const int64_t slot = first + (int64_t)j * a.G + h;
+    __hip_atomic_store(a.ws_acc + slot * D + (o - h * D), A, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (o == h * D) {
+      __hip_atomic_store(a.ws_m + slot, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a.ws_l + slot, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  // this workgroup's partial has reached memory before its arrival is counted
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (t == 0) last = atomicAdd(a.counters + row, 1) == nwg - 1;
+  __syncthreads();
+  if (!last) return;
+
+  // the row's merge: output (head h, dim d) from the nwg workgroup partials
+  for (int o = t; o < GD; o += 64 * IAK_WAVES_PER_BLOCK) {
+    const int h = o / D, d = o - h * D;
+    const int64_t s0 = first + h;
+    float M = -__builtin_inff();
+    for (int k = 0; k < nwg; ++k)
+      M = fmaxf(M, __hip_atomic_load(a.ws_m + s0 + (int64_t)k * a.G, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    float L = 0.f, A = 0.f;
+    if (M > -__builtin_inff()) {
+      constexpr int U = 8;
+      for (int i = 0; i < nwg; i += U) {
+        float ms[U], ls[U], av[U];
+#pragma unroll
+        for (int k = 0; k < U; ++k) {
+          const int64_t s = s0 + (int64_t)(i + k < nwg ? i + k : nwg - 1) * a.G;
+          ms[k] = __hip_atomic_load(a.ws_m + s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          ls[k] = __hip_atomic_load(a.ws_l + s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          av[k] = __hip_atomic_load(a.ws_acc + s * D + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (int k = 0; k < U; ++k) {
+          const float wt = i + k < nwg ? __builtin_amdgcn_exp2f(ms[k] - M) : 0.f;
+          L += wt * ls[k];
+          A += wt * av[k];
+        }
+      }
+    }
+    const float v = A * (L > 0.f ? 1.0f / L : 0.f);
+    const int64_t op = (int64_t)sp.b * a.osb + (int64_t)(sp.hk * a.G + h) * a.osh + d;
+    if (a.out_dtype == IAK_DTYPE_F32) reinterpret_cast<float*>(a.out)[op] = v;
+    else if (a.out_dtype == IAK_DTYPE_F16) reinterpret_cast<_Float16*>(a.out)[op] = (_Float16)v;
+    else reinterpret_cast<__bf16*>(a.out)[op] = (__bf16)v;
+  }
+  // reset for the next call, written through like the partials (its cache
+  // line holds other rows' counters)
+  if (t == 0) __hip_atomic_store(a.counters + row, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Q operand of head c (zero for padding columns): dims (D/4)g + 8i .. +7 of step i,
 // loaded as 16-byte vectors (the C ABI checks 16-byte alignment of q rows).
 template <int D, int QT>
@@ -691,10 +797,13 @@ void paged_decode_kernel(const KArgs a) {
   const int lane = threadIdx.x & 63;
   const int c = lane & 15, g = lane >> 4;
   const int item = blockIdx.x * IAK_WAVES_PER_BLOCK + (threadIdx.x >> 6);
-  if (item >= a.items) return;
-  // the wave's K transpose buffer: one FP16 page's K (a one-byte page uses half)
-  __shared__ u4 kt_all[IAK_WAVES_PER_BLOCK][PS * D / 8];
-  u4* kt = kt_all[threadIdx.x >> 6];
+  if (item >= a.items) return;   // never taken by an in-kernel-merge grid (whole workgroups)
+  // the wave's K transpose buffer: one FP16 page's K (a one-byte page uses
+  // half), in dynamic LDS whose per-wave stride also holds the in-kernel merge's
+  // 16 x D floats when a.fused
+  extern __shared__ u4 decode_lds[];
+  const int wv = threadIdx.x >> 6;
+  u4* kt = decode_lds + wv * (a.fused ? 4 * D : PS * D / 8);
 
   Split sp;
   int pid, tag, lim;
@@ -796,18 +905,25 @@ void paged_decode_kernel(const KArgs a) {
         });
   }
 
+  if (a.fused) {
+    merge_in_kernel<D, QT>(a, sp, w, c, g, reinterpret_cast<float*>(decode_lds), wv);
+    return;
+  }
   write_result<D, QT>(a, sp, w, c, g);
 }
 
 template <int D, int QT>
 hipError_t launch_decode(const KArgs& k, hipStream_t stream, hipEvent_t ev_begin, hipEvent_t ev_end) {
   const int blocks = (k.items + IAK_WAVES_PER_BLOCK - 1) / IAK_WAVES_PER_BLOCK;
+  // per-wave LDS: the K transpose buffer (PS x D halves), or 16 x D floats for
+  // the in-kernel merge
+  const size_t lds = (size_t)IAK_WAVES_PER_BLOCK * (k.fused ? 4 * D : PS * D / 8) * sizeof(u4);
   if (ev_begin) (void)hipEventRecord(ev_begin, stream);
-  hipLaunchKernelGGL((paged_decode_kernel<D, QT>), dim3(blocks), dim3(64 * IAK_WAVES_PER_BLOCK), 0,
+  hipLaunchKernelGGL((paged_decode_kernel<D, QT>), dim3(blocks), dim3(64 * IAK_WAVES_PER_BLOCK), lds,
                      stream, k);
   hipError_t e = hipGetLastError();
   if (ev_end) (void)hipEventRecord(ev_end, stream);
-  if (e != hipSuccess || k.splits == 1) return e;
+  if (e != hipSuccess || k.splits == 1 || k.fused) return e;
   return launch_merge<D>(k, stream);
 }
 

@@ -14,7 +14,7 @@ from typing import Optional
 _HERE = os.path.dirname(os.path.abspath(__file__))
 # IAK_LIBRARY selects another build of the same ABI (e.g. a tuning variant)
 LIB_PATH = os.environ.get("IAK_LIBRARY") or os.path.join(_HERE, "libiak.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 IAK_OK, IAK_EINVAL, IAK_ENOTSUP, IAK_EHIP = 0, 1, 2, 3
 
@@ -50,6 +50,7 @@ class PagedDecodeArgs(ctypes.Structure):
         ("pages_per_split", c_i32),
         ("map_other_tags", c_i32),
         ("valid_tokens", c_void_p),
+        ("merge_in_kernel", c_i32),
     ]
 
 
@@ -130,7 +131,7 @@ EXPORTED = ("iak_abi_version", "iak_status_string", "iak_last_error",
             "iak_paged_decode_workspace", "iak_paged_decode",
             "iak_mla_decode_workspace", "iak_mla_decode", "iak_quantize_pages",
             "iak_build_page_tables", "iak_paged_decode_timed", "iak_mla_decode_timed",
-            "iak_paged_decode_noalloc", "iak_transcode_pages", "iak_prefetch_pages")
+            "iak_paged_decode_noalloc", "iak_transcode_pages", "iak_prefetch_pages", "iak_paged_decode_plan")
 NOALLOC_SCRATCH_BYTES = 16 << 20   # IAK_NOALLOC_SCRATCH_BYTES
 
 _lib: Optional[ctypes.CDLL] = None
@@ -161,6 +162,8 @@ def load() -> ctypes.CDLL:
     lib.iak_last_error.argtypes = []
     lib.iak_paged_decode_workspace.restype = ctypes.c_int
     lib.iak_paged_decode_workspace.argtypes = [ctypes.POINTER(PagedDecodeArgs), ctypes.POINTER(ctypes.c_size_t)]
+    lib.iak_paged_decode_plan.restype = ctypes.c_int
+    lib.iak_paged_decode_plan.argtypes = [ctypes.POINTER(PagedDecodeArgs), ctypes.POINTER(PlanInfo)]
     lib.iak_paged_decode.restype = ctypes.c_int
     lib.iak_paged_decode.argtypes = [ctypes.POINTER(PagedDecodeArgs), c_void_p, ctypes.c_size_t, c_void_p]
     lib.iak_mla_decode_workspace.restype = ctypes.c_int
@@ -201,6 +204,21 @@ def check(status: int) -> None:
     if status in (IAK_EINVAL, IAK_ENOTSUP):
         raise ValueError(f"{msg} ({what})")
     raise RuntimeError(f"{msg} ({what})")
+
+
+class PlanInfo(ctypes.Structure):
+    """Mirror of ``iak_paged_decode_plan_info`` (include/iak.h)."""
+
+    _fields_ = [("splits", c_i32), ("pages_per_split", c_i32), ("merge_in_kernel", c_i32),
+                ("workspace_bytes", ctypes.c_size_t)]
+
+
+def plan_info(args: PagedDecodeArgs) -> dict:
+    """The split plan the library chooses for ``args``."""
+    info = PlanInfo()
+    check(load().iak_paged_decode_plan(ctypes.byref(args), ctypes.byref(info)))
+    return {"splits": int(info.splits), "pages_per_split": int(info.pages_per_split),
+            "merge_in_kernel": bool(info.merge_in_kernel), "workspace_bytes": int(info.workspace_bytes)}
 
 
 def workspace_bytes(args: PagedDecodeArgs) -> int:

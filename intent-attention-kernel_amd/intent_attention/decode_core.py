@@ -18,6 +18,9 @@ import torch
 from . import _native as N
 
 PAGE_SIZE = 16
+# iak_paged_decode_args.merge_in_kernel for merge_in_kernel=None: automatic (the
+# decode kernel merges its split partials itself on grids of many workgroups)
+MERGE_IN_KERNEL_AUTO = 2
 
 _DT = {torch.float16: N.DTYPE_F16, torch.float32: N.DTYPE_F32, torch.bfloat16: N.DTYPE_BF16}
 
@@ -116,7 +119,8 @@ def paged_decode(q: torch.Tensor, pools: PagePools, page_table: torch.Tensor, pa
                  negative_ids: bool = False, sm_scale: Optional[float] = None,
                  out: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None,
                  pages_per_split: int = 0, map_other_tags: bool = False,
-                 valid_tokens: Optional[torch.Tensor] = None) -> torch.Tensor:
+                 valid_tokens: Optional[torch.Tensor] = None,
+                 merge_in_kernel: Optional[bool] = None) -> torch.Tensor:
     """Selected-page decode attention on the GPU.
 
     q [B, Hq, D] (f16 / f32 / bf16, any strides with unit last stride);
@@ -128,11 +132,14 @@ def paged_decode(q: torch.Tensor, pools: PagePools, page_table: torch.Tensor, pa
     ``map_other_tags``. Query head h uses row h // (Hq // Hkv).
     ``valid_tokens`` [B, Hkv] int32 (optional): token t of table entry e of a
     row exists only if e * 16 + t < valid_tokens[row] (a ragged last page).
+    ``merge_in_kernel``: True: the decode kernel merges the split partials
+    itself (one launch); False: a merge kernel after it; None: the library
+    chooses (in-kernel on grids of many workgroups).
     Returns out [B, Hq, D].
     """
     plan = make_plan(q, pools, page_table, page_counts, page_tags, tag_map=tag_map, negative_ids=negative_ids,
                      sm_scale=sm_scale, out=out, out_dtype=out_dtype, pages_per_split=pages_per_split,
-                     map_other_tags=map_other_tags, valid_tokens=valid_tokens)
+                     map_other_tags=map_other_tags, valid_tokens=valid_tokens, merge_in_kernel=merge_in_kernel)
     plan.run()
     return plan.out
 
@@ -142,7 +149,8 @@ def make_plan(q: torch.Tensor, pools: PagePools, page_table: torch.Tensor, page_
               negative_ids: bool = False, sm_scale: Optional[float] = None,
               out: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None,
               pages_per_split: int = 0, map_other_tags: bool = False,
-              valid_tokens: Optional[torch.Tensor] = None) -> "DecodePlan":
+              valid_tokens: Optional[torch.Tensor] = None,
+              merge_in_kernel: Optional[bool] = None) -> "DecodePlan":
     """Validate the arguments of ``paged_decode`` once; the returned plan
     re-launches the decode on the same tensors with ``run()``."""
     if q.dim() != 3:
@@ -238,6 +246,7 @@ def make_plan(q: torch.Tensor, pools: PagePools, page_table: torch.Tensor, page_
     a.pages_per_split = int(pages_per_split)
     a.map_other_tags = 1 if map_other_tags else 0
     a.valid_tokens = _ptr(valid_tokens)
+    a.merge_in_kernel = MERGE_IN_KERNEL_AUTO if merge_in_kernel is None else (1 if merge_in_kernel else 0)
 
     return DecodePlan(a, dev, out, keep=(q, page_table, page_counts, page_tags, valid_tokens, pools))
 
@@ -253,8 +262,10 @@ class DecodePlan:
         self.out = out
         self._keep = keep
         self.workspace_bytes = N.workspace_bytes(args)
-        self._ws = (torch.empty(self.workspace_bytes, dtype=torch.uint8, device=device)
-                    if self.workspace_bytes else None)
+        # the in-kernel merge's arrival counters (at the end of the workspace)
+        # start at zero, and every run leaves them zero
+        alloc = torch.zeros if args.merge_in_kernel else torch.empty
+        self._ws = alloc(self.workspace_bytes, dtype=torch.uint8, device=device) if self.workspace_bytes else None
 
     def run(self, stream: Optional[int] = None, events: Optional[tuple] = None) -> None:
         """Launch on ``stream`` (default: torch's current stream). ``events``: an

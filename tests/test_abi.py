@@ -39,7 +39,8 @@ def test_library_exports_every_declared_symbol():
                                           ("iak_quantize_args", "QuantizeArgs"),
                                           ("iak_transcode_args", "TranscodeArgs"),
                                           ("iak_prefetch_args", "PrefetchArgs"),
-                                          ("iak_page_table_args", "PageTableArgs")])
+                                          ("iak_page_table_args", "PageTableArgs"),
+                                          ("iak_paged_decode_plan_info", "PlanInfo")])
 def test_ctypes_struct_matches_c_layout(cname, pyname):
     from intent_attention import _native as N
     S = getattr(N, pyname)
@@ -162,3 +163,45 @@ def test_page_table_validation_errors_without_gpu():
     a.num_rows, a.page_table, a.page_counts, a.page_precision = 4, 32, 64, 18   # precision 2 bytes off
     with pytest.raises(ValueError, match="4-byte aligned"):
         N.build_page_tables(a, 0)
+
+
+def _decode_args(N, B, Hkv, G, W):
+    a = N.PagedDecodeArgs()
+    a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim, a.page_size = B, Hkv * G, Hkv, 128, 16
+    a.table_width, a.num_pages = W, 1 << 20
+    a.q = a.out = a.page_table = a.page_counts = a.page_tags = a.k_fp16 = a.v_fp16 = 16
+    for i in range(8):
+        a.tag_map[i] = N.TAG_FP16 if i == 0 else N.TAG_SKIP
+    a.sm_scale = 0.1
+    return a
+
+
+def test_split_plan_and_merge_form_without_gpu():
+    """merge_in_kernel: 0 keeps the split count and the merge kernel; 1 rounds
+    the split count up to whole workgroups of four and sizes one partial per
+    workgroup plus one counter per row; 2 picks the in-kernel form only for
+    grids of IAK_MERGE_IN_KERNEL_MIN_WORKGROUPS workgroups or more."""
+    from intent_attention import _native as N
+    rows_cfg3, rows_cfg4 = (32, 8, 4, 1638), (4, 8, 4, 1229)
+    a = _decode_args(N, *rows_cfg3)
+    p0 = N.plan_info(a)
+    assert (p0["splits"], p0["pages_per_split"], p0["merge_in_kernel"]) == (26, 63, False)
+    a.merge_in_kernel = 1
+    p1 = N.plan_info(a)
+    assert p1["splits"] == 28 and p1["splits"] % 4 == 0 and p1["merge_in_kernel"]
+    assert p1["pages_per_split"] * (p1["splits"] - 4) < 1638 <= p1["pages_per_split"] * p1["splits"]
+    rows, G, D = 256, 4, 128
+    slots = rows * (p1["splits"] // 4) * G
+    r256 = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    assert p1["workspace_bytes"] == 2 * r256(4 * slots) + r256(4 * slots * D) + r256(4 * rows)
+    assert p1["workspace_bytes"] == N.workspace_bytes(a)
+    a.merge_in_kernel = 2                       # 256 rows x 7 workgroups: in-kernel
+    assert N.plan_info(a)["merge_in_kernel"]
+    b = _decode_args(N, *rows_cfg4)
+    b.merge_in_kernel = 2                       # 32 rows x 8 workgroups: the merge kernel
+    p4 = N.plan_info(b)
+    assert not p4["merge_in_kernel"] and p4["splits"] == 32
+    c = _decode_args(N, 1, 2, 4, 40)            # one split per row: no merge, no workspace
+    c.merge_in_kernel, c.pages_per_split = 1, 64
+    pc = N.plan_info(c)
+    assert pc["splits"] == 1 and not pc["merge_in_kernel"] and pc["workspace_bytes"] == 0

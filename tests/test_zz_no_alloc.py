@@ -1,8 +1,9 @@
 """iak_paged_decode_noalloc (no caller workspace, no allocation: the split-K
 partials in the library's own per-GPU scratch) against iak_paged_decode with
-a caller workspace, through the C ABI: two calls in a row, the second with a
-smaller input, each bit-identical to the workspace entry point (the same
-kernels and split plan) and within the quantised-page bar of the oracle; a
+a caller workspace and the merge kernel (merge_in_kernel = 0, the form the
+no-alloc entry point always takes), through the C ABI: two calls in a row, the
+second with a smaller input, each bit-identical to the workspace entry point
+(the same kernels and split plan) and within the quantised-page bar of the oracle; a
 call whose partials exceed the scratch is rejected before any launch."""
 import sys
 
@@ -27,7 +28,7 @@ def _case(dev, seed, B, Hq, Hkv, W, NP, pps):
     q, pools, table, counts, tags = random_case(seed, B, Hq, Hkv, 128, NP, W, mix, outliers=0.01)
     t = lambda x: torch.from_numpy(x).to(dev)  # noqa: E731
     plan = make_plan(t(q), to_device_pools(pools, dev), t(table), t(counts), t(tags), out_dtype=torch.float32,
-                     pages_per_split=pps)
+                     pages_per_split=pps, merge_in_kernel=False)
     return plan, (q, pools, table, counts, tags)
 
 
@@ -66,7 +67,7 @@ def test_noalloc_rejects_partials_above_the_scratch():
     plan = make_plan(torch.zeros(B, Hq, D, dtype=torch.float16, device=dev), pools,
                      torch.zeros(B, Hkv, W, dtype=torch.int32, device=dev),
                      torch.full((B, Hkv), W, dtype=torch.int32, device=dev),
-                     torch.zeros(NP, dtype=torch.int32, device=dev), pages_per_split=64)
+                     torch.zeros(NP, dtype=torch.int32, device=dev), pages_per_split=64, merge_in_kernel=False)
     assert plan.workspace_bytes > N.NOALLOC_SCRATCH_BYTES
     with pytest.raises(ValueError, match="no-alloc scratch"):
         N.paged_decode_noalloc(plan.args, torch.cuda.current_stream(dev).cuda_stream)
