@@ -21,6 +21,10 @@
  *                               (the latent context; mla_sparse_decode_reference mla.py:61-92,
  *                               mla_triton_decode mla.py:95-136)
  *   iak_mla_decode_workspace    (no counterpart: sizes the split-K partial buffer)
+ *   iak_mla_decode_rows         the latent context of mla_decode_triton() in the reference's float32
+ *                               arithmetic: its Triton kernel triton_mla_decode.py:47-107 and
+ *                               _mla_decode_cpu :155-186 (also under mla_sparse_decode_reference /
+ *                               mla_triton_decode, mla.py:61-136)
  *   iak_quantize_pages          fake_quantize_tensor() intent_quant.py:221-312 at page granules, and
  *                               fake_int8_pages_from_fp16() fused_selected_quant_decode.py:521-542 /
  *                               triton_intent_quant_attention.py:460-496
@@ -383,6 +387,31 @@ typedef struct {
 
 /* Warm pages into the caches; async on `stream`. */
 iak_status iak_prefetch_pages(const iak_prefetch_args* args, void* stream);
+
+/* Latent context of the reference's MLA decode API (mla_decode_triton,
+ * triton_mla_decode.py:47-107 / _mla_decode_cpu :155-186), in float32: for each
+ * (batch, query position) row, softmax((q . c) * sm_scale) over the latent rows
+ * of the listed pages, context = sum(p c) / sum(p), zeros when nothing is
+ * visited. Page p is rows p * page_size .. (p + 1) * page_size - 1 of the
+ * latents (the last page may be shorter); ids outside [0, ceil(num_rows /
+ * page_size)) are rejected by the caller's contract and skipped by the kernel.
+ *
+ *   q        [batch, q_len, latent_dim] (q_dtype), element strides q_stride_b / q_stride_t
+ *   latents  [num_rows, latent_dim] (latent_dtype), element row stride latent_stride
+ *   page_ids [num_selected] int32, shared by every row
+ *   context  [batch, q_len, latent_dim] float32, contiguous (written)
+ *   latent_dim <= 1024; any page_size >= 1. */
+typedef struct {
+  int32_t batch, q_len, latent_dim, page_size, num_selected;
+  int64_t num_rows;
+  const void* q; int32_t q_dtype; int64_t q_stride_b, q_stride_t;
+  const void* latents; int32_t latent_dtype; int64_t latent_stride;
+  const int32_t* page_ids;
+  float* context;
+  float sm_scale;
+} iak_mla_rows_args;
+
+iak_status iak_mla_decode_rows(const iak_mla_rows_args* args, void* stream);
 
 #ifdef __cplusplus
 }

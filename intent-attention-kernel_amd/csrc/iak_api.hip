@@ -279,6 +279,10 @@ iak_status scratch_address(int dev, void** out) {
 
 }  // namespace
 
+namespace iak {
+hipError_t launch_mla_rows(const iak_mla_rows_args& a, hipStream_t stream);   // mla_rows.hip
+}
+
 extern "C" {
 
 int iak_abi_version(void) { return IAK_ABI_VERSION; }
@@ -539,6 +543,27 @@ iak_status iak_prefetch_pages(const iak_prefetch_args* a, void* stream) {
   if ((reinterpret_cast<uintptr_t>(a->k) | reinterpret_cast<uintptr_t>(a->v)) & 1u)
     return fail(IAK_EINVAL, "k/v must be 2-byte aligned");
   const hipError_t e = iak::launch_prefetch(*a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(IAK_EHIP, "kernel launch failed: %s", hipGetErrorString(e));
+  return IAK_OK;
+}
+
+iak_status iak_mla_decode_rows(const iak_mla_rows_args* a, void* stream) {
+  if (!a) return fail(IAK_EINVAL, "args is NULL");
+  if (a->batch < 0 || a->q_len < 0 || a->num_selected < 0 || a->num_rows < 0)
+    return fail(IAK_EINVAL, "negative size (batch=%d, q_len=%d, num_selected=%d, num_rows=%lld)", a->batch, a->q_len,
+                a->num_selected, (long long)a->num_rows);
+  if (a->latent_dim <= 0 || a->latent_dim > 1024)
+    return fail(IAK_ENOTSUP, "latent_dim %d is not supported (1 .. 1024)", a->latent_dim);
+  if (a->page_size <= 0) return fail(IAK_EINVAL, "page_size must be positive, got %d", a->page_size);
+  if ((long long)a->batch * a->q_len > 0x7FFFFFFFLL) return fail(IAK_EINVAL, "batch * q_len too large");
+  for (int dt : {a->q_dtype, a->latent_dtype})
+    if (dt < 0 || dt > 2) return fail(IAK_EINVAL, "unknown dtype %d", dt);
+  if ((long long)a->batch * a->q_len == 0) return IAK_OK;
+  if (!a->q || !a->context) return fail(IAK_EINVAL, "q/context is NULL");
+  if (a->num_selected > 0 && (!a->page_ids || !a->latents)) return fail(IAK_EINVAL, "page_ids/latents is NULL");
+  if (a->latent_stride < a->latent_dim && a->num_rows > 1)
+    return fail(IAK_EINVAL, "latent_stride %lld is below latent_dim %d", (long long)a->latent_stride, a->latent_dim);
+  const hipError_t e = iak::launch_mla_rows(*a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(IAK_EHIP, "kernel launch failed: %s", hipGetErrorString(e));
   return IAK_OK;
 }

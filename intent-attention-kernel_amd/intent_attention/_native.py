@@ -127,11 +127,26 @@ class PrefetchArgs(ctypes.Structure):
     ]
 
 
+class MlaRowsArgs(ctypes.Structure):
+    """Mirror of ``iak_mla_rows_args`` (include/iak.h)."""
+
+    _fields_ = [
+        ("batch", c_i32), ("q_len", c_i32), ("latent_dim", c_i32), ("page_size", c_i32), ("num_selected", c_i32),
+        ("num_rows", c_i64),
+        ("q", c_void_p), ("q_dtype", c_i32), ("q_stride_b", c_i64), ("q_stride_t", c_i64),
+        ("latents", c_void_p), ("latent_dtype", c_i32), ("latent_stride", c_i64),
+        ("page_ids", c_void_p),
+        ("context", c_void_p),
+        ("sm_scale", c_float),
+    ]
+
+
 EXPORTED = ("iak_abi_version", "iak_status_string", "iak_last_error",
             "iak_paged_decode_workspace", "iak_paged_decode",
             "iak_mla_decode_workspace", "iak_mla_decode", "iak_quantize_pages",
             "iak_build_page_tables", "iak_paged_decode_timed", "iak_mla_decode_timed",
-            "iak_paged_decode_noalloc", "iak_transcode_pages", "iak_prefetch_pages", "iak_paged_decode_plan")
+            "iak_paged_decode_noalloc", "iak_transcode_pages", "iak_prefetch_pages", "iak_paged_decode_plan",
+            "iak_mla_decode_rows")
 NOALLOC_SCRATCH_BYTES = 16 << 20   # IAK_NOALLOC_SCRATCH_BYTES
 
 _lib: Optional[ctypes.CDLL] = None
@@ -185,6 +200,8 @@ def load() -> ctypes.CDLL:
     lib.iak_prefetch_pages.restype = ctypes.c_int
     lib.iak_prefetch_pages.argtypes = [ctypes.POINTER(PrefetchArgs), c_void_p]
     lib.iak_build_page_tables.restype = ctypes.c_int
+    lib.iak_mla_decode_rows.restype = ctypes.c_int
+    lib.iak_mla_decode_rows.argtypes = [ctypes.POINTER(MlaRowsArgs), c_void_p]
     lib.iak_build_page_tables.argtypes = [ctypes.POINTER(PageTableArgs), c_void_p]
     ver = lib.iak_abi_version()
     if ver != ABI_VERSION:
@@ -268,6 +285,10 @@ def transcode_pages(args: TranscodeArgs, stream: int) -> None:
 
 def prefetch_pages(args: PrefetchArgs, stream: int) -> None:
     check(load().iak_prefetch_pages(ctypes.byref(args), stream or None))
+
+
+def mla_decode_rows(args: MlaRowsArgs, stream: int) -> None:
+    check(load().iak_mla_decode_rows(ctypes.byref(args), stream or None))
 
 
 def build_page_tables(args: PageTableArgs, stream: int) -> None:

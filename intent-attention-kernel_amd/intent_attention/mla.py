@@ -3,8 +3,8 @@ with the reference's interface (src/intent_attention/mla.py).
 
 ``MLAConfig``, ``absorb_weights`` and ``MLABlockTable`` keep the reference's
 definitions (mla.py:15-58). The two decode entry points run the latent
-attention on the MI355X MFMA kernel (``triton_mla_decode.mla_latent_context``)
-and keep the reference's results:
+attention on libiak's float32 row kernel (``triton_mla_decode.mla_latent_context``,
+the reference's arithmetic) and keep the reference's results:
 
 * ``mla_sparse_decode_reference`` (mla.py:61-92): the selected blocks' latents
   concatenated, ``softmax(q_absorb C^T / sqrt(d_c)) C @ W_VO`` returned as

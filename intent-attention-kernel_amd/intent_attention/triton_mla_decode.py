@@ -1,16 +1,18 @@
-"""Drop-in for the reference's ``triton_mla_decode`` module on the MI355X
-MFMA kernel (``mla_core.mla_paged_decode``).
+"""Drop-in for the reference's ``triton_mla_decode`` module on the MI355X.
 
 ``mla_decode_triton`` keeps the reference signature and result
 (triton_mla_decode.py:110-152): ``q_absorb [batch, q_len, d_c]`` attends to the
 latent rows of the pages listed in a 1-D ``page_table`` shared by the batch
-(page ``p`` = rows ``p*page_size .. (p+1)*page_size - 1`` of ``C [T, d_c]``),
-softmax scale ``1/sqrt(d_c)``, and the context is projected by ``W_VO_fused``;
-zeros when the table is empty. The selected rows are gathered in table order
-into 16-row pages of float16 (any ``page_size``; the last page of ``C`` may be
-shorter, and the gathered rows are bounded by the kernel's token count), ``d_c`` is zero-padded to a supported width
-(64, 128, 256, 512 or 576), and the projection is one float32 GEMM. Host
-tensors raise RuntimeError: there is no CPU path in this package.
+(page ``p`` = rows ``p*page_size .. (p+1)*page_size - 1`` of ``C [T, d_c]``,
+the last page of ``C`` possibly shorter), softmax scale ``1/sqrt(d_c)``, and
+the context is projected by ``W_VO_fused``; zeros when the table is empty.
+
+The latent context runs on libiak's ``iak_mla_decode_rows`` in the reference's
+arithmetic: float32 products and sums over the inputs as given (float32,
+float16 or bfloat16, read in place), any ``page_size``, any ``d_c`` up to 1,024
+in one launch. The projection is one float32 GEMM. (The paged serving path,
+``mla_core.mla_paged_decode``, is the MFMA kernel over f16 / FP8 / INT8 latent
+pools.) Host tensors raise RuntimeError: there is no CPU path in this package.
 """
 from __future__ import annotations
 
@@ -18,10 +20,11 @@ import math
 
 import torch
 
+from . import _native as N
 from .decode_core import require_device
-from .mla_core import LatentPools, mla_paged_decode
 
-_WIDTHS = (64, 128, 256, 512, 576)
+_DT = {torch.float32: N.DTYPE_F32, torch.float16: N.DTYPE_F16, torch.bfloat16: N.DTYPE_BF16}
+MAX_LATENT = 1024
 
 
 def is_triton_available() -> bool:
@@ -42,41 +45,34 @@ def mla_latent_context(q_absorb: torch.Tensor, C: torch.Tensor, page_table: torc
         raise ValueError(f"q_absorb must be [batch, q_len, d_c] and C [T, d_c], got {tuple(q_absorb.shape)} "
                          f"and {tuple(C.shape)}")
     batch, q_len, d_c = q_absorb.shape
-    if d_c > _WIDTHS[-1]:
-        raise ValueError(f"d_c {d_c} exceeds the widest supported latent ({_WIDTHS[-1]})")
+    if d_c > MAX_LATENT:
+        raise ValueError(f"d_c {d_c} exceeds the widest supported latent ({MAX_LATENT})")
     if page_size <= 0:
         raise ValueError(f"page_size must be positive, got {page_size}")
-    ids = page_table.reshape(-1).to(device=dev, dtype=torch.int64)
-    n_sel = ids.numel()
-    if n_sel == 0:
-        return torch.zeros(batch, q_len, d_c, dtype=torch.float32, device=dev)
+    if q_absorb.dtype not in _DT or C.dtype not in _DT:
+        raise ValueError(f"q_absorb and C must be float32, float16 or bfloat16, got {q_absorb.dtype} and {C.dtype}")
+    ids = page_table.reshape(-1).to(device=dev, dtype=torch.int32)
+    ctx = torch.empty(batch, q_len, d_c, dtype=torch.float32, device=dev)
+    if ids.numel() == 0 or batch * q_len == 0:
+        return ctx.zero_()
     # page p is rows p*page_size .. (p+1)*page_size - 1 of C, the last page of
     # C possibly shorter (the reference slices C[p*ps:(p+1)*ps])
     n_src = (C.shape[0] + page_size - 1) // page_size
     if int(ids.min()) < 0 or int(ids.max()) >= n_src:
         raise ValueError(f"page ids must lie in [0, {n_src})")
-    width = next(w for w in _WIDTHS if w >= d_c)
-    rows = (ids[:, None] * page_size + torch.arange(page_size, device=dev)).reshape(-1)
-    rows = rows[rows < C.shape[0]]
-    T = rows.numel()
-    n16 = (T + 15) // 16
-    lat = torch.zeros(n16 * 16, width, dtype=torch.float16, device=dev)
-    lat[:T, :d_c] = C.index_select(0, rows).to(torch.float16)
-    pools = LatentPools(c_fp16=lat.view(n16, 16, width))
-    table = torch.arange(n16, dtype=torch.int32, device=dev).expand(batch, n16).contiguous()
-    counts = torch.full((batch,), n16, dtype=torch.int32, device=dev)
-    valid = torch.full((batch,), T, dtype=torch.int32, device=dev)
-    q = torch.zeros(batch, q_len, width, dtype=torch.float16, device=dev)
-    q[..., :d_c] = q_absorb.to(torch.float16)
-    scale = 1.0 / math.sqrt(d_c)
-    v_main = width if width <= 512 else 512
-    ctx = mla_paged_decode(q, pools, table, counts, None, v_dim=v_main, sm_scale=scale, valid_tokens=valid,
-                           out_dtype=torch.float32)
-    if width > 512:
-        tail = mla_paged_decode(q, pools, table, counts, None, v_dim=width - 512, v_offset=512, sm_scale=scale,
-                                valid_tokens=valid, out_dtype=torch.float32)
-        ctx = torch.cat([ctx, tail], dim=-1)
-    return ctx[..., :d_c]
+    if q_absorb.stride(2) != 1:
+        q_absorb = q_absorb.contiguous()
+    if C.stride(1) != 1:
+        C = C.contiguous()
+    a = N.MlaRowsArgs()
+    a.batch, a.q_len, a.latent_dim, a.page_size, a.num_selected = batch, q_len, d_c, int(page_size), ids.numel()
+    a.num_rows = C.shape[0]
+    a.q, a.q_dtype, a.q_stride_b, a.q_stride_t = q_absorb.data_ptr(), _DT[q_absorb.dtype], q_absorb.stride(0), \
+        q_absorb.stride(1)
+    a.latents, a.latent_dtype, a.latent_stride = C.data_ptr(), _DT[C.dtype], C.stride(0)
+    a.page_ids, a.context, a.sm_scale = ids.data_ptr(), ctx.data_ptr(), 1.0 / math.sqrt(d_c)
+    N.mla_decode_rows(a, torch.cuda.current_stream(dev).cuda_stream)
+    return ctx
 
 
 def mla_decode_triton(q_absorb: torch.Tensor, C: torch.Tensor, W_VO_fused: torch.Tensor,

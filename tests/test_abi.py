@@ -40,7 +40,8 @@ def test_library_exports_every_declared_symbol():
                                           ("iak_transcode_args", "TranscodeArgs"),
                                           ("iak_prefetch_args", "PrefetchArgs"),
                                           ("iak_page_table_args", "PageTableArgs"),
-                                          ("iak_paged_decode_plan_info", "PlanInfo")])
+                                          ("iak_paged_decode_plan_info", "PlanInfo"),
+                                          ("iak_mla_rows_args", "MlaRowsArgs")])
 def test_ctypes_struct_matches_c_layout(cname, pyname):
     from intent_attention import _native as N
     S = getattr(N, pyname)
@@ -205,3 +206,22 @@ def test_split_plan_and_merge_form_without_gpu():
     c.merge_in_kernel, c.pages_per_split = 1, 64
     pc = N.plan_info(c)
     assert pc["splits"] == 1 and not pc["merge_in_kernel"] and pc["workspace_bytes"] == 0
+
+
+def test_mla_rows_validation_errors_without_gpu():
+    from intent_attention import _native as N
+    a = N.MlaRowsArgs()
+    a.batch, a.q_len, a.latent_dim, a.page_size, a.num_selected, a.num_rows = 1, 1, 1025, 16, 1, 64
+    with pytest.raises(ValueError, match="latent_dim 1025"):
+        N.mla_decode_rows(a, 0)
+    a.latent_dim, a.page_size = 576, 0
+    with pytest.raises(ValueError, match="page_size"):
+        N.mla_decode_rows(a, 0)
+    a.page_size, a.q_dtype = 16, 7
+    with pytest.raises(ValueError, match="dtype"):
+        N.mla_decode_rows(a, 0)
+    a.q_dtype = N.DTYPE_F32
+    with pytest.raises(ValueError, match="NULL"):
+        N.mla_decode_rows(a, 0)
+    a.batch = 0                                   # nothing to do: no launch, no error
+    N.mla_decode_rows(a, 0)
