@@ -956,7 +956,7 @@ def run_cfg1(args, cpu=None, cfg1_paths=None) -> None:
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="cfg3",
                     choices=sorted(CONFIGS) + ["cfg1"] + sorted(MLA_CONFIGS) + sorted(QUANT_CONFIGS)

@@ -266,10 +266,18 @@ class DecodePlan:
         # start at zero, and every run leaves them zero
         alloc = torch.zeros if args.merge_in_kernel else torch.empty
         self._ws = alloc(self.workspace_bytes, dtype=torch.uint8, device=device) if self.workspace_bytes else None
+        # the zero fill runs on the current stream; a run on another stream waits for it once
+        self._filled = None
+        if self._ws is not None and args.merge_in_kernel:
+            self._filled = torch.cuda.Event()
+            self._filled.record(torch.cuda.current_stream(device))
 
     def run(self, stream: Optional[int] = None, events: Optional[tuple] = None) -> None:
         """Launch on ``stream`` (default: torch's current stream). ``events``: an
         optional pair of torch.cuda.Event recorded around the split kernel alone."""
         s = torch.cuda.current_stream(self.device).cuda_stream if stream is None else stream
+        if self._filled is not None:
+            torch.cuda.ExternalStream(s, device=self.device).wait_event(self._filled)
+            self._filled = None
         ev = None if events is None else (events[0].cuda_event, events[1].cuda_event)
         N.paged_decode(self.args, self._ws.data_ptr() if self._ws is not None else 0, self.workspace_bytes, s, ev)

@@ -154,3 +154,19 @@ def test_graph_replays_equal_eager(dev):
         torch.cuda.synchronize()
         assert torch.equal(fused.out, want), i
         assert int(_counters(fused).abs().sum()) == 0
+
+
+def test_first_run_on_another_stream(dev):
+    """The plan zero-fills its counters on the current stream; a first run on
+    another stream waits for that fill."""
+    import torch
+    _say("in-kernel merge on a side stream")
+    fused, _, ref = _plans(dev, 141, 2, 8, 2, 128, 96, 70, 8)
+    side = torch.cuda.Stream(dev)
+    fused.run(stream=side.cuda_stream)
+    side.synchronize()
+    got = fused.out.clone()
+    assert np.abs(got.cpu().numpy() - ref).max() <= TOL_QUANT
+    fused.run()
+    torch.cuda.synchronize()
+    assert torch.equal(got, fused.out)
