@@ -261,14 +261,16 @@ class DecodePlan:
         self.device = device
         self.out = out
         self._keep = keep
-        self.workspace_bytes = N.workspace_bytes(args)
+        info = N.plan_info(args)
+        self.workspace_bytes = info["workspace_bytes"]
+        self.merge_in_kernel = info["merge_in_kernel"]
         # the in-kernel merge's arrival counters (at the end of the workspace)
         # start at zero, and every run leaves them zero
-        alloc = torch.zeros if args.merge_in_kernel else torch.empty
+        alloc = torch.zeros if self.merge_in_kernel else torch.empty
         self._ws = alloc(self.workspace_bytes, dtype=torch.uint8, device=device) if self.workspace_bytes else None
         # the zero fill runs on the current stream; a run on another stream waits for it once
         self._filled = None
-        if self._ws is not None and args.merge_in_kernel:
+        if self._ws is not None and self.merge_in_kernel:
             self._filled = torch.cuda.Event()
             self._filled.record(torch.cuda.current_stream(device))
 
