@@ -63,6 +63,8 @@ iak_status validate(const iak_paged_decode_args* a, Plan* plan) {
   if (!std::isfinite(a->sm_scale)) return fail(IAK_EINVAL, "sm_scale is not finite");
   if (a->pages_per_split < 0 || a->pages_per_split > 64)
     return fail(IAK_EINVAL, "pages_per_split %d outside [0, 64]", a->pages_per_split);
+  if (a->merge_in_kernel < 0 || a->merge_in_kernel > 2)
+    return fail(IAK_EINVAL, "merge_in_kernel %d is not 0, 1 or 2", a->merge_in_kernel);
   if (a->map_other_tags != 0 && a->map_other_tags != 1)
     return fail(IAK_EINVAL, "map_other_tags must be 0 or 1, got %d", a->map_other_tags);
   const long long rows = (long long)a->batch * a->num_kv_heads;

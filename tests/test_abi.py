@@ -202,6 +202,9 @@ def test_split_plan_and_merge_form_without_gpu():
     b.merge_in_kernel = 2                       # 32 rows x 8 workgroups: the merge kernel
     p4 = N.plan_info(b)
     assert not p4["merge_in_kernel"] and p4["splits"] == 32
+    b.merge_in_kernel = 3
+    with pytest.raises(ValueError, match="merge_in_kernel 3"):
+        N.plan_info(b)
     c = _decode_args(N, 1, 2, 4, 40)            # one split per row: no merge, no workspace
     c.merge_in_kernel, c.pages_per_split = 1, 64
     pc = N.plan_info(c)
