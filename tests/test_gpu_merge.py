@@ -170,3 +170,31 @@ def test_first_run_on_another_stream(dev):
     fused.run()
     torch.cuda.synchronize()
     assert torch.equal(got, fused.out)
+
+
+def test_long_rows(dev):
+    """Rows of 8,192 selected pages (131,072 tokens; entries may repeat a page):
+    128 splits per row, 32 workgroup partials per row in-kernel; both merge
+    forms against the oracle, with a peaked softmax (query scale 4)."""
+    import torch
+    from intent_attention import _native as N
+    from intent_attention.decode_core import make_plan
+    B, Hq, Hkv, D, NP, W = 1, 16, 2, 128, 2048, 8192
+    q, pools, table, counts, tags = random_case(151, B, Hq, Hkv, D, NP, W, {"FP16": .5, "INT8": .3, "FP8": .2},
+                                                q_scale=4.0)
+    counts[:] = [[W, W - 777]]
+    ref = Dm.paged_decode_oracle(q, pools, table, counts, tags, dtype=np.float32)
+    t = lambda x: torch.from_numpy(x).to(dev)  # noqa: E731
+    dp = to_device_pools(pools, dev)
+    for merge in (True, False):
+        _say("long rows", f"merge_in_kernel={merge}")
+        plan = make_plan(t(q), dp, t(table), t(counts), t(tags), out_dtype=torch.float32, merge_in_kernel=merge)
+        info = N.plan_info(plan.args)
+        assert info["splits"] >= 128 and info["merge_in_kernel"] == merge
+        plan.run()
+        torch.cuda.synchronize()
+        got = plan.out.cpu().numpy()
+        err = float(np.abs(got - ref).max())
+        rel = err / float(np.abs(ref).max())
+        _say(f"  splits {info['splits']}, max abs err {err:.2e}, relative {rel:.2e}")
+        assert err <= TOL_QUANT and rel <= 1e-2
