@@ -281,10 +281,15 @@ def build_workload(name: str, device: torch.device, seed: int = 1234, chunk_page
 # decode kernel's sources it was measured on (kernel_source_digest); a build whose
 # sources differ reports traffic null (stale) until the counters are run again.
 MEASURED_TRAFFIC = {
-    "cfg3": {"bytes": 2_105_201_844 + 4_456_448, "src": "fbd947793aa59b0a",
+    "cfg3": {"bytes": 2_105_121_910 + 4_456_448, "src": "b266f20edd69048d",
              "source": "profiles/paged_decode_cfg3_hbm_traffic.txt"},
-    "cfg4": {"bytes": 189_782_836 + 2_129_920, "src": "fbd947793aa59b0a",
+    "cfg4": {"bytes": 189_794_989 + 2_129_923, "src": "b266f20edd69048d",
              "source": "profiles/paged_decode_cfg4_kernel_stats.txt"},
+    # --page-descriptors: the same decodes reading 32-byte page descriptors
+    "cfg3-desc": {"bytes": 2_080_171_008 + 4_456_448, "src": "b266f20edd69048d",
+                  "source": "profiles/paged_decode_cfg3_hbm_traffic.txt"},
+    "cfg4-desc": {"bytes": 182_759_931 + 2_129_920, "src": "b266f20edd69048d",
+                  "source": "profiles/paged_decode_cfg4_kernel_stats.txt"},
 }
 KERNEL_SOURCES = ("paged_decode.hip", "iak_device.h", "iak_internal.h")
 
@@ -967,6 +972,9 @@ def main() -> None:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--merge", choices=("auto", "kernel", "in-kernel"), default="auto",
                     help="decode legs: where the split partials are merged (auto: the library's choice)")
+    ap.add_argument("--page-descriptors", action="store_true",
+                    help="decode legs: pack 32-byte page descriptors once (timed apart) and decode from them "
+                         "instead of the tag and scale arrays; `value` keeps the reference format's bytes")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="after the timed steps, run a plain device copy of MIB MiB (read + write "
                          "MIB MiB each): the reference point that scales rocprof FETCH_SIZE/WRITE_SIZE")
@@ -1037,6 +1045,19 @@ def run_decode(args, cpu=None) -> None:
                        pages_per_split=args.pages_per_split, merge_in_kernel=merge) for t in wl["tables"]]
     plan = plans[0]
     from intent_attention import _native as N
+    desc_info = None
+    if args.page_descriptors:
+        # one pack serves every plan (same pages, pools and tag map); timed on its own
+        desc = plan.pack_descriptors()
+        p0, p1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        cur = torch.cuda.current_stream(dev)
+        p0.record(cur)
+        plan.pack_descriptors(desc)
+        p1.record(cur)
+        torch.cuda.synchronize()
+        for p in plans[1:]:
+            p.use_descriptors(desc)
+        desc_info = {"pack_us": round(p0.elapsed_time(p1) * 1e3, 2), "bytes": desc.numel() * 4}
     split_plan = N.plan_info(plan.args)
     fused = split_plan["merge_in_kernel"]
     nsets = len(plans)
@@ -1078,6 +1099,7 @@ def run_decode(args, cpu=None) -> None:
     kernel_bytes = ab["total"] - (0 if fused else ab["qo"] // 2)
     kernel_gbps = kernel_bytes / (kernel_ms * 1e-3) / 1e9
     med = per[len(per) // 2]
+    traffic_key = args.config + ("-desc" if args.page_descriptors else "")
     res = {
         "metric": METRIC, "value": round(achieved, 1), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
@@ -1095,15 +1117,16 @@ def run_decode(args, cpu=None) -> None:
                    "pages_per_tag": ab["per_tag"], "pages_per_split": split_plan["pages_per_split"],
                    "splits_per_row": split_plan["splits"],
                    "merge": "in the decode kernel" if fused else "merge kernel",
+                   "page_descriptors": desc_info,
                    "gflop": round(flops(wl) / 1e9, 3)},
         "roofline": {"bound": "hbm", "achieved": round(kernel_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(kernel_gbps / HBM_PEAK_GBPS, 4),
-                     "traffic": measured_traffic(args.config)[0],
+                     "traffic": measured_traffic(traffic_key)[0],
                      "kernel": "paged_decode_kernel", "kernel_us": round(kernel_ms * 1e3, 2),
                      "kernel_bytes": kernel_bytes, "step_frac": round(achieved / HBM_PEAK_GBPS, 4)},
     }
-    if args.config in MEASURED_TRAFFIC:
-        res["roofline"]["traffic_source"] = measured_traffic(args.config)[1]
+    if traffic_key in MEASURED_TRAFFIC:
+        res["roofline"]["traffic_source"] = measured_traffic(traffic_key)[1]
     if args.calibrate_copy:
         n = args.calibrate_copy * (1 << 20)
         src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)

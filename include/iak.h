@@ -15,6 +15,9 @@
  *                                                                      triton_intent_quant_attention.py:342-457
  *   iak_paged_decode_workspace  (no counterpart: sizes the split-K partial buffer the caller allocates)
  *   iak_paged_decode_plan       (no counterpart: the split plan the library chooses for a call)
+ *   iak_pack_page_descriptors   (no counterpart: page_precision, page_tags and the per-precision scale
+ *                               arrays of fused_selected_quant_decode.py:408-464 packed into one
+ *                               32-byte descriptor per page)
  *   iak_paged_decode_timed,     (no counterpart: the same calls with HIP events around the split
  *   iak_mla_decode_timed         kernel, for timing it apart from the merge)
  *   iak_mla_decode              mla_decode_triton() / _mla_decode_cpu()    triton_mla_decode.py:110-186
@@ -47,7 +50,7 @@
 extern "C" {
 #endif
 
-#define IAK_ABI_VERSION 3
+#define IAK_ABI_VERSION 4
 
 /* Grid size from which merge_in_kernel = 2 merges inside the decode kernel. */
 #define IAK_MERGE_IN_KERNEL_MIN_WORKGROUPS 1024
@@ -123,6 +126,12 @@ enum { IAK_DTYPE_F16 = 0, IAK_DTYPE_F32 = 1, IAK_DTYPE_BF16 = 2 };
  *                partials into the output. The counters live at the end of the workspace:
  *                they must be zero before a workspace's first use, and every call leaves
  *                them zero (iak_paged_decode_noalloc ignores this field).
+ *   page_desc    NULL, or [num_pages] 32-byte page descriptors (32-byte aligned) written by
+ *                iak_pack_page_descriptors: the page's native tag and scales in one line, read
+ *                instead of page_tags, tag_map and the scale arrays (which may then be NULL;
+ *                a tag whose K/V pools are NULL contributes nothing). Word 0: native tag;
+ *                words 1-3: 0; words 4-7: FP8 / INT8 K and V scale (f32), INT4 K group scales
+ *                (4 x f16) then V, INT4_RESIDUAL K base, K residual, V base, V residual (f32).
  */
 typedef struct {
   int32_t batch, num_q_heads, num_kv_heads, head_dim, page_size, table_width;
@@ -153,6 +162,7 @@ typedef struct {
   int32_t map_other_tags;
   const int32_t* valid_tokens;
   int32_t merge_in_kernel;
+  const void* page_desc;
 } iak_paged_decode_args;
 
 /* ABI version of the loaded library (IAK_ABI_VERSION). */
@@ -177,6 +187,15 @@ typedef struct {
   size_t workspace_bytes;    /* = iak_paged_decode_workspace */
 } iak_paged_decode_plan_info;
 iak_status iak_paged_decode_plan(const iak_paged_decode_args* args, iak_paged_decode_plan_info* info);
+
+/* Page descriptors for `page_desc` (layout above) from the arguments' page_tags,
+ * tag_map, map_other_tags and scale arrays, for every one of num_pages pages:
+ * the native tag a decode with these arguments would use, and the scales it
+ * would load. `page_desc` (32-byte aligned, num_pages x 32 B) is written; the
+ * arguments' own page_desc field is ignored. No counterpart in the reference:
+ * a layout in which a page's metadata costs one cache line instead of up to
+ * three. Async on `stream`. */
+iak_status iak_pack_page_descriptors(const iak_paged_decode_args* args, void* page_desc, void* stream);
 
 /* Selected-page mixed-precision decode attention, split-K over pages with an
  * LSE merge. `workspace` must hold iak_paged_decode_workspace() bytes (may be

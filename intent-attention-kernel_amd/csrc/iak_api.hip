@@ -75,12 +75,22 @@ iak_status validate(const iak_paged_decode_args* a, Plan* plan) {
     if (!aligned16(a->q) || a->q_stride_b % qvec != 0 || a->q_stride_h % qvec != 0)
       return fail(IAK_EINVAL, "q must be 16-byte aligned with strides that are multiples of %d elements", qvec);
     if (!a->page_table || !a->page_counts) return fail(IAK_EINVAL, "page_table/page_counts is NULL");
-    if (a->num_pages > 0 && !a->page_tags) return fail(IAK_EINVAL, "page_tags is NULL");
+    if (a->num_pages > 0 && !a->page_tags && !a->page_desc) return fail(IAK_EINVAL, "page_tags is NULL");
     if (reinterpret_cast<uintptr_t>(a->valid_tokens) & 3u) return fail(IAK_EINVAL, "valid_tokens must be 4-byte aligned");
   }
-  // every native precision reachable through the tag map needs its pools
+  if (reinterpret_cast<uintptr_t>(a->page_desc) & 31u) return fail(IAK_EINVAL, "page_desc must be 32-byte aligned");
+  // every native precision reachable through the tag map needs its pools (with
+  // page descriptors: every native precision whose pools are given, scales
+  // coming from the descriptors)
   for (int t = 0; t < 8; ++t) {
-    const int n = a->tag_map[t];
+    int n = a->tag_map[t];
+    if (a->page_desc) {
+      n = t;
+      const bool given = (t == IAK_TAG_FP16 && a->k_fp16) || (t == IAK_TAG_FP8 && a->k_fp8) ||
+                         (t == IAK_TAG_INT8 && a->k_int8) || (t == IAK_TAG_INT4 && a->k_int4) ||
+                         (t == IAK_TAG_INT4_RESIDUAL && a->k_int4r);
+      if (!given) continue;
+    }
     const void *k = nullptr, *v = nullptr, *ks = nullptr, *vs = nullptr;
     int sd = IAK_DTYPE_F32;
     switch (n) {
@@ -91,6 +101,7 @@ iak_status validate(const iak_paged_decode_args* a, Plan* plan) {
       case IAK_TAG_INT4_RESIDUAL: k = a->k_int4r; v = a->v_int4r; ks = a->k_int4r_scale; vs = a->v_int4r_scale; break;
       default: continue;   // SKIP or unknown: contributes nothing
     }
+    if (a->page_desc) ks = vs = k;   // scales come from the descriptors
     if (!k || !v || !ks || !vs)
       return fail(IAK_EINVAL, "tag %d maps to %s but its K/V pool or scales are NULL", t, tag_name(n));
     if (!aligned16(k) || !aligned16(v))
@@ -322,6 +333,63 @@ iak_status iak_paged_decode_plan(const iak_paged_decode_args* args, iak_paged_de
   return IAK_OK;
 }
 
+// Tag translation, pools and scales of a decode (or of a descriptor pack).
+// With page descriptors the tag map passes every native precision whose pools
+// are given (the descriptor holds the native tag) and the scale arrays are
+// not read.
+static void fill_metadata(const iak_paged_decode_args* a, iak::KArgs& k) {
+  uint64_t map = 0;
+  for (int t = 0; t < 8; ++t) {
+    int n = a->page_desc ? t : a->tag_map[t];
+    if (n != IAK_TAG_FP16 && n != IAK_TAG_INT8 && n != IAK_TAG_FP8 && n != IAK_TAG_INT4 && n != IAK_TAG_INT4_RESIDUAL)
+      n = IAK_TAG_SKIP;
+    if (a->page_desc) {
+      const void* pool = n == IAK_TAG_FP16 ? a->k_fp16 : n == IAK_TAG_FP8 ? a->k_fp8 : n == IAK_TAG_INT8 ? a->k_int8
+                       : n == IAK_TAG_INT4 ? a->k_int4 : n == IAK_TAG_INT4_RESIDUAL ? a->k_int4r : nullptr;
+      if (!pool) n = IAK_TAG_SKIP;
+    }
+    map |= (uint64_t)n << (8 * t);
+  }
+  k.tagmap = map;
+  k.other_tag = (a->map_other_tags && !a->page_desc) ? (int)((map >> 56) & 0xFFu) : IAK_TAG_SKIP;
+  k.desc = static_cast<const uint32_t*>(a->page_desc);
+  k.neg_wrap = a->negative_ids != 0;
+  k.valid = a->valid_tokens;
+  k.k_fp16 = a->k_fp16; k.v_fp16 = a->v_fp16; k.k_fp8 = a->k_fp8; k.v_fp8 = a->v_fp8;
+  k.k_int8 = a->k_int8; k.v_int8 = a->v_int8; k.k_int4 = a->k_int4; k.v_int4 = a->v_int4;
+  k.k_int4r = a->k_int4r; k.v_int4r = a->v_int4r;
+  k.k_fp8_scale = a->k_fp8_scale; k.v_fp8_scale = a->v_fp8_scale; k.fp8_sd = a->fp8_scale_dtype;
+  k.k_int8_scale = a->k_int8_scale; k.v_int8_scale = a->v_int8_scale; k.int8_sd = a->int8_scale_dtype;
+  k.k_int4_scale = a->k_int4_scale; k.v_int4_scale = a->v_int4_scale; k.int4_sd = a->int4_scale_dtype;
+  k.int4_group = a->int4_group > 0 ? a->int4_group : a->head_dim;
+  k.k_int4r_scale = a->k_int4r_scale; k.v_int4r_scale = a->v_int4r_scale;
+}
+
+iak_status iak_pack_page_descriptors(const iak_paged_decode_args* args, void* page_desc, void* stream) {
+  if (!args) return fail(IAK_EINVAL, "args is NULL");
+  // the descriptors come from page_tags, the tag map and the scales: validated
+  // as for a decode without descriptors and without rows
+  iak_paged_decode_args a = *args;
+  a.page_desc = nullptr;
+  a.batch = 0;
+  Plan plan;
+  const iak_status st = validate(&a, &plan);
+  if (st != IAK_OK) return st;
+  if (a.num_pages == 0) return IAK_OK;
+  if (!a.page_tags) return fail(IAK_EINVAL, "page_tags is NULL");
+  if (!page_desc || (reinterpret_cast<uintptr_t>(page_desc) & 31u))
+    return fail(IAK_EINVAL, "page_desc must be non-NULL and 32-byte aligned");
+  iak::KArgs k;
+  std::memset(&k, 0, sizeof(k));
+  k.D = a.head_dim;
+  k.NP = a.num_pages;
+  k.tags = a.page_tags;
+  fill_metadata(&a, k);
+  const hipError_t e = iak::launch_pack_descriptors(k, page_desc, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(IAK_EHIP, "kernel launch failed: %s", hipGetErrorString(e));
+  return IAK_OK;
+}
+
 static iak_status paged_decode_impl(const iak_paged_decode_args* a, void* workspace, size_t workspace_bytes,
                                     void* stream, void* ev_begin, void* ev_end) {
   Plan plan;
@@ -343,25 +411,7 @@ static iak_status paged_decode_impl(const iak_paged_decode_args* a, void* worksp
   k.qsb = a->q_stride_b; k.qsh = a->q_stride_h;
   k.out = a->out; k.out_dtype = a->out_dtype; k.osb = a->out_stride_b; k.osh = a->out_stride_h;
   k.table = a->page_table; k.counts = a->page_counts; k.tags = a->page_tags;
-  uint64_t map = 0;
-  for (int t = 0; t < 8; ++t) {
-    int n = a->tag_map[t];
-    if (n != IAK_TAG_FP16 && n != IAK_TAG_INT8 && n != IAK_TAG_FP8 && n != IAK_TAG_INT4 && n != IAK_TAG_INT4_RESIDUAL)
-      n = IAK_TAG_SKIP;
-    map |= (uint64_t)n << (8 * t);
-  }
-  k.tagmap = map;
-  k.other_tag = a->map_other_tags ? (int)((map >> 56) & 0xFFu) : IAK_TAG_SKIP;
-  k.neg_wrap = a->negative_ids != 0;
-  k.valid = a->valid_tokens;
-  k.k_fp16 = a->k_fp16; k.v_fp16 = a->v_fp16; k.k_fp8 = a->k_fp8; k.v_fp8 = a->v_fp8;
-  k.k_int8 = a->k_int8; k.v_int8 = a->v_int8; k.k_int4 = a->k_int4; k.v_int4 = a->v_int4;
-  k.k_int4r = a->k_int4r; k.v_int4r = a->v_int4r;
-  k.k_fp8_scale = a->k_fp8_scale; k.v_fp8_scale = a->v_fp8_scale; k.fp8_sd = a->fp8_scale_dtype;
-  k.k_int8_scale = a->k_int8_scale; k.v_int8_scale = a->v_int8_scale; k.int8_sd = a->int8_scale_dtype;
-  k.k_int4_scale = a->k_int4_scale; k.v_int4_scale = a->v_int4_scale; k.int4_sd = a->int4_scale_dtype;
-  k.int4_group = a->int4_group > 0 ? a->int4_group : a->head_dim;
-  k.k_int4r_scale = a->k_int4r_scale; k.v_int4r_scale = a->v_int4r_scale;
+  fill_metadata(a, k);
   k.score_mult = a->sm_scale * 1.4426950408889634f;
   if (plan.total > 0) {
     char* ws = static_cast<char*>(workspace);

@@ -64,7 +64,13 @@ struct KArgs {
   // [B, Hkv, splits / 4, G] and [.., D]; counters [B * Hkv] arrivals per row
   int fused;
   int32_t* counters;
+
+  // page descriptors (iak_paged_decode_args.page_desc): [NP] x 32 B as two u4 (tag word, scale slots)
+  const uint32_t* desc;
 };
+
+// page descriptors from page_tags, the tag map and the scale arrays of `k`
+hipError_t launch_pack_descriptors(const KArgs& k, void* desc, hipStream_t stream);
 
 // ev_begin / ev_end (may be null) are recorded on `stream` around the split
 // kernel alone, so callers can time it apart from the merge

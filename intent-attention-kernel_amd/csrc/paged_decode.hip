@@ -473,11 +473,17 @@ __device__ __forceinline__ uint32_t scale_bits_f16(const void* p, int64_t idx, i
 //   FP8 / INT8      s0 = K scale, s1 = V scale (f32 bits)
 //   INT4_RESIDUAL   s0, s1 = K base / residual scale, s2, s3 = V base / residual (f32 bits)
 //   INT4            s0, s1 = K group scales as f16 pairs (g0,g1), (g2,g3); s2, s3 = V
+// With page descriptors the four slots are words 4-7 of the page's descriptor.
 template <int D>
 __device__ __forceinline__ void load_page_scales(const KArgs& a, int pid, int tag, uint32_t (&slot)[4]) {
   slot[0] = slot[1] = slot[2] = slot[3] = 0u;
   if (pid < 0) return;
   const int64_t p = pid;
+  if (a.desc) {
+    const u4 x = *reinterpret_cast<const u4*>(a.desc + 8 * p + 4);
+    slot[0] = x[0]; slot[1] = x[1]; slot[2] = x[2]; slot[3] = x[3];
+    return;
+  }
   if (tag == IAK_TAG_FP8) {
     slot[0] = scale_bits_f32(a.k_fp8_scale, p, a.fp8_sd);
     slot[1] = scale_bits_f32(a.v_fp8_scale, p, a.fp8_sd);
@@ -775,7 +781,9 @@ __device__ __forceinline__ void load_tag(const KArgs& a, int raw, int cnt, int b
     int p = raw;
     if (a.neg_wrap && p < 0 && (int64_t)p >= -a.NP) p = (int)((int64_t)p + a.NP);
     if (p >= 0 && (int64_t)p < a.NP) {
-      const int t = a.tags[p];
+      // the caller's tag, or the native tag of the page's descriptor (the tag
+      // map then passes the precisions whose pools are present)
+      const int t = a.desc ? (int)a.desc[8 * (int64_t)p] : a.tags[p];
       tag = (t >= 0 && t < 8) ? (int)((a.tagmap >> (8 * t)) & 0xFFu) : a.other_tag;
       pid = p;
     }
@@ -910,6 +918,33 @@ void paged_decode_kernel(const KArgs a) {
     return;
   }
   write_result<D, QT>(a, sp, w, c, g);
+}
+
+// Page descriptors: one thread per page writes the native tag a decode would
+// use for it (word 0) and the scale slots it would load (words 4-7).
+template <int D>
+__global__ __launch_bounds__(256) void pack_descriptors_kernel(const KArgs a, uint32_t* desc) {
+  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (p >= a.NP) return;
+  const int t = a.tags[p];
+  const int tag = (t >= 0 && t < 8) ? (int)((a.tagmap >> (8 * t)) & 0xFFu) : a.other_tag;
+  uint32_t slot[4];
+  load_page_scales<D>(a, (int)p, tag, slot);
+  u4* out = reinterpret_cast<u4*>(desc + 8 * p);
+  out[0] = u4{(uint32_t)tag, 0u, 0u, 0u};
+  out[1] = u4{slot[0], slot[1], slot[2], slot[3]};
+}
+
+hipError_t launch_pack_descriptors(const KArgs& k, void* desc, hipStream_t stream) {
+  const int64_t blocks = (k.NP + 255) / 256;
+  if (blocks == 0) return hipSuccess;
+  if (k.D == 128)
+    hipLaunchKernelGGL(pack_descriptors_kernel<128>, dim3((unsigned)blocks), dim3(256), 0, stream, k,
+                       static_cast<uint32_t*>(desc));
+  else
+    hipLaunchKernelGGL(pack_descriptors_kernel<64>, dim3((unsigned)blocks), dim3(256), 0, stream, k,
+                       static_cast<uint32_t*>(desc));
+  return hipGetLastError();
 }
 
 template <int D, int QT>

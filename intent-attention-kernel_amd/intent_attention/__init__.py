@@ -38,7 +38,7 @@ from .intent_quant_decode import (
     make_page_tables_from_selected_pages,
     make_precision_tensor,
 )
-from .decode_core import PagePools, paged_decode
+from .decode_core import PagePools, make_plan, pack_page_descriptors, paged_decode
 from .reference import dense_attention
 from .intent_quant_attention import intent_quant_attention_reference
 from .mla import MLABlockTable, MLAConfig, absorb_weights, mla_sparse_decode_reference, mla_triton_decode
@@ -67,7 +67,7 @@ __all__ = [
     "fake_quantize_tensor",
     "IntentQuantKernelConfig", "TritonKVPrecision", "fake_int8_pages_from_fp16",
     "intent_quant_decode_attention_triton", "make_page_tables_from_selected_pages", "make_precision_tensor",
-    "PagePools", "paged_decode",
+    "PagePools", "make_plan", "pack_page_descriptors", "paged_decode",
     "dense_attention", "intent_quant_attention_reference",
     "MLABlockTable", "MLAConfig", "absorb_weights", "mla_sparse_decode_reference", "mla_triton_decode",
     "LatentPools", "mla_paged_decode", "mla_decode_triton",

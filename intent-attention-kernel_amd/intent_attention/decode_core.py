@@ -150,9 +150,15 @@ def make_plan(q: torch.Tensor, pools: PagePools, page_table: torch.Tensor, page_
               out: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None,
               pages_per_split: int = 0, map_other_tags: bool = False,
               valid_tokens: Optional[torch.Tensor] = None,
-              merge_in_kernel: Optional[bool] = None) -> "DecodePlan":
+              merge_in_kernel: Optional[bool] = None,
+              page_descriptors: Optional[torch.Tensor] = None) -> "DecodePlan":
     """Validate the arguments of ``paged_decode`` once; the returned plan
-    re-launches the decode on the same tensors with ``run()``."""
+    re-launches the decode on the same tensors with ``run()``.
+
+    ``page_descriptors`` (optional): [num_pages, 8] int32 descriptors from
+    ``DecodePlan.pack_descriptors`` (or ``pack_page_descriptors``), read in
+    place of ``page_tags``, ``tag_map`` and the scale tensors: one 32-byte
+    line of metadata per selected page."""
     if q.dim() != 3:
         raise ValueError(f"q must have shape [B, H, D], got {tuple(q.shape)}")
     B, Hq, D = q.shape
@@ -248,7 +254,34 @@ def make_plan(q: torch.Tensor, pools: PagePools, page_table: torch.Tensor, page_
     a.valid_tokens = _ptr(valid_tokens)
     a.merge_in_kernel = MERGE_IN_KERNEL_AUTO if merge_in_kernel is None else (1 if merge_in_kernel else 0)
 
-    return DecodePlan(a, dev, out, keep=(q, page_table, page_counts, page_tags, valid_tokens, pools))
+    plan = DecodePlan(a, dev, out, keep=(q, page_table, page_counts, page_tags, valid_tokens, pools))
+    if page_descriptors is not None:
+        plan.use_descriptors(page_descriptors)
+    return plan
+
+
+def _check_descriptors(desc: torch.Tensor, NP: int, device: torch.device) -> None:
+    if desc.dtype != torch.int32 or tuple(desc.shape) != (NP, N.PAGE_DESC_BYTES // 4):
+        raise ValueError(f"page descriptors must be int32 [{NP}, {N.PAGE_DESC_BYTES // 4}], "
+                         f"got {desc.dtype} {tuple(desc.shape)}")
+    if desc.device != device or not desc.is_contiguous() or desc.data_ptr() % 32:
+        raise ValueError(f"page descriptors must be a contiguous, 32-byte aligned tensor on {device}")
+
+
+def pack_page_descriptors(q: torch.Tensor, pools: PagePools, page_tags: torch.Tensor, *,
+                          tag_map: Optional[Sequence[int]] = None, map_other_tags: bool = False,
+                          out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The page descriptors of ``page_tags`` and ``pools`` (tags translated
+    through ``tag_map`` as ``paged_decode`` would), as [num_pages, 8] int32 on
+    the GPU, written on the current stream. ``q`` gives head_dim and device
+    ([B, Hq, D]; its values are not read)."""
+    D = int(q.shape[-1])
+    # a one-entry table with no selected pages: the plan carries the tags and pools
+    table = torch.zeros((1, 1, 1), dtype=torch.int32, device=q.device)
+    counts = torch.zeros((1, 1), dtype=torch.int32, device=q.device)
+    plan = make_plan(q[:1, :1], pools, table, counts, page_tags, tag_map=tag_map, map_other_tags=map_other_tags)
+    assert plan.args.head_dim == D
+    return plan.pack_descriptors(out)
 
 
 class DecodePlan:
@@ -273,6 +306,30 @@ class DecodePlan:
         if self._ws is not None and self.merge_in_kernel:
             self._filled = torch.cuda.Event()
             self._filled.record(torch.cuda.current_stream(device))
+        self._desc: Optional[torch.Tensor] = None
+
+    def pack_descriptors(self, out: Optional[torch.Tensor] = None, stream: Optional[int] = None) -> torch.Tensor:
+        """Pack this plan's page tags (through its tag map), and the scales each
+        page's precision uses, into 32-byte page descriptors ([num_pages, 8]
+        int32; ``out`` if given) on ``stream``, and make later runs read them
+        instead. The descriptors are a snapshot: pack again after the tags or
+        scales change."""
+        NP = int(self.args.num_pages)
+        if out is None:
+            out = torch.empty((NP, N.PAGE_DESC_BYTES // 4), dtype=torch.int32, device=self.device)
+        _check_descriptors(out, NP, self.device)
+        s = torch.cuda.current_stream(self.device).cuda_stream if stream is None else stream
+        N.pack_page_descriptors(self.args, out.data_ptr(), s)
+        self.use_descriptors(out)
+        return out
+
+    def use_descriptors(self, desc: Optional[torch.Tensor]) -> None:
+        """Read ``desc`` (packed for the same pages and pools) in place of the
+        tags, tag map and scales; None goes back to them."""
+        if desc is not None:
+            _check_descriptors(desc, int(self.args.num_pages), self.device)
+        self._desc = desc
+        self.args.page_desc = desc.data_ptr() if desc is not None else None
 
     def run(self, stream: Optional[int] = None, events: Optional[tuple] = None) -> None:
         """Launch on ``stream`` (default: torch's current stream). ``events``: an

@@ -228,3 +228,38 @@ def test_mla_rows_validation_errors_without_gpu():
         N.mla_decode_rows(a, 0)
     a.batch = 0                                   # nothing to do: no launch, no error
     N.mla_decode_rows(a, 0)
+
+
+def test_page_descriptor_validation_without_gpu():
+    """page_desc: 32-byte aligned; with it page_tags and the scale arrays may be
+    NULL, and only precisions whose K pool is given need their V pool. The pack
+    entry point rejects a NULL or misaligned destination and NULL page_tags
+    before any launch."""
+    from intent_attention import _native as N
+    a = _decode_args(N, 2, 2, 4, 100)
+    a.num_pages = 64
+    a.page_desc = 0x100010                      # 16-byte aligned only
+    with pytest.raises(ValueError, match="32-byte aligned"):
+        N.workspace_bytes(a)
+    a.page_desc = 0x100020
+    a.page_tags = None
+    assert N.workspace_bytes(a) > 0             # tags come from the descriptors
+    a.k_fp8 = 0x200000                          # FP8 K pool without its V pool
+    with pytest.raises(ValueError, match="FP8"):
+        N.workspace_bytes(a)
+    a.v_fp8 = 0x300000                          # scales not needed with descriptors
+    assert N.workspace_bytes(a) > 0
+    with pytest.raises(ValueError, match="page_tags"):
+        N.pack_page_descriptors(a, 0x400000, 0)
+    a.page_tags = 16
+    with pytest.raises(ValueError, match="page_desc"):
+        N.pack_page_descriptors(a, 0, 0)
+    with pytest.raises(ValueError, match="page_desc"):
+        N.pack_page_descriptors(a, 0x400010, 0)
+    # packing reads the tag map and scales: FP8 reachable without its scales
+    a.tag_map[3] = N.TAG_FP8
+    with pytest.raises(ValueError, match="FP8"):
+        N.pack_page_descriptors(a, 0x400000, 0)
+    a.num_pages = 0                             # nothing to pack: no launch, no error
+    a.tag_map[3] = N.TAG_SKIP
+    N.pack_page_descriptors(a, 0, 0)
