@@ -281,15 +281,20 @@ def build_workload(name: str, device: torch.device, seed: int = 1234, chunk_page
 # decode kernel's sources it was measured on (kernel_source_digest); a build whose
 # sources differ reports traffic null (stale) until the counters are run again.
 MEASURED_TRAFFIC = {
-    "cfg3": {"bytes": 2_105_121_910 + 4_456_448, "src": "b266f20edd69048d",
+    "cfg3": {"bytes": 2_105_134_111 + 4_456_448, "src": "b03928340f2a8b0e",
              "source": "profiles/paged_decode_cfg3_hbm_traffic.txt"},
-    "cfg4": {"bytes": 189_794_989 + 2_129_923, "src": "b266f20edd69048d",
+    "cfg4": {"bytes": 189_785_413 + 2_129_920, "src": "b03928340f2a8b0e",
              "source": "profiles/paged_decode_cfg4_kernel_stats.txt"},
-    # --page-descriptors: the same decodes reading 32-byte page descriptors
-    "cfg3-desc": {"bytes": 2_080_171_008 + 4_456_448, "src": "b266f20edd69048d",
+    # the same decodes reading 32-byte page descriptors (--page-descriptors) or
+    # 32-byte entry records (--entry-records)
+    "cfg3-desc": {"bytes": 2_080_233_492 + 4_456_448, "src": "b03928340f2a8b0e",
                   "source": "profiles/paged_decode_cfg3_hbm_traffic.txt"},
-    "cfg4-desc": {"bytes": 182_759_931 + 2_129_920, "src": "b266f20edd69048d",
+    "cfg4-desc": {"bytes": 182_748_185 + 2_129_920, "src": "b03928340f2a8b0e",
                   "source": "profiles/paged_decode_cfg4_kernel_stats.txt"},
+    "cfg3-records": {"bytes": 2_005_509_914 + 4_456_448, "src": "b03928340f2a8b0e",
+                     "source": "profiles/paged_decode_cfg3_hbm_traffic.txt"},
+    "cfg4-records": {"bytes": 178_927_876 + 2_129_920, "src": "b03928340f2a8b0e",
+                     "source": "profiles/paged_decode_cfg4_kernel_stats.txt"},
 }
 KERNEL_SOURCES = ("paged_decode.hip", "iak_device.h", "iak_internal.h")
 
@@ -975,6 +980,10 @@ def main() -> None:
     ap.add_argument("--page-descriptors", action="store_true",
                     help="decode legs: pack 32-byte page descriptors once (timed apart) and decode from them "
                          "instead of the tag and scale arrays; `value` keeps the reference format's bytes")
+    ap.add_argument("--entry-records", action="store_true",
+                    help="decode legs: pack 32-byte entry records once per page table (timed apart) and decode "
+                         "from them instead of the table, tag and scale arrays; `value` keeps the reference "
+                         "format's bytes")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="after the timed steps, run a plain device copy of MIB MiB (read + write "
                          "MIB MiB each): the reference point that scales rocprof FETCH_SIZE/WRITE_SIZE")
@@ -1058,6 +1067,21 @@ def run_decode(args, cpu=None) -> None:
         for p in plans[1:]:
             p.use_descriptors(desc)
         desc_info = {"pack_us": round(p0.elapsed_time(p1) * 1e3, 2), "bytes": desc.numel() * 4}
+    rec_info = None
+    if args.entry_records:
+        # one pack per page table (a routing decision), each timed on its own
+        cur = torch.cuda.current_stream(dev)
+        times, nbytes = [], 0
+        for p in plans:
+            recs = p.pack_records()
+            p0, p1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            p0.record(cur)
+            p.pack_records(recs)
+            p1.record(cur)
+            torch.cuda.synchronize()
+            times.append(p0.elapsed_time(p1) * 1e3)
+            nbytes = recs.numel() * 4
+        rec_info = {"pack_us_per_table": round(sum(times) / len(times), 2), "bytes_per_table": nbytes}
     split_plan = N.plan_info(plan.args)
     fused = split_plan["merge_in_kernel"]
     nsets = len(plans)
@@ -1095,11 +1119,20 @@ def run_decode(args, cpu=None) -> None:
     ab["per_tag"] = {k: int(round(sum(x["per_tag"][k] for x in abs_) / nsets)) for k in abs_[0]["per_tag"]}
     achieved = ab["total"] / (ms * 1e-3) / 1e9
     # the split kernel moves every algorithmic byte but the output, which the
-    # merge kernel writes (unless the decode kernel merges itself)
-    kernel_bytes = ab["total"] - (0 if fused else ab["qo"] // 2)
+    # merge kernel writes (unless the decode kernel merges itself); with page
+    # descriptors or entry records its metadata bytes are theirs: 32 B per
+    # selected page (+ its 4 B table entry), or 32 B per table entry
+    kernel_alg, kernel_fmt = ab["total"], "reference tensors"
+    if rec_info is not None:
+        kernel_alg = ab["codes"] + rec_info["bytes_per_table"] + wl["counts"].numel() * 4 + ab["qo"]
+        kernel_fmt = "entry records"
+    elif desc_info is not None:
+        kernel_alg = ab["codes"] + ab["pages"] * (32 + 4) + wl["counts"].numel() * 4 + ab["qo"]
+        kernel_fmt = "page descriptors"
+    kernel_bytes = kernel_alg - (0 if fused else ab["qo"] // 2)
     kernel_gbps = kernel_bytes / (kernel_ms * 1e-3) / 1e9
     med = per[len(per) // 2]
-    traffic_key = args.config + ("-desc" if args.page_descriptors else "")
+    traffic_key = args.config + ("-records" if args.entry_records else "-desc" if args.page_descriptors else "")
     res = {
         "metric": METRIC, "value": round(achieved, 1), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
@@ -1118,12 +1151,14 @@ def run_decode(args, cpu=None) -> None:
                    "splits_per_row": split_plan["splits"],
                    "merge": "in the decode kernel" if fused else "merge kernel",
                    "page_descriptors": desc_info,
+                   "entry_records": rec_info,
                    "gflop": round(flops(wl) / 1e9, 3)},
         "roofline": {"bound": "hbm", "achieved": round(kernel_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(kernel_gbps / HBM_PEAK_GBPS, 4),
                      "traffic": measured_traffic(traffic_key)[0],
                      "kernel": "paged_decode_kernel", "kernel_us": round(kernel_ms * 1e3, 2),
-                     "kernel_bytes": kernel_bytes, "step_frac": round(achieved / HBM_PEAK_GBPS, 4)},
+                     "kernel_bytes": kernel_bytes, "kernel_metadata_format": kernel_fmt,
+                     "step_frac": round(achieved / HBM_PEAK_GBPS, 4)},
     }
     if traffic_key in MEASURED_TRAFFIC:
         res["roofline"]["traffic_source"] = measured_traffic(traffic_key)[1]

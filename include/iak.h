@@ -18,6 +18,9 @@
  *   iak_pack_page_descriptors   (no counterpart: page_precision, page_tags and the per-precision scale
  *                               arrays of fused_selected_quant_decode.py:408-464 packed into one
  *                               32-byte descriptor per page)
+ *   iak_pack_entry_records      (no counterpart: the page table's entries with their page's native
+ *                               tag and scales (fused_selected_quant_decode.py:344-400 reads them
+ *                               entry by entry) packed into one 32-byte record per entry)
  *   iak_paged_decode_timed,     (no counterpart: the same calls with HIP events around the split
  *   iak_mla_decode_timed         kernel, for timing it apart from the merge)
  *   iak_mla_decode              mla_decode_triton() / _mla_decode_cpu()    triton_mla_decode.py:110-186
@@ -50,7 +53,7 @@
 extern "C" {
 #endif
 
-#define IAK_ABI_VERSION 4
+#define IAK_ABI_VERSION 5
 
 /* Grid size from which merge_in_kernel = 2 merges inside the decode kernel. */
 #define IAK_MERGE_IN_KERNEL_MIN_WORKGROUPS 1024
@@ -132,6 +135,16 @@ enum { IAK_DTYPE_F16 = 0, IAK_DTYPE_F32 = 1, IAK_DTYPE_BF16 = 2 };
  *                a tag whose K/V pools are NULL contributes nothing). Word 0: native tag;
  *                words 1-3: 0; words 4-7: FP8 / INT8 K and V scale (f32), INT4 K group scales
  *                (4 x f16) then V, INT4_RESIDUAL K base, K residual, V base, V residual (f32).
+ *                INT4 scales are per quarter of head_dim: quarter q holds the scale of group
+ *                q * head_dim / 4 / int4_group.
+ *   entry_records NULL, or [batch, num_kv_heads, table_width] 32-byte records (32-byte
+ *                aligned) written by iak_pack_entry_records: per table entry the page's native
+ *                tag (word 0), its page id (word 1; -1 when the table's id is out of range,
+ *                negative ids already wrapped when negative_ids was set at packing), words
+ *                2-3: 0, words 4-7 the scales as in page_desc. Read instead of page_table,
+ *                page_tags, tag_map, the scale arrays and page_desc (all may then be NULL;
+ *                negative_ids is ignored; a tag whose K/V pools are NULL contributes
+ *                nothing); page_counts and valid_tokens still apply.
  */
 typedef struct {
   int32_t batch, num_q_heads, num_kv_heads, head_dim, page_size, table_width;
@@ -163,6 +176,7 @@ typedef struct {
   const int32_t* valid_tokens;
   int32_t merge_in_kernel;
   const void* page_desc;
+  const void* entry_records;
 } iak_paged_decode_args;
 
 /* ABI version of the loaded library (IAK_ABI_VERSION). */
@@ -196,6 +210,16 @@ iak_status iak_paged_decode_plan(const iak_paged_decode_args* args, iak_paged_de
  * a layout in which a page's metadata costs one cache line instead of up to
  * three. Async on `stream`. */
 iak_status iak_pack_page_descriptors(const iak_paged_decode_args* args, void* page_desc, void* stream);
+
+/* Entry records for `entry_records` (layout above) from the arguments' page_table,
+ * negative_ids, page_tags, tag_map, map_other_tags and scale arrays, for all
+ * batch x num_kv_heads x table_width entries: the page id, native tag and scales a
+ * decode with these arguments would use for each entry. `records` (32-byte aligned,
+ * that many x 32 B) is written; the arguments' page_desc and entry_records fields
+ * are ignored. No counterpart in the reference: run once per routing decision
+ * (after iak_build_page_tables), it turns each split's metadata into one
+ * contiguous stream. Async on `stream`. */
+iak_status iak_pack_entry_records(const iak_paged_decode_args* args, void* records, void* stream);
 
 /* Selected-page mixed-precision decode attention, split-K over pages with an
  * LSE merge. `workspace` must hold iak_paged_decode_workspace() bytes (may be

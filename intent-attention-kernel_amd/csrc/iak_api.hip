@@ -74,17 +74,22 @@ iak_status validate(const iak_paged_decode_args* a, Plan* plan) {
     const int qvec = a->q_dtype == IAK_DTYPE_F32 ? 4 : 8;
     if (!aligned16(a->q) || a->q_stride_b % qvec != 0 || a->q_stride_h % qvec != 0)
       return fail(IAK_EINVAL, "q must be 16-byte aligned with strides that are multiples of %d elements", qvec);
-    if (!a->page_table || !a->page_counts) return fail(IAK_EINVAL, "page_table/page_counts is NULL");
-    if (a->num_pages > 0 && !a->page_tags && !a->page_desc) return fail(IAK_EINVAL, "page_tags is NULL");
+    if ((!a->page_table && !a->entry_records) || !a->page_counts)
+      return fail(IAK_EINVAL, "page_table/page_counts is NULL");
+    if (a->num_pages > 0 && !a->page_tags && !a->page_desc && !a->entry_records)
+      return fail(IAK_EINVAL, "page_tags is NULL");
     if (reinterpret_cast<uintptr_t>(a->valid_tokens) & 3u) return fail(IAK_EINVAL, "valid_tokens must be 4-byte aligned");
   }
   if (reinterpret_cast<uintptr_t>(a->page_desc) & 31u) return fail(IAK_EINVAL, "page_desc must be 32-byte aligned");
+  if (reinterpret_cast<uintptr_t>(a->entry_records) & 31u)
+    return fail(IAK_EINVAL, "entry_records must be 32-byte aligned");
   // every native precision reachable through the tag map needs its pools (with
-  // page descriptors: every native precision whose pools are given, scales
-  // coming from the descriptors)
+  // page descriptors or entry records: every native precision whose pools are
+  // given, scales coming from the descriptors or records)
+  const bool native = a->page_desc || a->entry_records;
   for (int t = 0; t < 8; ++t) {
     int n = a->tag_map[t];
-    if (a->page_desc) {
+    if (native) {
       n = t;
       const bool given = (t == IAK_TAG_FP16 && a->k_fp16) || (t == IAK_TAG_FP8 && a->k_fp8) ||
                          (t == IAK_TAG_INT8 && a->k_int8) || (t == IAK_TAG_INT4 && a->k_int4) ||
@@ -101,7 +106,7 @@ iak_status validate(const iak_paged_decode_args* a, Plan* plan) {
       case IAK_TAG_INT4_RESIDUAL: k = a->k_int4r; v = a->v_int4r; ks = a->k_int4r_scale; vs = a->v_int4r_scale; break;
       default: continue;   // SKIP or unknown: contributes nothing
     }
-    if (a->page_desc) ks = vs = k;   // scales come from the descriptors
+    if (native) ks = vs = k;   // scales come from the descriptors or records
     if (!k || !v || !ks || !vs)
       return fail(IAK_EINVAL, "tag %d maps to %s but its K/V pool or scales are NULL", t, tag_name(n));
     if (!aligned16(k) || !aligned16(v))
@@ -333,17 +338,18 @@ iak_status iak_paged_decode_plan(const iak_paged_decode_args* args, iak_paged_de
   return IAK_OK;
 }
 
-// Tag translation, pools and scales of a decode (or of a descriptor pack).
-// With page descriptors the tag map passes every native precision whose pools
-// are given (the descriptor holds the native tag) and the scale arrays are
-// not read.
+// Tag translation, pools and scales of a decode (or of a pack). With page
+// descriptors or entry records the tag map passes every native precision whose
+// pools are given (they hold the native tag) and the scale arrays are not read;
+// records also hold resolved page ids (negative_ids is not applied again).
 static void fill_metadata(const iak_paged_decode_args* a, iak::KArgs& k) {
+  const bool native = a->page_desc || a->entry_records;
   uint64_t map = 0;
   for (int t = 0; t < 8; ++t) {
-    int n = a->page_desc ? t : a->tag_map[t];
+    int n = native ? t : a->tag_map[t];
     if (n != IAK_TAG_FP16 && n != IAK_TAG_INT8 && n != IAK_TAG_FP8 && n != IAK_TAG_INT4 && n != IAK_TAG_INT4_RESIDUAL)
       n = IAK_TAG_SKIP;
-    if (a->page_desc) {
+    if (native) {
       const void* pool = n == IAK_TAG_FP16 ? a->k_fp16 : n == IAK_TAG_FP8 ? a->k_fp8 : n == IAK_TAG_INT8 ? a->k_int8
                        : n == IAK_TAG_INT4 ? a->k_int4 : n == IAK_TAG_INT4_RESIDUAL ? a->k_int4r : nullptr;
       if (!pool) n = IAK_TAG_SKIP;
@@ -351,9 +357,10 @@ static void fill_metadata(const iak_paged_decode_args* a, iak::KArgs& k) {
     map |= (uint64_t)n << (8 * t);
   }
   k.tagmap = map;
-  k.other_tag = (a->map_other_tags && !a->page_desc) ? (int)((map >> 56) & 0xFFu) : IAK_TAG_SKIP;
-  k.desc = static_cast<const uint32_t*>(a->page_desc);
-  k.neg_wrap = a->negative_ids != 0;
+  k.other_tag = (a->map_other_tags && !native) ? (int)((map >> 56) & 0xFFu) : IAK_TAG_SKIP;
+  k.desc = a->entry_records ? nullptr : static_cast<const uint32_t*>(a->page_desc);
+  k.recs = static_cast<const uint32_t*>(a->entry_records);
+  k.neg_wrap = a->negative_ids != 0 && !a->entry_records;
   k.valid = a->valid_tokens;
   k.k_fp16 = a->k_fp16; k.v_fp16 = a->v_fp16; k.k_fp8 = a->k_fp8; k.v_fp8 = a->v_fp8;
   k.k_int8 = a->k_int8; k.v_int8 = a->v_int8; k.k_int4 = a->k_int4; k.v_int4 = a->v_int4;
@@ -371,6 +378,7 @@ iak_status iak_pack_page_descriptors(const iak_paged_decode_args* args, void* pa
   // as for a decode without descriptors and without rows
   iak_paged_decode_args a = *args;
   a.page_desc = nullptr;
+  a.entry_records = nullptr;
   a.batch = 0;
   Plan plan;
   const iak_status st = validate(&a, &plan);
@@ -386,6 +394,33 @@ iak_status iak_pack_page_descriptors(const iak_paged_decode_args* args, void* pa
   k.tags = a.page_tags;
   fill_metadata(&a, k);
   const hipError_t e = iak::launch_pack_descriptors(k, page_desc, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(IAK_EHIP, "kernel launch failed: %s", hipGetErrorString(e));
+  return IAK_OK;
+}
+
+iak_status iak_pack_entry_records(const iak_paged_decode_args* args, void* records, void* stream) {
+  if (!args) return fail(IAK_EINVAL, "args is NULL");
+  // the records come from the table, the tags, the tag map and the scales:
+  // validated as for a decode that reads them
+  iak_paged_decode_args a = *args;
+  a.page_desc = nullptr;
+  a.entry_records = nullptr;
+  Plan plan;
+  const iak_status st = validate(&a, &plan);
+  if (st != IAK_OK) return st;
+  const int64_t entries = (int64_t)a.batch * a.num_kv_heads * a.table_width;
+  if (entries == 0) return IAK_OK;
+  if (!records || (reinterpret_cast<uintptr_t>(records) & 31u))
+    return fail(IAK_EINVAL, "records must be non-NULL and 32-byte aligned");
+  if (reinterpret_cast<uintptr_t>(a.page_table) & 3u) return fail(IAK_EINVAL, "page_table must be 4-byte aligned");
+  iak::KArgs k;
+  std::memset(&k, 0, sizeof(k));
+  k.B = a.batch; k.Hkv = a.num_kv_heads; k.W = a.table_width; k.D = a.head_dim;
+  k.NP = a.num_pages;
+  k.table = a.page_table;
+  k.tags = a.page_tags;
+  fill_metadata(&a, k);
+  const hipError_t e = iak::launch_pack_records(k, records, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(IAK_EHIP, "kernel launch failed: %s", hipGetErrorString(e));
   return IAK_OK;
 }

@@ -67,10 +67,15 @@ struct KArgs {
 
   // page descriptors (iak_paged_decode_args.page_desc): [NP] x 32 B as two u4 (tag word, scale slots)
   const uint32_t* desc;
+  // entry records (iak_paged_decode_args.entry_records): [B * Hkv * W] x 32 B as two u4
+  // ((native tag, page id, 0, 0), scale slots)
+  const uint32_t* recs;
 };
 
 // page descriptors from page_tags, the tag map and the scale arrays of `k`
 hipError_t launch_pack_descriptors(const KArgs& k, void* desc, hipStream_t stream);
+// entry records from the page table, page_tags, the tag map and the scale arrays of `k`
+hipError_t launch_pack_records(const KArgs& k, void* recs, hipStream_t stream);
 
 // ev_begin / ev_end (may be null) are recorded on `stream` around the split
 // kernel alone, so callers can time it apart from the merge

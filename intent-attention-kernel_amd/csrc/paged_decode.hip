@@ -472,13 +472,22 @@ __device__ __forceinline__ uint32_t scale_bits_f16(const void* p, int64_t idx, i
 // Per-lane scale slots of the lane's own page, loaded once per split:
 //   FP8 / INT8      s0 = K scale, s1 = V scale (f32 bits)
 //   INT4_RESIDUAL   s0, s1 = K base / residual scale, s2, s3 = V base / residual (f32 bits)
-//   INT4            s0, s1 = K group scales as f16 pairs (g0,g1), (g2,g3); s2, s3 = V
-// With page descriptors the four slots are words 4-7 of the page's descriptor.
+//   INT4            s0, s1 = f16 pairs (q0,q1), (q2,q3) of the K scales of the four
+//                   quarters of head_dim (quarter q lies in group q * D/4 / int4_group);
+//                   s2, s3 = V
+// With page descriptors the four slots are words 4-7 of the page's descriptor;
+// with entry records, words 4-7 of the record of table entry `ent`.
 template <int D>
-__device__ __forceinline__ void load_page_scales(const KArgs& a, int pid, int tag, uint32_t (&slot)[4]) {
+__device__ __forceinline__ void load_page_scales(const KArgs& a, int pid, int tag, uint32_t (&slot)[4],
+                                                 int64_t ent) {
   slot[0] = slot[1] = slot[2] = slot[3] = 0u;
   if (pid < 0) return;
   const int64_t p = pid;
+  if (a.recs) {
+    const u4 x = *reinterpret_cast<const u4*>(a.recs + 8 * ent + 4);
+    slot[0] = x[0]; slot[1] = x[1]; slot[2] = x[2]; slot[3] = x[3];
+    return;
+  }
   if (a.desc) {
     const u4 x = *reinterpret_cast<const u4*>(a.desc + 8 * p + 4);
     slot[0] = x[0]; slot[1] = x[1]; slot[2] = x[2]; slot[3] = x[3];
@@ -499,7 +508,7 @@ __device__ __forceinline__ void load_page_scales(const KArgs& a, int pid, int ta
     const int ng = D / a.int4_group;   // 1, 2 or 4
 #pragma unroll
     for (int gi = 0; gi < 4; ++gi) {
-      const int src = gi < ng ? gi : ng - 1;
+      const int src = gi * ng / 4;      // the group of quarter gi
       const uint32_t kh = scale_bits_f16(a.k_int4_scale, p * ng + src, a.int4_sd);
       const uint32_t vh = scale_bits_f16(a.v_int4_scale, p * ng + src, a.int4_sd);
       slot[gi >> 1] |= kh << (16 * (gi & 1));
@@ -755,11 +764,22 @@ __device__ __forceinline__ void locate(const KArgs& a, int item, Split& sp, int&
 
 // First metadata stage of an item: lane i loads table entry start + i (bounded
 // by the table width, so it needs no count), the row's page count and token
-// bound.
+// bound. With entry records the entry's record gives the page id and its
+// native tag (`rtag`) in the same load.
 __device__ __forceinline__ void load_entry(const KArgs& a, int unit, int start, int len, int lane, int& raw,
-                                           int& cnt, int& bnd) {
+                                           int& rtag, int& cnt, int& bnd) {
   raw = -1;
-  if (lane < len && start + lane < a.W) raw = a.table[(int64_t)unit * a.W + start + lane];
+  rtag = IAK_TAG_SKIP;
+  if (lane < len && start + lane < a.W) {
+    const int64_t e = (int64_t)unit * a.W + start + lane;
+    if (a.recs) {
+      const u4 r = *reinterpret_cast<const u4*>(a.recs + 8 * e);
+      rtag = (int)r[0];
+      raw = (int)r[1];
+    } else {
+      raw = a.table[e];
+    }
+  }
   cnt = a.counts[unit];
   bnd = a.valid ? a.valid[unit] : 0x7FFFFFFF;
 }
@@ -768,8 +788,8 @@ __device__ __forceinline__ void load_entry(const KArgs& a, int unit, int start, 
 // token bound, validate the page id (wrapping negative ids when asked) and load
 // its tag through the tag map (caller tags outside [0, 8) take other_tag).
 // `lim`: tokens of the lane's entry that exist (PS unless the bound cuts it).
-__device__ __forceinline__ void load_tag(const KArgs& a, int raw, int cnt, int bnd, int start, int len, int lane,
-                                         int& pid, int& tag, int& n, int& lim) {
+__device__ __forceinline__ void load_tag(const KArgs& a, int raw, int rtag, int cnt, int bnd, int start, int len,
+                                         int lane, int& pid, int& tag, int& n, int& lim) {
   cnt = cnt < 0 ? 0 : (cnt > a.W ? a.W : cnt);
   n = cnt - start < len ? cnt - start : len;
   if (n < 0) n = 0;
@@ -781,9 +801,10 @@ __device__ __forceinline__ void load_tag(const KArgs& a, int raw, int cnt, int b
     int p = raw;
     if (a.neg_wrap && p < 0 && (int64_t)p >= -a.NP) p = (int)((int64_t)p + a.NP);
     if (p >= 0 && (int64_t)p < a.NP) {
-      // the caller's tag, or the native tag of the page's descriptor (the tag
-      // map then passes the precisions whose pools are present)
-      const int t = a.desc ? (int)a.desc[8 * (int64_t)p] : a.tags[p];
+      // the caller's tag, or the native tag of the entry's record or of the
+      // page's descriptor (the tag map then passes the precisions whose pools
+      // are present)
+      const int t = a.recs ? rtag : a.desc ? (int)a.desc[8 * (int64_t)p] : a.tags[p];
       tag = (t >= 0 && t < 8) ? (int)((a.tagmap >> (8 * t)) & 0xFFu) : a.other_tag;
       pid = p;
     }
@@ -814,13 +835,13 @@ void paged_decode_kernel(const KArgs a) {
   u4* kt = decode_lds + wv * (a.fused ? 4 * D : PS * D / 8);
 
   Split sp;
-  int pid, tag, lim;
+  int pid, tag, lim, start, unit;
   uint32_t slot[4];
   {
-    int start, unit, raw, cnt, bnd;
+    int raw, rtag, cnt, bnd;
     locate(a, item, sp, start, unit);
-    load_entry(a, unit, start, a.chunk, lane, raw, cnt, bnd);
-    load_tag(a, raw, cnt, bnd, start, a.chunk, lane, pid, tag, sp.n, lim);
+    load_entry(a, unit, start, a.chunk, lane, raw, rtag, cnt, bnd);
+    load_tag(a, raw, rtag, cnt, bnd, start, a.chunk, lane, pid, tag, sp.n, lim);
   }
 
   Wave<D, QF32> w;
@@ -851,7 +872,7 @@ void paged_decode_kernel(const KArgs a) {
   }
   // the scales are first needed by the classes below: loaded here, their round
   // trip overlaps the next class's ring fill instead of preceding the FP16 pages
-  load_page_scales<D>(a, pid, tag, slot);
+  load_page_scales<D>(a, pid, tag, slot, (int64_t)unit * a.W + start + lane);
 
   // ---- one-byte precisions ----
   {
@@ -899,8 +920,8 @@ void paged_decode_kernel(const KArgs a) {
       w.qhi[i] = q_int4_order(w.qhi[i]);
       if constexpr (QF32) w.qlo[i] = q_int4_order(w.qlo[i]);
     }
-    const int kg = ((D / 4) * g) / a.int4_group;
-    const int vg = ((D / 16) * c) / a.int4_group;
+    const int kg = g;        // the quarter of head_dim holding the lane's K dims (D/4)g ..
+    const int vg = c >> 2;   // and its V dims (D/16)c ..
     class_loop<IAK_RING_INT4, Raw4<D>>(
         __builtin_amdgcn_ballot_w64(tag == IAK_TAG_INT4), pid,
         [&](Raw4<D>& r, int p) {
@@ -929,7 +950,7 @@ __global__ __launch_bounds__(256) void pack_descriptors_kernel(const KArgs a, ui
   const int t = a.tags[p];
   const int tag = (t >= 0 && t < 8) ? (int)((a.tagmap >> (8 * t)) & 0xFFu) : a.other_tag;
   uint32_t slot[4];
-  load_page_scales<D>(a, (int)p, tag, slot);
+  load_page_scales<D>(a, (int)p, tag, slot, 0);
   u4* out = reinterpret_cast<u4*>(desc + 8 * p);
   out[0] = u4{(uint32_t)tag, 0u, 0u, 0u};
   out[1] = u4{slot[0], slot[1], slot[2], slot[3]};
@@ -944,6 +965,43 @@ hipError_t launch_pack_descriptors(const KArgs& k, void* desc, hipStream_t strea
   else
     hipLaunchKernelGGL(pack_descriptors_kernel<64>, dim3((unsigned)blocks), dim3(256), 0, stream, k,
                        static_cast<uint32_t*>(desc));
+  return hipGetLastError();
+}
+
+// Entry records: one thread per table entry writes the native tag and the
+// resolved page id a decode would use for it (words 0, 1; -1 and SKIP for an
+// entry whose id is out of range) and the page's scale slots (words 4-7).
+template <int D>
+__global__ __launch_bounds__(256) void pack_records_kernel(const KArgs a, uint32_t* recs, int64_t entries) {
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < entries; e += (int64_t)gridDim.x * 256) {
+    int p = a.table[e];
+    if (a.neg_wrap && p < 0 && (int64_t)p >= -a.NP) p = (int)((int64_t)p + a.NP);
+    int tag = IAK_TAG_SKIP;
+    if (p >= 0 && (int64_t)p < a.NP) {
+      const int t = a.tags[p];
+      tag = (t >= 0 && t < 8) ? (int)((a.tagmap >> (8 * t)) & 0xFFu) : a.other_tag;
+    } else {
+      p = -1;
+    }
+    uint32_t slot[4];
+    load_page_scales<D>(a, p, tag, slot, 0);
+    u4* out = reinterpret_cast<u4*>(recs + 8 * e);
+    out[0] = u4{(uint32_t)tag, (uint32_t)p, 0u, 0u};
+    out[1] = u4{slot[0], slot[1], slot[2], slot[3]};
+  }
+}
+
+hipError_t launch_pack_records(const KArgs& k, void* recs, hipStream_t stream) {
+  const int64_t entries = (int64_t)k.B * k.Hkv * k.W;
+  if (entries == 0) return hipSuccess;
+  const int64_t want = (entries + 255) / 256;
+  const unsigned blocks = (unsigned)(want < 65536 ? want : 65536);
+  if (k.D == 128)
+    hipLaunchKernelGGL(pack_records_kernel<128>, dim3(blocks), dim3(256), 0, stream, k, static_cast<uint32_t*>(recs),
+                       entries);
+  else
+    hipLaunchKernelGGL(pack_records_kernel<64>, dim3(blocks), dim3(256), 0, stream, k, static_cast<uint32_t*>(recs),
+                       entries);
   return hipGetLastError();
 }
 

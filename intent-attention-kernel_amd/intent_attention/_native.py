@@ -14,7 +14,7 @@ from typing import Optional
 _HERE = os.path.dirname(os.path.abspath(__file__))
 # IAK_LIBRARY selects another build of the same ABI (e.g. a tuning variant)
 LIB_PATH = os.environ.get("IAK_LIBRARY") or os.path.join(_HERE, "libiak.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 IAK_OK, IAK_EINVAL, IAK_ENOTSUP, IAK_EHIP = 0, 1, 2, 3
 
@@ -52,6 +52,7 @@ class PagedDecodeArgs(ctypes.Structure):
         ("valid_tokens", c_void_p),
         ("merge_in_kernel", c_i32),
         ("page_desc", c_void_p),
+        ("entry_records", c_void_p),
     ]
 
 
@@ -147,7 +148,8 @@ EXPORTED = ("iak_abi_version", "iak_status_string", "iak_last_error",
             "iak_mla_decode_workspace", "iak_mla_decode", "iak_quantize_pages",
             "iak_build_page_tables", "iak_paged_decode_timed", "iak_mla_decode_timed",
             "iak_paged_decode_noalloc", "iak_transcode_pages", "iak_prefetch_pages", "iak_paged_decode_plan",
-            "iak_mla_decode_rows", "iak_pack_page_descriptors")
+            "iak_mla_decode_rows", "iak_pack_page_descriptors",
+            "iak_pack_entry_records")
 NOALLOC_SCRATCH_BYTES = 16 << 20   # IAK_NOALLOC_SCRATCH_BYTES
 
 _lib: Optional[ctypes.CDLL] = None
@@ -206,6 +208,8 @@ def load() -> ctypes.CDLL:
     lib.iak_build_page_tables.argtypes = [ctypes.POINTER(PageTableArgs), c_void_p]
     lib.iak_pack_page_descriptors.restype = ctypes.c_int
     lib.iak_pack_page_descriptors.argtypes = [ctypes.POINTER(PagedDecodeArgs), c_void_p, c_void_p]
+    lib.iak_pack_entry_records.restype = ctypes.c_int
+    lib.iak_pack_entry_records.argtypes = [ctypes.POINTER(PagedDecodeArgs), c_void_p, c_void_p]
     ver = lib.iak_abi_version()
     if ver != ABI_VERSION:
         _load_error = f"libiak.so ABI version {ver} != expected {ABI_VERSION}; rebuild the library"
@@ -263,6 +267,14 @@ PAGE_DESC_BYTES = 32   # one iak_paged_decode_args.page_desc entry
 def pack_page_descriptors(args: PagedDecodeArgs, desc_ptr: int, stream: int) -> None:
     """iak_pack_page_descriptors: ``args.num_pages`` 32-byte descriptors at ``desc_ptr``."""
     check(load().iak_pack_page_descriptors(ctypes.byref(args), desc_ptr or None, stream or None))
+
+
+ENTRY_RECORD_BYTES = 32   # one iak_paged_decode_args.entry_records entry
+
+
+def pack_entry_records(args: PagedDecodeArgs, records_ptr: int, stream: int) -> None:
+    """iak_pack_entry_records: batch x num_kv_heads x table_width 32-byte records at ``records_ptr``."""
+    check(load().iak_pack_entry_records(ctypes.byref(args), records_ptr or None, stream or None))
 
 
 def paged_decode_noalloc(args: PagedDecodeArgs, stream: int) -> None:

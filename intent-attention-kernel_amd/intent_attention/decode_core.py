@@ -151,14 +151,18 @@ def make_plan(q: torch.Tensor, pools: PagePools, page_table: torch.Tensor, page_
               pages_per_split: int = 0, map_other_tags: bool = False,
               valid_tokens: Optional[torch.Tensor] = None,
               merge_in_kernel: Optional[bool] = None,
-              page_descriptors: Optional[torch.Tensor] = None) -> "DecodePlan":
+              page_descriptors: Optional[torch.Tensor] = None,
+              entry_records: Optional[torch.Tensor] = None) -> "DecodePlan":
     """Validate the arguments of ``paged_decode`` once; the returned plan
     re-launches the decode on the same tensors with ``run()``.
 
     ``page_descriptors`` (optional): [num_pages, 8] int32 descriptors from
     ``DecodePlan.pack_descriptors`` (or ``pack_page_descriptors``), read in
     place of ``page_tags``, ``tag_map`` and the scale tensors: one 32-byte
-    line of metadata per selected page."""
+    line of metadata per selected page.
+    ``entry_records`` (optional): [B, Hkv, W, 8] int32 records from
+    ``DecodePlan.pack_records``, read in place of the page table's entries and
+    their pages' tags and scales: one contiguous metadata stream per split."""
     if q.dim() != 3:
         raise ValueError(f"q must have shape [B, H, D], got {tuple(q.shape)}")
     B, Hq, D = q.shape
@@ -257,6 +261,8 @@ def make_plan(q: torch.Tensor, pools: PagePools, page_table: torch.Tensor, page_
     plan = DecodePlan(a, dev, out, keep=(q, page_table, page_counts, page_tags, valid_tokens, pools))
     if page_descriptors is not None:
         plan.use_descriptors(page_descriptors)
+    if entry_records is not None:
+        plan.use_records(entry_records)
     return plan
 
 
@@ -307,6 +313,7 @@ class DecodePlan:
             self._filled = torch.cuda.Event()
             self._filled.record(torch.cuda.current_stream(device))
         self._desc: Optional[torch.Tensor] = None
+        self._recs: Optional[torch.Tensor] = None
 
     def pack_descriptors(self, out: Optional[torch.Tensor] = None, stream: Optional[int] = None) -> torch.Tensor:
         """Pack this plan's page tags (through its tag map), and the scales each
@@ -322,6 +329,42 @@ class DecodePlan:
         N.pack_page_descriptors(self.args, out.data_ptr(), s)
         self.use_descriptors(out)
         return out
+
+    def _records_shape(self) -> tuple:
+        a = self.args
+        return (int(a.batch), int(a.num_kv_heads), int(a.table_width), N.ENTRY_RECORD_BYTES // 4)
+
+    def pack_records(self, out: Optional[torch.Tensor] = None, stream: Optional[int] = None) -> torch.Tensor:
+        """Pack this plan's page table entries with their pages' native tags and
+        scales into 32-byte entry records ([B, Hkv, W, 8] int32; ``out`` if
+        given) on ``stream``, and make later runs read them instead of the
+        table, tags and scales. A snapshot: pack again after the table, the
+        tags or the scales change (once per routing decision)."""
+        shape = self._records_shape()
+        if out is None:
+            out = torch.empty(shape, dtype=torch.int32, device=self.device)
+        self._check_records(out)
+        s = torch.cuda.current_stream(self.device).cuda_stream if stream is None else stream
+        saved = (self.args.page_desc, self.args.entry_records)
+        N.pack_entry_records(self.args, out.data_ptr(), s)
+        self.args.page_desc, self.args.entry_records = saved
+        self.use_records(out)
+        return out
+
+    def _check_records(self, recs: torch.Tensor) -> None:
+        shape = self._records_shape()
+        if recs.dtype != torch.int32 or tuple(recs.shape) != shape:
+            raise ValueError(f"entry records must be int32 {list(shape)}, got {recs.dtype} {tuple(recs.shape)}")
+        if recs.device != self.device or not recs.is_contiguous() or recs.data_ptr() % 32:
+            raise ValueError(f"entry records must be a contiguous, 32-byte aligned tensor on {self.device}")
+
+    def use_records(self, recs: Optional[torch.Tensor]) -> None:
+        """Read ``recs`` (packed for this plan's table, pages and pools) in place
+        of the table entries, tags, tag map and scales; None goes back to them."""
+        if recs is not None:
+            self._check_records(recs)
+        self._recs = recs
+        self.args.entry_records = recs.data_ptr() if recs is not None else None
 
     def use_descriptors(self, desc: Optional[torch.Tensor]) -> None:
         """Read ``desc`` (packed for the same pages and pools) in place of the

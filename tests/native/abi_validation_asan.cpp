@@ -59,9 +59,12 @@ void fuzz_paged_decode(int n) {
     // a NULL or misaligned destination is rejected before any launch
     count(iak_pack_page_descriptors(&a, nullptr, nullptr));
     count(iak_pack_page_descriptors(&a, reinterpret_cast<void*>(0x100010), nullptr));
+    count(iak_pack_entry_records(&a, nullptr, nullptr));
+    count(iak_pack_entry_records(&a, reinterpret_cast<void*>(0x100010), nullptr));
   }
   count(iak_paged_decode_workspace(nullptr, nullptr));
   count(iak_pack_page_descriptors(nullptr, nullptr, nullptr));
+  count(iak_pack_entry_records(nullptr, nullptr, nullptr));
   count(iak_paged_decode_plan(nullptr, nullptr));
   // well-formed arguments (fake, aligned device addresses; never launched):
   // the plan and workspace sizes are computed for every shape

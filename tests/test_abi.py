@@ -263,3 +263,35 @@ def test_page_descriptor_validation_without_gpu():
     a.num_pages = 0                             # nothing to pack: no launch, no error
     a.tag_map[3] = N.TAG_SKIP
     N.pack_page_descriptors(a, 0, 0)
+
+
+def test_entry_record_validation_without_gpu():
+    """entry_records: 32-byte aligned; with them page_table, page_tags and the
+    scale arrays may be NULL (page_counts may not). The pack entry point needs
+    the table and tags of a valid decode call and a 32-byte aligned
+    destination; it rejects the rest before any launch."""
+    from intent_attention import _native as N
+    a = _decode_args(N, 2, 2, 4, 100)
+    a.num_pages = 64
+    a.entry_records = 0x100010
+    with pytest.raises(ValueError, match="entry_records must be 32-byte aligned"):
+        N.workspace_bytes(a)
+    a.entry_records = 0x100020
+    a.page_table = a.page_tags = None
+    assert N.workspace_bytes(a) > 0
+    a.page_counts = None
+    with pytest.raises(ValueError, match="page_counts"):
+        N.workspace_bytes(a)
+    a.page_counts = 16
+    with pytest.raises(ValueError, match="page_table"):        # packing needs the table
+        N.pack_entry_records(a, 0x400000, 0)
+    a.page_table = 16
+    with pytest.raises(ValueError, match="page_tags"):
+        N.pack_entry_records(a, 0x400000, 0)
+    a.page_tags = 16
+    with pytest.raises(ValueError, match="records"):
+        N.pack_entry_records(a, 0, 0)
+    with pytest.raises(ValueError, match="records"):
+        N.pack_entry_records(a, 0x400010, 0)
+    a.table_width = 0                                          # no entries: no launch, no error
+    N.pack_entry_records(a, 0, 0)

@@ -1,14 +1,16 @@
 """Page descriptors (iak_paged_decode_args.page_desc, iak_pack_page_descriptors)
-on the GPU.
+and entry records (entry_records, iak_pack_entry_records) on the GPU.
 
 A descriptor holds a page's native tag and the scales its precision uses in
-one 32-byte line. Checked here: the packed words equal a host restatement of
-the tag translation and scale slots (tag map, map_other_tags, out-of-range
-tags, f16 and f32 scales, INT4 groups of D/4, D/2 and D); a decode that reads
-descriptors is bit-identical to the same decode on page_tags, tag_map and the
+one 32-byte line; an entry record holds the same for one page-table entry,
+with the resolved page id. Checked here: the packed words equal a host
+restatement of the tag translation, id resolution and scale slots (tag map,
+map_other_tags, out-of-range tags and ids, negative ids, f16 and f32 scales,
+INT4 groups of D/4, D/2 and D); a decode that reads descriptors or records is
+bit-identical to the same decode on page_table, page_tags, tag_map and the
 scale arrays, in both merge forms, with token bounds and negative page ids; a
-descriptor whose precision has no pools in the decode contributes nothing;
-the result also matches the oracle."""
+precision with no pools in the decode contributes nothing; the result also
+matches the oracle."""
 import sys
 
 import numpy as np
@@ -48,25 +50,50 @@ def expected_descriptors(caller_tags, tag_map, map_other_tags, pools, D, group):
     NP = len(caller_tags)
     out = np.zeros((NP, 8), np.uint32)
     tm = [int(t) if int(t) in NATIVE else Dm.SKIP for t in tag_map]
-    ng = D // group
     for p, c in enumerate(caller_tags):
         c = int(c)
         t = tm[c] if 0 <= c < 8 else (tm[7] if map_other_tags else Dm.SKIP)
         out[p, 0] = t
-        if t == Dm.FP8:
-            out[p, 4], out[p, 5] = _f32_bits(pools["k_fp8_scale"][p]), _f32_bits(pools["v_fp8_scale"][p])
-        elif t == Dm.INT8:
-            out[p, 4], out[p, 5] = _f32_bits(pools["k_i8_scale"][p]), _f32_bits(pools["v_i8_scale"][p])
-        elif t == Dm.INT4_RESIDUAL:
-            kr, vr = pools["k_i4r_scale"][p], pools["v_i4r_scale"][p]
-            out[p, 4:8] = [_f32_bits(kr[0]), _f32_bits(kr[1]), _f32_bits(vr[0]), _f32_bits(vr[1])]
-        elif t == Dm.INT4:
-            for w, base in (("k", 4), ("v", 6)):
-                s = pools[f"{w}_i4_scale"][p]
-                h = [_f16_bits(s[min(g, ng - 1)]) for g in range(4)]
-                out[p, base] = h[0] | (h[1] << 16)
-                out[p, base + 1] = h[2] | (h[3] << 16)
+        out[p, 4:8] = scale_slots(t, p, pools, D, group)
     return out
+
+
+def scale_slots(t, p, pools, D, group):
+    """Words 4-7 of page p's descriptor for native tag t."""
+    out = np.zeros(4, np.uint32)
+    if t == Dm.FP8:
+        out[0], out[1] = _f32_bits(pools["k_fp8_scale"][p]), _f32_bits(pools["v_fp8_scale"][p])
+    elif t == Dm.INT8:
+        out[0], out[1] = _f32_bits(pools["k_i8_scale"][p]), _f32_bits(pools["v_i8_scale"][p])
+    elif t == Dm.INT4_RESIDUAL:
+        kr, vr = pools["k_i4r_scale"][p], pools["v_i4r_scale"][p]
+        out[:] = [_f32_bits(kr[0]), _f32_bits(kr[1]), _f32_bits(vr[0]), _f32_bits(vr[1])]
+    elif t == Dm.INT4:
+        # one f16 scale per quarter of head_dim: the group holding dims q * D/4 ..
+        for w, base in (("k", 0), ("v", 2)):
+            s = pools[f"{w}_i4_scale"][p]
+            h = [_f16_bits(s[(q * (D // 4)) // group]) for q in range(4)]
+            out[base] = h[0] | (h[1] << 16)
+            out[base + 1] = h[2] | (h[3] << 16)
+    return out
+
+
+def expected_records(table, caller_tags, tag_map, map_other_tags, negative_ids, pools, D, group):
+    """Host restatement of the entry records of every table entry."""
+    NP = len(caller_tags)
+    per_page = expected_descriptors(caller_tags, tag_map, map_other_tags, pools, D, group)
+    flat = table.reshape(-1)
+    out = np.zeros((flat.size, 8), np.uint32)
+    for e, raw in enumerate(flat):
+        p = int(raw)
+        if negative_ids and -NP <= p < 0:
+            p += NP
+        if 0 <= p < NP:
+            out[e] = per_page[p]
+            out[e, 1] = p
+        else:
+            out[e, 0], out[e, 1] = Dm.SKIP, 0xFFFFFFFF
+    return out.reshape(*table.shape, 8)
 
 
 def _case(seed, B, Hq, Hkv, D, NP, W, *, group=32, scale_f32=False, mix=None):
@@ -118,6 +145,16 @@ def test_descriptor_decode_bit_identical(dev, case, merge):
     assert torch.equal(desc_plan.out, base.out)
     ref = Dm.paged_decode_oracle(q.astype(np.float32), pools, table, counts, tags)
     assert float(np.abs(desc_plan.out.cpu().numpy() - ref).max()) <= TOL_QUANT
+    # entry records (the plan reads them in place of the descriptors too)
+    recs = desc_plan.pack_records()
+    torch.cuda.synchronize()
+    want_r = expected_records(table, tags, list(range(8)), False, False, pools, D, group)
+    assert np.array_equal(recs.cpu().numpy().view(np.uint32), want_r)
+    desc_plan.out.fill_(float("nan"))
+    desc_plan.run()
+    torch.cuda.synchronize()
+    assert torch.equal(desc_plan.out, base.out)
+    desc_plan.use_records(None)
     # back to the tag and scale arrays
     desc_plan.use_descriptors(None)
     desc_plan.out.fill_(float("nan"))
@@ -164,6 +201,19 @@ def test_descriptors_follow_tag_map_and_other_tags(dev):
     assert torch.equal(dplan.out, base.out)
     ref = Dm.paged_decode_oracle(q.astype(np.float32), pools, table, counts, native, valid_tokens=valid)
     assert float(np.abs(dplan.out.cpu().numpy() - ref).max()) <= TOL_QUANT
+    # entry records: negative ids resolved at packing, out-of-range ids past the counts
+    neg2 = neg.copy()
+    for r in range(B * Hkv):
+        b, h = divmod(r, Hkv)
+        neg2[b, h, counts[b, h]:] = rng.choice([NP, NP + 5, -NP - 1, 2 ** 31 - 1], size=W - counts[b, h])
+    rplan = make_plan(t(q), dp, t(neg2), t(counts), t(caller), **kw)
+    recs = rplan.pack_records()
+    torch.cuda.synchronize()
+    want_r = expected_records(neg2, caller, tag_map, True, True, pools, D, 32)
+    assert np.array_equal(recs.cpu().numpy().view(np.uint32), want_r)
+    rplan.run()
+    torch.cuda.synchronize()
+    assert torch.equal(rplan.out, base.out)
 
 
 def test_descriptor_precision_without_pools_is_skipped(dev):
@@ -186,6 +236,13 @@ def test_descriptor_precision_without_pools_is_skipped(dev):
     got.run()
     torch.cuda.synchronize()
     assert torch.equal(got.out, want.out)
+    # the same with entry records packed on the full pools
+    rfull = make_plan(t(q), full, t(table), t(counts), t(tags), out_dtype=torch.float32)
+    recs = rfull.pack_records()
+    got_r = make_plan(t(q), no_int4, t(table), t(counts), t(tags), out_dtype=torch.float32, entry_records=recs)
+    got_r.run()
+    torch.cuda.synchronize()
+    assert torch.equal(got_r.out, want.out)
     tags_skip = np.where(tags == Dm.INT4, Dm.SKIP, tags).astype(np.int32)
     ref = Dm.paged_decode_oracle(q.astype(np.float32), pools, table, counts, tags_skip)
     assert float(np.abs(got.out.cpu().numpy() - ref).max()) <= TOL_QUANT
