@@ -189,8 +189,10 @@ __device__ __forceinline__ uint32_t f2u(float x) { return __builtin_bit_cast(uin
 // ((b * Hkv + hk) * splits + s) * G + c; acc is float32, or acc / l as float16
 // (A16: KArgs::acc16). WPR waves (1, 2 or 4) share one
 // (batch, query head): wave part p takes the splits s = p (mod WPR), eight at a
-// time with their loads issued together; the parts agree on the global max
-// and add their sums through LDS. A 256-thread block holds 4 / WPR heads.
+// time with their loads issued together, and keeps a running (max, sum, acc)
+// with the online log-sum-exp rule, so it reads every partial once; the parts
+// then combine through LDS by the same rule. A 256-thread block holds 4 / WPR
+// heads.
 // --------------------------------------------------------------------------- //
 
 template <int D, int WPR, bool A16>
@@ -207,23 +209,11 @@ __global__ __launch_bounds__(256) void splitk_merge_kernel(const KArgs a) {
   const int hk = h / a.G, c = h - hk * a.G;
   const int S = live ? a.splits : 0;
   const int64_t first = (((int64_t)b * a.Hkv + hk) * a.splits) * a.G + c;   // slot of split 0
-  // max over the part's splits, then over the parts
-  float M = -__builtin_inff();
-  for (int s = p + WPR * lane; s < S; s += WPR * 64) M = fmaxf(M, a.ws_m[first + (int64_t)s * a.G]);
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
-  if constexpr (WPR > 1) {
-    if (lane == 0) part_m[w] = M;
-    __syncthreads();
-    const int w0 = w - p;
-#pragma unroll
-    for (int k = 0; k < WPR; ++k) M = fmaxf(M, part_m[w0 + k]);
-  }
+  float M = -__builtin_inff(), L = 0.f;
   float o[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) o[j] = 0.f;
-  float L = 0.f;
-  if (M > -__builtin_inff()) {
+  {
     constexpr int U = 8;
     const int n = S > p ? (S - p + WPR - 1) / WPR : 0;   // splits of this part
     for (int i = 0; i < n; i += U) {
@@ -246,26 +236,45 @@ __global__ __launch_bounds__(256) void splitk_merge_kernel(const KArgs a) {
       }
 #pragma unroll
       for (int k = 0; k < U; ++k) {
-        // 0 for empty splits (m = -inf) and for the clamped reloads past the part's end
-        const float wgt = i + k < n ? __builtin_amdgcn_exp2f(ms[k] - M) : 0.f;
-        L += wgt * ls[k];
-        const float wa = A16 ? wgt * ls[k] : wgt;   // compact partials hold acc / l
+        const float mk = ms[k];
+        // empty splits (m = -inf) and the clamped reloads past the part's end add nothing
+        if (i + k < n && mk > -__builtin_inff()) {
+          if (mk > M) {
+            const float sc = __builtin_amdgcn_exp2f(M - mk);   // 0 while M is -inf
+            L *= sc;
 #pragma unroll
-        for (int j = 0; j < PER; ++j) o[j] += wa * av[k][j];
+            for (int j = 0; j < PER; ++j) o[j] *= sc;
+            M = mk;
+          }
+          const float wgt = __builtin_amdgcn_exp2f(mk - M);
+          L += wgt * ls[k];
+          const float wa = A16 ? wgt * ls[k] : wgt;   // compact partials hold acc / l
+#pragma unroll
+          for (int j = 0; j < PER; ++j) o[j] += wa * av[k][j];
+        }
       }
     }
   }
   if constexpr (WPR > 1) {
-    if (lane == 0) part_l[w] = L;
+    if (lane == 0) { part_m[w] = M; part_l[w] = L; }
 #pragma unroll
     for (int j = 0; j < PER; ++j) part_o[w][PER * lane + j] = o[j];
     __syncthreads();
     if (p != 0) return;
+    float Mx = M;
 #pragma unroll
-    for (int k = 1; k < WPR; ++k) {
-      L += part_l[w + k];
+    for (int k = 1; k < WPR; ++k) Mx = fmaxf(Mx, part_m[w + k]);
+    L = 0.f;
 #pragma unroll
-      for (int j = 0; j < PER; ++j) o[j] += part_o[w + k][PER * lane + j];
+    for (int j = 0; j < PER; ++j) o[j] = 0.f;
+    if (Mx > -__builtin_inff()) {
+#pragma unroll
+      for (int k = 0; k < WPR; ++k) {
+        const float wk = __builtin_amdgcn_exp2f(part_m[w + k] - Mx);   // 0 for an empty part
+        L += wk * part_l[w + k];
+#pragma unroll
+        for (int j = 0; j < PER; ++j) o[j] += wk * part_o[w + k][PER * lane + j];
+      }
     }
   }
   if (!live) return;

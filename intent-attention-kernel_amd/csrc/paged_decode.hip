@@ -626,38 +626,58 @@ __device__ void merge_in_kernel(const KArgs& a, const Split& sp, const Wave<D, Q
   __syncthreads();
   if (!last) return;
 
-  // the row's merge: output (head h, dim d) from the nwg workgroup partials
-  for (int o = t; o < GD; o += 64 * IAK_WAVES_PER_BLOCK) {
-    const int h = o / D, d = o - h * D;
-    const int64_t s0 = first + h;
-    float M = -__builtin_inff();
-    for (int k = 0; k < nwg; ++k)
-      M = fmaxf(M, __hip_atomic_load(a.ws_m + s0 + (int64_t)k * a.G, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    float L = 0.f, A = 0.f;
-    if (M > -__builtin_inff()) {
-      constexpr int U = 8;
-      for (int i = 0; i < nwg; i += U) {
-        float ms[U], ls[U], av[U];
+  // the row's merge: output (head h, dim d) from the nwg workgroup partials,
+  // OU outputs per thread and U partials per batch with every load of a batch
+  // issued together, combined with the online log-sum-exp rule
+  constexpr int OU = 2, U = 8;
+  constexpr int NT = 64 * IAK_WAVES_PER_BLOCK;
+  for (int o0 = t; o0 < GD; o0 += NT * OU) {
+    float M[OU], L[OU], A[OU];
+#pragma unroll
+    for (int j = 0; j < OU; ++j) { M[j] = -__builtin_inff(); L[j] = 0.f; A[j] = 0.f; }
+    for (int i = 0; i < nwg; i += U) {
+      float ms[OU][U], ls[OU][U], av[OU][U];
+#pragma unroll
+      for (int j = 0; j < OU; ++j) {
+        const int o = o0 + NT * j < GD ? o0 + NT * j : o0;   // past the end: a duplicate, not written
+        const int h = o / D, d = o - h * D;
 #pragma unroll
         for (int k = 0; k < U; ++k) {
-          const int64_t s = s0 + (int64_t)(i + k < nwg ? i + k : nwg - 1) * a.G;
-          ms[k] = __hip_atomic_load(a.ws_m + s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          ls[k] = __hip_atomic_load(a.ws_l + s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          av[k] = __hip_atomic_load(a.ws_acc + s * D + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-#pragma unroll
-        for (int k = 0; k < U; ++k) {
-          const float wt = i + k < nwg ? __builtin_amdgcn_exp2f(ms[k] - M) : 0.f;
-          L += wt * ls[k];
-          A += wt * av[k];
+          const int64_t sl = first + h + (int64_t)(i + k < nwg ? i + k : nwg - 1) * a.G;
+          ms[j][k] = __hip_atomic_load(a.ws_m + sl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          ls[j][k] = __hip_atomic_load(a.ws_l + sl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          av[j][k] = __hip_atomic_load(a.ws_acc + sl * D + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
       }
+#pragma unroll
+      for (int j = 0; j < OU; ++j)
+#pragma unroll
+        for (int k = 0; k < U; ++k) {
+          const float mk = ms[j][k];
+          if (i + k < nwg && mk > -__builtin_inff()) {   // an empty partial (m = -inf) adds nothing
+            if (mk > M[j]) {
+              const float sc = __builtin_amdgcn_exp2f(M[j] - mk);   // 0 while M is -inf
+              L[j] *= sc;
+              A[j] *= sc;
+              M[j] = mk;
+            }
+            const float wt = __builtin_amdgcn_exp2f(mk - M[j]);
+            L[j] += wt * ls[j][k];
+            A[j] += wt * av[j][k];
+          }
+        }
     }
-    const float v = A * (L > 0.f ? 1.0f / L : 0.f);
-    const int64_t op = (int64_t)sp.b * a.osb + (int64_t)(sp.hk * a.G + h) * a.osh + d;
-    if (a.out_dtype == IAK_DTYPE_F32) reinterpret_cast<float*>(a.out)[op] = v;
-    else if (a.out_dtype == IAK_DTYPE_F16) reinterpret_cast<_Float16*>(a.out)[op] = (_Float16)v;
-    else reinterpret_cast<__bf16*>(a.out)[op] = (__bf16)v;
+#pragma unroll
+    for (int j = 0; j < OU; ++j) {
+      const int o = o0 + NT * j;
+      if (o >= GD) continue;
+      const int h = o / D, d = o - h * D;
+      const float v = A[j] * (L[j] > 0.f ? 1.0f / L[j] : 0.f);
+      const int64_t op = (int64_t)sp.b * a.osb + (int64_t)(sp.hk * a.G + h) * a.osh + d;
+      if (a.out_dtype == IAK_DTYPE_F32) reinterpret_cast<float*>(a.out)[op] = v;
+      else if (a.out_dtype == IAK_DTYPE_F16) reinterpret_cast<_Float16*>(a.out)[op] = (_Float16)v;
+      else reinterpret_cast<__bf16*>(a.out)[op] = (__bf16)v;
+    }
   }
   // reset for the next call, written through like the partials (its cache
   // line holds other rows' counters)
