@@ -87,7 +87,8 @@ def test_full_config_sampled_rows(name, tol):
     bench times; 6 rows spread over the batch checked against the oracle with
     absolute, relative and cosine bars, for the bench's query scale and for
     peaked softmaxes (q times sqrt(128) and 4 sqrt(128)); then the negative
-    control."""
+    control. The same decode reading packed page descriptors, and packed entry
+    records, gives every output bit-identical."""
     print(f"[gpu-case] full {name} workload, sampled rows", flush=True)
     from intent_attention.decode_core import NATIVE_TAG_MAP, make_plan
     dev = torch.device("cuda:0")
@@ -104,6 +105,16 @@ def test_full_config_sampled_rows(name, tol):
         out = torch.empty((cfg["B"], cfg["Hq"], cfg["D"]), dtype=torch.float32, device=dev)
         make_plan(wl["q"], wl["pools"], wl["table"], wl["counts"], wl["tags"], out=out).run()
         torch.cuda.synchronize()
+        if mult == 1.0:
+            for form in ("page descriptors", "entry records"):
+                alt = torch.full_like(out, float("nan"))
+                plan = make_plan(wl["q"], wl["pools"], wl["table"], wl["counts"], wl["tags"], out=alt)
+                packed = plan.pack_descriptors() if form == "page descriptors" else plan.pack_records()
+                plan.run()
+                torch.cuda.synchronize()
+                print(f"[gpu-case] {name} with {form}: bit-identical {bool(torch.equal(alt, out))}", flush=True)
+                assert torch.equal(alt, out)
+                del alt, plan, packed
         ref = _row_oracle(wl, rows).reshape(len(rows), G, cfg["D"])
         got = out.reshape(R, G, cfg["D"])[rows].cpu().numpy()
         err, rel, cos = _metrics(got, ref)
