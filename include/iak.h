@@ -53,7 +53,7 @@
 extern "C" {
 #endif
 
-#define IAK_ABI_VERSION 5
+#define IAK_ABI_VERSION 6
 
 /* Grid size from which merge_in_kernel = 2 merges inside the decode kernel. */
 #define IAK_MERGE_IN_KERNEL_MIN_WORKGROUPS 1024
@@ -196,9 +196,13 @@ iak_status iak_paged_decode_workspace(const iak_paged_decode_args* args, size_t*
  * the reference (its Triton kernel has one program per (batch, head)). */
 typedef struct {
   int32_t splits;            /* splits per (batch, kv head) row (1: no merge) */
-  int32_t pages_per_split;   /* table entries per split */
+  int32_t pages_per_split;   /* table entries per split (of the first tier) */
   int32_t merge_in_kernel;   /* 1: the decode kernel merges the splits itself */
   size_t workspace_bytes;    /* = iak_paged_decode_workspace */
+  int32_t tail_splits;       /* of `splits`, those of the second tier (0: one tier): the
+                                last entries of each row in short splits launched after
+                                every row's first tier (automatic plans on large grids) */
+  int32_t tail_pages_per_split;   /* table entries per second-tier split (0: one tier) */
 } iak_paged_decode_plan_info;
 iak_status iak_paged_decode_plan(const iak_paged_decode_args* args, iak_paged_decode_plan_info* info);
 
@@ -241,8 +245,10 @@ iak_status iak_paged_decode_timed(const iak_paged_decode_args* args, void* works
 
 /* iak_paged_decode without a caller workspace and without any allocation: the
  * split-K partials live in a library-owned device array of
- * IAK_NOALLOC_SCRATCH_BYTES (one per GPU, held until the process ends).
- * Arguments whose partials need more return IAK_EINVAL. Every call on a GPU
+ * IAK_NOALLOC_SCRATCH_BYTES (one per GPU, held until the process ends). It
+ * runs the merge kernel on a one-tier split plan (tail_splits = 0), whose
+ * partials are at most those of iak_paged_decode_workspace with
+ * merge_in_kernel = 0. Arguments whose partials need more return IAK_EINVAL. Every call on a GPU
  * shares that GPU's array, so calls that overlap on one GPU (concurrent
  * streams or threads) race; calls ordered on one stream do not. No
  * counterpart in the reference: it is for callers that cannot allocate

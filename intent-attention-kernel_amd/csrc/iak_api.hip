@@ -41,11 +41,14 @@ size_t round_up(size_t x) { return (x + WS_ALIGN - 1) / WS_ALIGN * WS_ALIGN; }
 
 struct Plan {
   int G, splits, chunk;
+  int splitsA, chunkB;                        // the first tier's splits, the second tier's length
   bool fused;                                 // the decode kernel merges (merge_in_kernel)
   size_t ws_m, ws_l, ws_acc, ws_cnt, total;   // byte offsets / total
 };
 
-iak_status validate(const iak_paged_decode_args* a, Plan* plan) {
+// `tiers`: two-tier split plans allowed (not for iak_paged_decode_noalloc, whose
+// fixed scratch holds one-tier partials)
+iak_status validate(const iak_paged_decode_args* a, Plan* plan, bool tiers = true) {
   if (!a) return fail(IAK_EINVAL, "args is NULL");
   if (a->batch < 0 || a->num_q_heads <= 0 || a->num_kv_heads <= 0 || a->table_width < 0 || a->num_pages < 0)
     return fail(IAK_EINVAL, "negative or zero size (batch=%d, num_q_heads=%d, num_kv_heads=%d, table_width=%d, num_pages=%lld)",
@@ -145,6 +148,26 @@ iak_status validate(const iak_paged_decode_args* a, Plan* plan) {
   }
   int splits = (W + chunk - 1) / chunk;
   if (splits < 1) splits = 1;
+  // Two tiers on grids of more than about 1.5 resident generations of waves
+  // (automatic plans): the first three quarters of each row's entries in splits
+  // of `chunk` entries, the rest in 32-entry splits placed after every row's
+  // first tier in the grid. Of the waves sharing a CU the oldest are served
+  // first (a wave-timeline probe: at cfg3 the older workgroup of a CU takes
+  // 95 us per split, the younger 163 us, with the same bytes), so the grid's
+  // last workgroups are the slowest; short ones there shorten the tail (cfg3
+  // 326.3-327.7 -> 321.7-322.0 us per step). Both tiers hold whole fours of
+  // splits, so a workgroup's four waves stay in one tier and one row whichever
+  // merge form runs.
+  int splitsA = splits, chunkB = chunk;
+  if (tiers && a->pages_per_split == 0 && rows * (long long)splits > IAK_TIER_MIN_WAVES) {
+    const int sa = (int)((long long)W * 3 / 4 / chunk) / 4 * 4;
+    const int tail = W - sa * chunk;
+    if (sa >= 4 && tail > 0) {
+      splitsA = sa;
+      chunkB = IAK_TIER_CHUNK;
+      splits = sa + ((tail + IAK_TIER_CHUNK - 1) / IAK_TIER_CHUNK + 3) / 4 * 4;
+    }
+  }
   // in-kernel merge: a workgroup's four waves take four splits of one row, so
   // the row's split count becomes a multiple of four (trailing splits may be
   // empty: they read no entry)
@@ -155,11 +178,16 @@ iak_status validate(const iak_paged_decode_args* a, Plan* plan) {
   bool fused = a->merge_in_kernel != 0 && splits > 1;
   if (fused && a->merge_in_kernel == 2)
     fused = rows * (long long)((splits + 3) / 4) >= IAK_MERGE_IN_KERNEL_MIN_WORKGROUPS;
-  if (fused) splits = (splits + 3) / 4 * 4;
+  if (fused && splitsA == splits) {
+    splits = (splits + 3) / 4 * 4;
+    splitsA = splits;
+  }
   if (rows * (long long)splits > 0x7FFFFFFFLL) return fail(IAK_EINVAL, "too many splits");
   plan->G = G;
   plan->splits = splits;
   plan->chunk = chunk;
+  plan->splitsA = splitsA;
+  plan->chunkB = chunkB;
   plan->fused = fused;
   // workspace: the split partials (m, l, acc), one per split or, in-kernel,
   // one per workgroup, then the rows' arrival counters; none when one split
@@ -334,6 +362,8 @@ iak_status iak_paged_decode_plan(const iak_paged_decode_args* args, iak_paged_de
   info->splits = plan.splits;
   info->pages_per_split = plan.chunk;
   info->merge_in_kernel = plan.fused ? 1 : 0;
+  info->tail_splits = plan.splits - plan.splitsA;
+  info->tail_pages_per_split = plan.splits > plan.splitsA ? plan.chunkB : 0;
   info->workspace_bytes = plan.total;
   return IAK_OK;
 }
@@ -426,9 +456,9 @@ iak_status iak_pack_entry_records(const iak_paged_decode_args* args, void* recor
 }
 
 static iak_status paged_decode_impl(const iak_paged_decode_args* a, void* workspace, size_t workspace_bytes,
-                                    void* stream, void* ev_begin, void* ev_end) {
+                                    void* stream, void* ev_begin, void* ev_end, bool tiers = true) {
   Plan plan;
-  iak_status st = validate(a, &plan);
+  iak_status st = validate(a, &plan, tiers);
   if (st != IAK_OK) return st;
   const long long rows = (long long)a->batch * a->num_kv_heads;
   if (rows == 0) return IAK_OK;
@@ -440,7 +470,7 @@ static iak_status paged_decode_impl(const iak_paged_decode_args* a, void* worksp
   std::memset(&k, 0, sizeof(k));
   k.B = a->batch; k.Hq = a->num_q_heads; k.Hkv = a->num_kv_heads; k.G = plan.G; k.D = a->head_dim;
   k.W = a->table_width; k.NP = a->num_pages;
-  k.splits = plan.splits; k.chunk = plan.chunk;
+  k.splits = plan.splits; k.chunk = plan.chunk; k.splitsA = plan.splitsA; k.chunkB = plan.chunkB;
   k.items = (int)(rows * plan.splits);
   k.q = a->q; k.q_dtype = a->q_dtype; k.q_f32 = a->q_dtype != IAK_DTYPE_F16;
   k.qsb = a->q_stride_b; k.qsh = a->q_stride_h;
@@ -481,7 +511,7 @@ iak_status iak_paged_decode_noalloc(const iak_paged_decode_args* args, void* str
   local.merge_in_kernel = 0;
   const iak_paged_decode_args* a = &local;
   Plan plan;
-  const iak_status st = validate(a, &plan);
+  const iak_status st = validate(a, &plan, false);
   if (st != IAK_OK) return st;
   if (plan.total > IAK_NOALLOC_SCRATCH_BYTES)
     return fail(IAK_EINVAL,
@@ -497,7 +527,7 @@ iak_status iak_paged_decode_noalloc(const iak_paged_decode_args* args, void* str
     const iak_status s2 = scratch_address(dev, &ws);
     if (s2 != IAK_OK) return s2;
   }
-  return paged_decode_impl(a, ws, plan.total, stream, nullptr, nullptr);
+  return paged_decode_impl(a, ws, plan.total, stream, nullptr, nullptr, false);
 }
 
 iak_status iak_mla_decode_workspace(const iak_mla_decode_args* args, size_t* bytes) {

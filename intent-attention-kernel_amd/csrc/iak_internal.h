@@ -12,6 +12,10 @@
 #define IAK_MIN_WAVES_PER_SIMD 3
 // compute units of the MI355X / MI350X (gfx950) the split plan sizes grids for
 #define IAK_GPU_CUS 256
+// two-tier split plans: from this many waves (about 1.5 resident generations
+// of 3 waves per SIMD) the last quarter of each row goes in IAK_TIER_CHUNK-entry splits
+#define IAK_TIER_MIN_WAVES (IAK_GPU_CUS * 4 * IAK_MIN_WAVES_PER_SIMD * 3 / 2)
+#define IAK_TIER_CHUNK 32
 // pages per ring in each precision class loop (one computed, the rest in flight)
 #ifndef IAK_RING_FP16
 #define IAK_RING_FP16 2
@@ -70,6 +74,11 @@ struct KArgs {
   // entry records (iak_paged_decode_args.entry_records): [B * Hkv * W] x 32 B as two u4
   // ((native tag, page id, 0, 0), scale slots)
   const uint32_t* recs;
+
+  // two-tier plan: splits 0 .. splitsA-1 of a row take `chunk` entries each and
+  // come first in the grid (all rows); splits splitsA .. splits-1 take chunkB
+  // entries and come last. splitsA == splits: one tier.
+  int splitsA, chunkB;
 };
 
 // page descriptors from page_tags, the tag map and the scale arrays of `k`

@@ -772,12 +772,22 @@ template <typename T> __device__ __forceinline__ const T* page_at(const void* po
   return reinterpret_cast<const T*>(p < 0 ? pad_page : reinterpret_cast<const uint8_t*>(pool) + (int64_t)p * bytes);
 }
 
-// Position of work item `item`: split `item % splits` of row
-// `unit` = b * Hkv + hk, table entries [start, start + chunk).
-__device__ __forceinline__ void locate(const KArgs& a, int item, Split& sp, int& start, int& unit) {
-  unit = item / a.splits;
-  sp.split = item - unit * a.splits;
-  start = sp.split * a.chunk;
+// Position of work item `item`: split `sp.split` of row `unit` = b * Hkv + hk,
+// table entries [start, start + len). The grid holds every row's first-tier
+// splits (`chunk` entries) first, then every row's second-tier splits (chunkB
+// entries), so the short ones are the last to be dispatched.
+__device__ __forceinline__ void locate(const KArgs& a, int item, Split& sp, int& start, int& unit, int& len) {
+  // one division whichever tier (two, on branches, cost cfg4's short kernel 0.6 us)
+  item = __builtin_amdgcn_readfirstlane(item);
+  const int itemsA = a.B * a.Hkv * a.splitsA;
+  const bool tail = item >= itemsA;
+  const int j = tail ? item - itemsA : item;
+  const int per = tail ? a.splits - a.splitsA : a.splitsA;
+  len = tail ? a.chunkB : a.chunk;
+  unit = j / per;
+  const int k = j - unit * per;
+  sp.split = (tail ? a.splitsA : 0) + k;
+  start = (tail ? a.splitsA * a.chunk : 0) + k * len;
   sp.b = unit / a.Hkv;
   sp.hk = unit - sp.b * a.Hkv;
 }
@@ -858,10 +868,10 @@ void paged_decode_kernel(const KArgs a) {
   int pid, tag, lim, start, unit;
   uint32_t slot[4];
   {
-    int raw, rtag, cnt, bnd;
-    locate(a, item, sp, start, unit);
-    load_entry(a, unit, start, a.chunk, lane, raw, rtag, cnt, bnd);
-    load_tag(a, raw, rtag, cnt, bnd, start, a.chunk, lane, pid, tag, sp.n, lim);
+    int raw, rtag, cnt, bnd, len;
+    locate(a, item, sp, start, unit, len);
+    load_entry(a, unit, start, len, lane, raw, rtag, cnt, bnd);
+    load_tag(a, raw, rtag, cnt, bnd, start, len, lane, pid, tag, sp.n, lim);
   }
 
   Wave<D, QF32> w;

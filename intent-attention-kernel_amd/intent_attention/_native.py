@@ -14,7 +14,7 @@ from typing import Optional
 _HERE = os.path.dirname(os.path.abspath(__file__))
 # IAK_LIBRARY selects another build of the same ABI (e.g. a tuning variant)
 LIB_PATH = os.environ.get("IAK_LIBRARY") or os.path.join(_HERE, "libiak.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 IAK_OK, IAK_EINVAL, IAK_ENOTSUP, IAK_EHIP = 0, 1, 2, 3
 
@@ -234,7 +234,7 @@ class PlanInfo(ctypes.Structure):
     """Mirror of ``iak_paged_decode_plan_info`` (include/iak.h)."""
 
     _fields_ = [("splits", c_i32), ("pages_per_split", c_i32), ("merge_in_kernel", c_i32),
-                ("workspace_bytes", ctypes.c_size_t)]
+                ("workspace_bytes", ctypes.c_size_t), ("tail_splits", c_i32), ("tail_pages_per_split", c_i32)]
 
 
 def plan_info(args: PagedDecodeArgs) -> dict:
@@ -242,7 +242,8 @@ def plan_info(args: PagedDecodeArgs) -> dict:
     info = PlanInfo()
     check(load().iak_paged_decode_plan(ctypes.byref(args), ctypes.byref(info)))
     return {"splits": int(info.splits), "pages_per_split": int(info.pages_per_split),
-            "merge_in_kernel": bool(info.merge_in_kernel), "workspace_bytes": int(info.workspace_bytes)}
+            "merge_in_kernel": bool(info.merge_in_kernel), "workspace_bytes": int(info.workspace_bytes),
+            "tail_splits": int(info.tail_splits), "tail_pages_per_split": int(info.tail_pages_per_split)}
 
 
 def workspace_bytes(args: PagedDecodeArgs) -> int:

@@ -181,12 +181,17 @@ def test_split_plan_and_merge_form_without_gpu():
     """merge_in_kernel: 0 keeps the split count and the merge kernel; 1 rounds
     the split count up to whole workgroups of four and sizes one partial per
     workgroup plus one counter per row; 2 picks the in-kernel form only for
-    grids of IAK_MERGE_IN_KERNEL_MIN_WORKGROUPS workgroups or more."""
+    grids of IAK_MERGE_IN_KERNEL_MIN_WORKGROUPS workgroups or more. Automatic
+    plans of grids above about 1.5 resident generations of waves take two
+    tiers: the first three quarters of each row in full splits, whole fours of
+    them, the rest in 32-entry splits, whole fours too, so both merge forms
+    share the split boundaries."""
     from intent_attention import _native as N
     rows_cfg3, rows_cfg4 = (32, 8, 4, 1638), (4, 8, 4, 1229)
     a = _decode_args(N, *rows_cfg3)
+    a.pages_per_split = 63                      # an explicit split length: one tier
     p0 = N.plan_info(a)
-    assert (p0["splits"], p0["pages_per_split"], p0["merge_in_kernel"]) == (26, 63, False)
+    assert (p0["splits"], p0["pages_per_split"], p0["merge_in_kernel"], p0["tail_splits"]) == (26, 63, False, 0)
     a.merge_in_kernel = 1
     p1 = N.plan_info(a)
     assert p1["splits"] == 28 and p1["splits"] % 4 == 0 and p1["merge_in_kernel"]
@@ -196,12 +201,24 @@ def test_split_plan_and_merge_form_without_gpu():
     r256 = lambda x: (x + 255) // 256 * 256  # noqa: E731
     assert p1["workspace_bytes"] == 2 * r256(4 * slots) + r256(4 * slots * D) + r256(4 * rows)
     assert p1["workspace_bytes"] == N.workspace_bytes(a)
-    a.merge_in_kernel = 2                       # 256 rows x 7 workgroups: in-kernel
-    assert N.plan_info(a)["merge_in_kernel"]
+    # the automatic plan of the same grid: two tiers, the same for both merge forms
+    a.pages_per_split = 0
+    tiers = []
+    for m in (0, 1, 2):
+        a.merge_in_kernel = m
+        p = N.plan_info(a)
+        first = p["splits"] - p["tail_splits"]
+        assert p["pages_per_split"] == 63 and p["tail_pages_per_split"] == 32
+        assert first % 4 == 0 and p["tail_splits"] % 4 == 0
+        assert first * 63 <= 1638 * 3 // 4 and (first + 4) * 63 > 1638 * 3 // 4
+        assert first * 63 + (p["tail_splits"] - 4) * 32 < 1638 <= first * 63 + p["tail_splits"] * 32
+        assert p["workspace_bytes"] == N.workspace_bytes(a)
+        tiers.append((p["splits"], p["tail_splits"], p["merge_in_kernel"]))
+    assert tiers == [(36, 20, False), (36, 20, True), (36, 20, True)]
     b = _decode_args(N, *rows_cfg4)
-    b.merge_in_kernel = 2                       # 32 rows x 8 workgroups: the merge kernel
+    b.merge_in_kernel = 2                       # 32 rows x 8 workgroups: the merge kernel, one tier
     p4 = N.plan_info(b)
-    assert not p4["merge_in_kernel"] and p4["splits"] == 32
+    assert not p4["merge_in_kernel"] and p4["splits"] == 32 and p4["tail_splits"] == 0
     b.merge_in_kernel = 3
     with pytest.raises(ValueError, match="merge_in_kernel 3"):
         N.plan_info(b)

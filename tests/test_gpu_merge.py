@@ -198,3 +198,47 @@ def test_long_rows(dev):
         rel = err / float(np.abs(ref).max())
         _say(f"  splits {info['splits']}, max abs err {err:.2e}, relative {rel:.2e}")
         assert err <= TOL_QUANT and rel <= 1e-2
+
+
+def test_two_tier_plan(dev):
+    """A grid large enough for the automatic two-tier plan (64 rows of 4,800
+    entries: 5,120 waves): both merge forms against the oracle on two
+    sequences, and against a one-tier plan of the same split length."""
+    import torch
+    from intent_attention import _native as N
+    from intent_attention.decode_core import make_plan
+    B, Hq, Hkv, D, NP, W = 8, 32, 8, 128, 2048, 4800
+    q, pools, table, counts, tags = random_case(161, B, Hq, Hkv, D, NP, W, {"FP16": .3, "INT8": .3, "FP8": .2,
+                                                                          "INT4": .2}, q_scale=4.0)
+    counts[:] = W
+    counts[3, 5] = W - 1111
+    t = lambda x: torch.from_numpy(x).to(dev)  # noqa: E731
+    dp = to_device_pools(pools, dev)
+    sel = [0, 3]
+    ref = Dm.paged_decode_oracle(q[sel], pools, table[sel], counts[sel], tags, dtype=np.float32)
+    outs = {}
+    for merge in (True, False):
+        plan = make_plan(t(q), dp, t(table), t(counts), t(tags), out_dtype=torch.float32, merge_in_kernel=merge)
+        info = N.plan_info(plan.args)
+        _say("two-tier plan", f"merge_in_kernel={merge}", info)
+        assert info["tail_splits"] > 0 and info["merge_in_kernel"] == merge
+        plan.run()
+        torch.cuda.synchronize()
+        got = plan.out.cpu().numpy()
+        err = float(np.abs(got[sel] - ref).max())
+        rel = err / float(np.abs(ref).max())
+        _say(f"  vs oracle: max abs err {err:.2e}, relative {rel:.2e}")
+        assert err <= TOL_QUANT and rel <= 1e-2
+        outs[merge] = got
+    one = make_plan(t(q), dp, t(table), t(counts), t(tags), out_dtype=torch.float32, merge_in_kernel=False,
+                    pages_per_split=info["pages_per_split"])
+    assert N.plan_info(one.args)["tail_splits"] == 0
+    one.run()
+    torch.cuda.synchronize()
+    base = one.out.cpu().numpy()
+    scale = float(np.abs(base).max())
+    for merge, got in outs.items():
+        d = float(np.abs(got - base).max())
+        _say(f"  merge_in_kernel={merge} vs one tier: {d:.2e} (max |out| {scale:.2e})")
+        assert d <= 1e-3 * scale
+    assert float(np.abs(outs[True] - outs[False]).max()) <= 1e-5 * scale

@@ -103,9 +103,15 @@ def test_full_config_sampled_rows(name, tol):
     for mult in mults:
         wl["q"] = (q0.float() * mult).half() if mult != 1.0 else q0
         out = torch.empty((cfg["B"], cfg["Hq"], cfg["D"]), dtype=torch.float32, device=dev)
-        make_plan(wl["q"], wl["pools"], wl["table"], wl["counts"], wl["tags"], out=out).run()
+        plan0 = make_plan(wl["q"], wl["pools"], wl["table"], wl["counts"], wl["tags"], out=out)
+        plan0.run()
         torch.cuda.synchronize()
         if mult == 1.0:
+            from intent_attention import _native as N
+            info = N.plan_info(plan0.args)
+            print(f"[gpu-case] {name} plan {info}", flush=True)
+            if name == "cfg3":   # the grid the two-tier plan is for
+                assert info["tail_splits"] > 0
             for form in ("page descriptors", "entry records"):
                 alt = torch.full_like(out, float("nan"))
                 plan = make_plan(wl["q"], wl["pools"], wl["table"], wl["counts"], wl["tags"], out=alt)
