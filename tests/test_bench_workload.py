@@ -56,3 +56,19 @@ def test_bench_refuses_more_than_one_gpu(monkeypatch, capsys):
     with pytest.raises(SystemExit) as e:
         bench.main()
     assert e.value.code == 2 and "one GPU" in capsys.readouterr().err
+
+
+def test_measured_traffic_is_tied_to_the_kernel_sources(monkeypatch):
+    """roofline.traffic comes from counter runs of one build of the decode
+    kernel: reported while the kernel's sources hash to the digest it was
+    measured on, null (with the reason) for any other sources."""
+    digest = bench.kernel_source_digest()
+    assert len(digest) == 16
+    for key, m in bench.MEASURED_TRAFFIC.items():
+        assert m["src"] == digest, f"{key}: measured on {m['src']}, sources are {digest}"
+        got, src = bench.measured_traffic(key)
+        assert got == m["bytes"] and src == m["source"]
+    monkeypatch.setattr(bench, "kernel_source_digest", lambda: "0" * 16)
+    got, why = bench.measured_traffic("cfg3")
+    assert got is None and "stale" in why
+    assert bench.measured_traffic("cfg2") == (None, None)

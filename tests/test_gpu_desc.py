@@ -246,3 +246,33 @@ def test_descriptor_precision_without_pools_is_skipped(dev):
     tags_skip = np.where(tags == Dm.INT4, Dm.SKIP, tags).astype(np.int32)
     ref = Dm.paged_decode_oracle(q.astype(np.float32), pools, table, counts, tags_skip)
     assert float(np.abs(got.out.cpu().numpy() - ref).max()) <= TOL_QUANT
+
+
+def test_records_plan_graph_replays(dev):
+    """A plan reading entry records, captured in a HIP graph (in-kernel merge):
+    three replays, with eager work between them, equal the eager call."""
+    import torch
+    from intent_attention.decode_core import make_plan
+    q, pools, table, counts, tags = _case(231, 2, 16, 4, 128, 128, 90)
+    t = lambda x: torch.from_numpy(x).to(dev)  # noqa: E731
+    dp = to_device_pools(pools, dev)
+    plan = make_plan(t(q), dp, t(table), t(counts), t(tags), out_dtype=torch.float32, pages_per_split=8,
+                     merge_in_kernel=True)
+    plan.pack_records()
+    plan.run()
+    torch.cuda.synchronize()
+    want = plan.out.clone()
+    s = torch.cuda.Stream(dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            plan.run()
+    torch.cuda.current_stream(dev).wait_stream(s)
+    torch.cuda.synchronize()
+    for i in range(3):
+        plan.out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(plan.out, want), i
