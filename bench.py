@@ -1038,6 +1038,58 @@ def main() -> None:
     run_decode(args, cpu)
 
 
+def metadata_variants(plans, steps: int, stream, job_bytes: int, config: str) -> dict:
+    """The same steps on the same plans reading the optional packed metadata:
+    entry records (packed once per page table) and page descriptors (packed
+    once for the pools), each timed twice, alternating with the other (the
+    mean of the two passes is reported). `value` is the job's reference-format bytes over
+    the step time, as on the headline line; the plans return to the reference
+    tensors afterwards."""
+    def timed(k):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for i in range(min(k, 10)):
+            plans[i % len(plans)].run()
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for i in range(k):
+            plans[i % len(plans)].run()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / k
+
+    def pack_timed(fn, *arg):
+        fn(*arg)   # the first launch of a pack kernel also loads its code
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        fn(*arg)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3
+
+    recs = [torch.empty(p._records_shape(), dtype=torch.int32, device=p.device) for p in plans]
+    desc = torch.empty((int(plans[0].args.num_pages), 8), dtype=torch.int32, device=plans[0].device)
+    rec_pack = [pack_timed(p.pack_records, r) for p, r in zip(plans, recs)]
+    desc_pack = pack_timed(plans[0].pack_descriptors, desc)
+
+    def use(form):
+        for p, r in zip(plans, recs):
+            p.use_records(r if form == "records" else None)
+            p.use_descriptors(desc if form == "desc" else None)
+
+    best = {"records": 0.0, "desc": 0.0}
+    for form in ("records", "desc", "records", "desc"):
+        use(form)
+        best[form] += timed(steps) / 2
+    use(None)
+    out = {}
+    for form, key, extra in (("records", "entry_records", {"pack_us_per_table": round(sum(rec_pack) / len(rec_pack), 2)}),
+                             ("desc", "page_descriptors", {"pack_us": round(desc_pack, 2)})):
+        ms = best[form]
+        out[key] = {"us_per_step": round(ms * 1e3, 2), "value": round(job_bytes / (ms * 1e-3) / 1e9, 1), "unit": "GB/s",
+                    **extra, "traffic": measured_traffic(config + ("-records" if form == "records" else "-desc"))[0]}
+    return out
+
+
 def run_decode(args, cpu=None) -> None:
     from intent_attention.decode_core import make_plan
     dev = torch.device("cuda:0")
@@ -1163,6 +1215,8 @@ def run_decode(args, cpu=None) -> None:
     }
     if traffic_key in MEASURED_TRAFFIC:
         res["roofline"]["traffic_source"] = measured_traffic(traffic_key)[1]
+    if not (args.page_descriptors or args.entry_records or args.calibrate_copy) and args.config in MEASURED_TRAFFIC:
+        res["variants"] = metadata_variants(plans, args.steps, stream, ab["total"], args.config)
     if args.calibrate_copy:
         n = args.calibrate_copy * (1 << 20)
         src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
