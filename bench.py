@@ -1226,6 +1226,15 @@ def run_decode(args, cpu=None) -> None:
             dst.copy_(src)
         torch.cuda.synchronize()
         res["copy_calibration_bytes"] = n
+        # the same copy timed: this GPU's read + write streaming rate, the
+        # ceiling of kernels that stream as much as they read
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(5):
+            dst.copy_(src)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        res["copy_read_write_gbps"] = round(2 * n / (e0.elapsed_time(e1) / 5 * 1e-3) / 1e9, 1)
     if cpu is not None:
         rows = cfg["B"] * cfg["Hkv"]
         res["cpu_baseline"] = cpu_baseline_decode(args.config, cpu, ab["total"], rows)
