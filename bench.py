@@ -281,19 +281,19 @@ def build_workload(name: str, device: torch.device, seed: int = 1234, chunk_page
 # decode kernel's sources it was measured on (kernel_source_digest); a build whose
 # sources differ reports traffic null (stale) until the counters are run again.
 MEASURED_TRAFFIC = {
-    "cfg3": {"bytes": 2_106_643_648 + 5_652_480, "src": "66c69d5924f89613",
+    "cfg3": {"bytes": 2_105_547_836 + 5_054_464, "src": "5e2a85410d072d75",
              "source": "profiles/paged_decode_cfg3_hbm_traffic.txt"},
-    "cfg4": {"bytes": 189_788_128 + 2_129_920, "src": "66c69d5924f89613",
+    "cfg4": {"bytes": 189_786_563 + 2_129_920, "src": "5e2a85410d072d75",
              "source": "profiles/paged_decode_cfg4_kernel_stats.txt"},
     # the same decodes reading 32-byte page descriptors (--page-descriptors) or
     # 32-byte entry records (--entry-records)
-    "cfg3-desc": {"bytes": 2_077_047_648 + 5_652_480, "src": "66c69d5924f89613",
+    "cfg3-desc": {"bytes": 2_079_972_170 + 5_054_464, "src": "5e2a85410d072d75",
                   "source": "profiles/paged_decode_cfg3_hbm_traffic.txt"},
-    "cfg4-desc": {"bytes": 182_750_378 + 2_129_920, "src": "66c69d5924f89613",
+    "cfg4-desc": {"bytes": 182_752_140 + 2_129_920, "src": "5e2a85410d072d75",
                   "source": "profiles/paged_decode_cfg4_kernel_stats.txt"},
-    "cfg3-records": {"bytes": 2_005_636_531 + 5_652_480, "src": "66c69d5924f89613",
+    "cfg3-records": {"bytes": 2_005_700_033 + 5_054_464, "src": "5e2a85410d072d75",
                      "source": "profiles/paged_decode_cfg3_hbm_traffic.txt"},
-    "cfg4-records": {"bytes": 178_930_607 + 2_129_923, "src": "66c69d5924f89613",
+    "cfg4-records": {"bytes": 178_931_777 + 2_129_923, "src": "5e2a85410d072d75",
                      "source": "profiles/paged_decode_cfg4_kernel_stats.txt"},
 }
 KERNEL_SOURCES = ("paged_decode.hip", "iak_device.h", "iak_internal.h")
@@ -984,6 +984,8 @@ def main() -> None:
                     help="decode legs: pack 32-byte entry records once per page table (timed apart) and decode "
                          "from them instead of the table, tag and scale arrays; `value` keeps the reference "
                          "format's bytes")
+    ap.add_argument("--no-variants", action="store_true",
+                    help="cfg3 / cfg4: skip the packed-metadata passes after the headline ones (profiling runs)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="after the timed steps, run a plain device copy of MIB MiB (read + write "
                          "MIB MiB each): the reference point that scales rocprof FETCH_SIZE/WRITE_SIZE")
@@ -1215,7 +1217,8 @@ def run_decode(args, cpu=None) -> None:
     }
     if traffic_key in MEASURED_TRAFFIC:
         res["roofline"]["traffic_source"] = measured_traffic(traffic_key)[1]
-    if not (args.page_descriptors or args.entry_records or args.calibrate_copy) and args.config in MEASURED_TRAFFIC:
+    plain = not (args.page_descriptors or args.entry_records or args.calibrate_copy or args.no_variants)
+    if plain and args.config in MEASURED_TRAFFIC:
         res["variants"] = metadata_variants(plans, args.steps, stream, ab["total"], args.config)
     if args.calibrate_copy:
         n = args.calibrate_copy * (1 << 20)

@@ -150,22 +150,25 @@ iak_status validate(const iak_paged_decode_args* a, Plan* plan, bool tiers = tru
   if (splits < 1) splits = 1;
   // Two tiers on grids of more than about 1.5 resident generations of waves
   // (automatic plans): the first three quarters of each row's entries in splits
-  // of `chunk` entries, the rest in 32-entry splits placed after every row's
-  // first tier in the grid. Of the waves sharing a CU the oldest are served
-  // first (a wave-timeline probe: at cfg3 the older workgroup of a CU takes
-  // 95 us per split, the younger 163 us, with the same bytes), so the grid's
-  // last workgroups are the slowest; short ones there shorten the tail (cfg3
-  // 326.3-327.7 -> 321.7-322.0 us per step). Both tiers hold whole fours of
-  // splits, so a workgroup's four waves stay in one tier and one row whichever
-  // merge form runs.
+  // of `chunk` entries, the rest in splits of about IAK_TIER_CHUNK entries
+  // (evened over a multiple of four splits) placed after every row's first tier
+  // in the grid. Of the waves sharing a CU the oldest are served first (a
+  // wave-timeline probe: at cfg3 the older workgroup of a CU takes 95 us per
+  // split, the younger 163 us, with the same bytes), so the grid's last
+  // workgroups are the slowest; short ones there shorten the tail (cfg3
+  // 326.3-327.7 -> 314.1-314.9 us per step with 16 tail splits of 40; tails of
+  // 24 / 32 / 44 / 48 entries measured 326.9 / 319.5-320.9 / 318.8 / 322-323).
+  // Both tiers hold whole fours of splits, so a workgroup's four waves stay in
+  // one tier and one row whichever merge form runs.
   int splitsA = splits, chunkB = chunk;
   if (tiers && a->pages_per_split == 0 && rows * (long long)splits > IAK_TIER_MIN_WAVES) {
     const int sa = (int)((long long)W * 3 / 4 / chunk) / 4 * 4;
     const int tail = W - sa * chunk;
     if (sa >= 4 && tail > 0) {
+      const int sb = ((tail + IAK_TIER_CHUNK - 1) / IAK_TIER_CHUNK + 3) / 4 * 4;
       splitsA = sa;
-      chunkB = IAK_TIER_CHUNK;
-      splits = sa + ((tail + IAK_TIER_CHUNK - 1) / IAK_TIER_CHUNK + 3) / 4 * 4;
+      chunkB = (tail + sb - 1) / sb;
+      splits = sa + sb;
     }
   }
   // in-kernel merge: a workgroup's four waves take four splits of one row, so

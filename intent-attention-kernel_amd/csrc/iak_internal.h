@@ -13,9 +13,10 @@
 // compute units of the MI355X / MI350X (gfx950) the split plan sizes grids for
 #define IAK_GPU_CUS 256
 // two-tier split plans: from this many waves (about 1.5 resident generations
-// of 3 waves per SIMD) the last quarter of each row goes in IAK_TIER_CHUNK-entry splits
+// of 3 waves per SIMD) the last quarter of each row goes in splits of about
+// IAK_TIER_CHUNK entries
 #define IAK_TIER_MIN_WAVES (IAK_GPU_CUS * 4 * IAK_MIN_WAVES_PER_SIMD * 3 / 2)
-#define IAK_TIER_CHUNK 32
+#define IAK_TIER_CHUNK 40
 // pages per ring in each precision class loop (one computed, the rest in flight)
 #ifndef IAK_RING_FP16
 #define IAK_RING_FP16 2

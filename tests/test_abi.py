@@ -184,8 +184,8 @@ def test_split_plan_and_merge_form_without_gpu():
     grids of IAK_MERGE_IN_KERNEL_MIN_WORKGROUPS workgroups or more. Automatic
     plans of grids above about 1.5 resident generations of waves take two
     tiers: the first three quarters of each row in full splits, whole fours of
-    them, the rest in 32-entry splits, whole fours too, so both merge forms
-    share the split boundaries."""
+    them, the rest in splits of about 40 entries, evened over a multiple of four
+    splits, so both merge forms share the split boundaries."""
     from intent_attention import _native as N
     rows_cfg3, rows_cfg4 = (32, 8, 4, 1638), (4, 8, 4, 1229)
     a = _decode_args(N, *rows_cfg3)
@@ -208,13 +208,15 @@ def test_split_plan_and_merge_form_without_gpu():
         a.merge_in_kernel = m
         p = N.plan_info(a)
         first = p["splits"] - p["tail_splits"]
-        assert p["pages_per_split"] == 63 and p["tail_pages_per_split"] == 32
+        tb = p["tail_pages_per_split"]
+        assert p["pages_per_split"] == 63 and 0 < tb <= 40
         assert first % 4 == 0 and p["tail_splits"] % 4 == 0
         assert first * 63 <= 1638 * 3 // 4 and (first + 4) * 63 > 1638 * 3 // 4
-        assert first * 63 + (p["tail_splits"] - 4) * 32 < 1638 <= first * 63 + p["tail_splits"] * 32
+        assert first * 63 + (p["tail_splits"] - 1) * tb < 1638 <= first * 63 + p["tail_splits"] * tb
         assert p["workspace_bytes"] == N.workspace_bytes(a)
         tiers.append((p["splits"], p["tail_splits"], p["merge_in_kernel"]))
-    assert tiers == [(36, 20, False), (36, 20, True), (36, 20, True)]
+    assert tiers == [(32, 16, False), (32, 16, True), (32, 16, True)]
+    assert p["tail_pages_per_split"] == 40
     b = _decode_args(N, *rows_cfg4)
     b.merge_in_kernel = 2                       # 32 rows x 8 workgroups: the merge kernel, one tier
     p4 = N.plan_info(b)
