@@ -290,7 +290,7 @@ typedef struct {
   const void* c_fp8_scale; const void* c_int8_scale; int32_t scale_dtype;   /* [num_pages] */
 
   float sm_scale;
-  int32_t pages_per_split;     /* 0 = automatic, else 1 .. 64 */
+  int32_t pages_per_split;     /* 0 = automatic, else 1 .. 128 */
 } iak_mla_decode_args;
 
 /* Bytes of device workspace iak_mla_decode needs (0 when one split covers a sequence). */

@@ -232,8 +232,8 @@ iak_status validate_mla(const iak_mla_decode_args* a, MPlan* plan) {
   if (a->q_dtype < 0 || a->q_dtype > 2 || a->out_dtype < 0 || a->out_dtype > 2)
     return fail(IAK_EINVAL, "bad q/out dtype (%d, %d)", a->q_dtype, a->out_dtype);
   if (!std::isfinite(a->sm_scale)) return fail(IAK_EINVAL, "sm_scale is not finite");
-  if (a->pages_per_split < 0 || a->pages_per_split > 64)
-    return fail(IAK_EINVAL, "pages_per_split %d outside [0, 64]", a->pages_per_split);
+  if (a->pages_per_split < 0 || a->pages_per_split > 128)
+    return fail(IAK_EINVAL, "pages_per_split %d outside [0, 128]", a->pages_per_split);
   if (a->scale_dtype != IAK_DTYPE_F16 && a->scale_dtype != IAK_DTYPE_F32)
     return fail(IAK_EINVAL, "scale dtype %d must be f16 or f32", a->scale_dtype);
   if (a->batch > 0) {
@@ -269,7 +269,7 @@ iak_status validate_mla(const iak_mla_decode_args* a, MPlan* plan) {
     const long long units = (long long)a->batch * HG;
     const long long want = units > 0 ? (256 + units - 1) / units : 1;
     chunk = (int)((W + want - 1) / (want > 0 ? want : 1));
-    if (chunk > 64) chunk = 64;
+    if (chunk > 128) chunk = 128;
     if (chunk < 1) chunk = 1;
   }
   int splits = (W + chunk - 1) / chunk;

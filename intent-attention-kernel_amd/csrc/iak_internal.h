@@ -97,7 +97,7 @@ struct MArgs {
   int B, H, DQK, DV, VOFF, W;
   int64_t NP;
   int splits;   // splits per sequence
-  int chunk;    // table entries per split (<= 64)
+  int chunk;    // table entries per split (<= 128)
   int HG;       // groups of 128 heads
 
   const void* q; int q_dtype; int64_t qsb, qsh;

@@ -10,7 +10,7 @@
 //
 // Work decomposition
 //   One workgroup of 8 waves (two per SIMD, up to 256 registers each) reduces
-//   one split -- up to 64 consecutive page-table entries of one sequence -- for
+//   one split -- up to 128 consecutive page-table entries of one sequence -- for
 //   128 heads, so each latent page is read from HBM once per sequence. A step
 //   is a pair of pages (32 tokens). Pages stream from HBM straight into an LDS
 //   ring of page pairs (global_load_lds), SLOTS - 1 steps ahead, and each pair
@@ -83,7 +83,7 @@ template <int DQK, int DV, bool WIDE> struct MlaShared {
   float mmax[C::HEADS];                             // final maxima
 };
 
-// Page metadata of one split: lane i holds entry i.
+// Page metadata of one split entry (lane i holds entries i and i + 64).
 struct MlaPages {
   int pid, tag;
   float scale;
@@ -91,14 +91,14 @@ struct MlaPages {
 
 // Entries past the row's count, invalid ids, SKIP pages and pages whose first
 // token lies at or past the sequence's token bound are left out (pid -1).
-__device__ __forceinline__ MlaPages mla_page_meta(const MArgs& a, int b, int start, int lane, int limit) {
+__device__ __forceinline__ MlaPages mla_page_meta(const MArgs& a, int b, int start, int e, int limit) {
   MlaPages m{-1, IAK_TAG_SKIP, 1.0f};
   int raw = -1;
-  if (lane < a.chunk && start + lane < a.W) raw = a.table[(int64_t)b * a.W + start + lane];
+  if (e < a.chunk && start + e < a.W) raw = a.table[(int64_t)b * a.W + start + e];
   int cnt = a.counts[b];
   cnt = cnt < 0 ? 0 : (cnt > a.W ? a.W : cnt);
   int n = cnt - start < a.chunk ? cnt - start : a.chunk;
-  if (lane < n && (int64_t)(start + lane) * PS < limit) {
+  if (e < n && (int64_t)(start + e) * PS < limit) {
     int p = raw;
     if (a.neg_wrap && p < 0 && (int64_t)p >= -a.NP) p = (int)((int64_t)p + a.NP);
     if (p >= 0 && (int64_t)p < a.NP) {
@@ -141,7 +141,10 @@ __device__ __forceinline__ void mla_dma_page(uint8_t* slot, const MArgs& a, int 
     ch = ch < nch ? ch : nch - 1;
     const uint8_t* src = base + (int64_t)ch * 1024 + 16 * lane;
     const uint32_t dst = (uint32_t)(uintptr_t)(lds_u8*)(slot + ch * 1024);
-    asm volatile("global_load_lds_dwordx4 %0, off" : : "v"(src), "{m0}"(dst) : "memory");
+    // the copy takes its LDS address from M0, which the compiler writes just
+    // before this statement: one wait state between an SALU write of M0 and an
+    // LDS DMA that reads it
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "{m0}"(dst) : "memory");
   }
 }
 
@@ -196,12 +199,14 @@ __device__ __forceinline__ void mla_stage_pair(MlaShared<DQK, DV, WIDE>& sh, int
 // each 16-lane group names row `row0 + i / 4`, columns col0 + 4 (i % 4) .. +3;
 // lane j receives column col0 + j of rows row0 .. row0 + 3 (ds_read_b64_tr_b16:
 // element m of lane j comes from lane 4m + j / 4 of its group, element j % 4).
+// `lane_off` is the lane's part of the address, (i / 4) rows + 4 (i % 4)
+// columns, computed once per kernel; `off` (row0 rows + col0 columns, and the
+// buffer) is uniform, so each read is one add or an immediate offset.
 template <int DQK, int DV, bool WIDE>
-__device__ __forceinline__ h4 mla_read_column(const MlaShared<DQK, DV, WIDE>& sh, int buf, int row0, int col0,
-                                              int c) {
+__device__ __forceinline__ h4 mla_read_column(const MlaShared<DQK, DV, WIDE>& sh, int lane_off, int off) {
   typedef short s4 __attribute__((ext_vector_type(4)));
   typedef __attribute__((address_space(3))) s4 lds_s4;
-  const _Float16* p = &sh.t1[buf][row0 + (c >> 2)][col0 + 4 * (c & 3)];
+  const _Float16* p = &sh.t1[0][0][0] + off + lane_off;
   const s4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p));
   return __builtin_bit_cast(h4, v);
 }
@@ -218,12 +223,17 @@ __global__ __launch_bounds__(512, 1) void mla_decode_kernel(const MArgs a) {
   const int hg = blockIdx.y;
   const int start = split * a.chunk;
   const int head = hg * C::HEADS + 16 * w + c;   // this lane's score / P head
+  // the lane's part of a value-operand read: rows 4g + c / 4, columns 4 (c % 4)
+  const int vlane = (4 * g + (c >> 2)) * C::T1 + 4 * (c & 3);
 
   // token bound of the sequence (table entry e holds tokens 16e .. 16e+15)
   const int limit = a.valid ? __builtin_amdgcn_readfirstlane(a.valid[b]) : 0x7FFFFFFF;
+  // entries lane and lane + 64 of the split (up to 128 entries)
   const MlaPages meta = mla_page_meta(a, b, start, lane, limit);
+  const MlaPages meta2 = mla_page_meta(a, b, start, lane + 64, limit);
   const uint64_t mask = __builtin_amdgcn_ballot_w64(meta.pid >= 0);
-  const int np = __builtin_popcountll(mask);
+  const uint64_t mask2 = __builtin_amdgcn_ballot_w64(meta2.pid >= 0);
+  const int np = __builtin_popcountll(mask) + __builtin_popcountll(mask2);
 
   // Q of the lane's head, rounded to f16: dims 32i + 8g .. +7 (B operand of the scores)
   h8 q[C::KSTEPS];
@@ -264,18 +274,26 @@ __global__ __launch_bounds__(512, 1) void mla_decode_kernel(const MArgs a) {
 
   if (np > 0) {
     const int nsteps = (np + 1) >> 1;
-    // page cursor: lanes of the pages in table order; past the end the last
-    // page is named again (copies stay unconditional, compute is masked)
-    uint64_t rem = mask;
-    int last = __builtin_ctzll(mask);
+    // page cursor: entry indexes (0 .. 127) of the pages in table order; past
+    // the end the last page is named again (copies stay unconditional,
+    // compute is masked)
+    uint64_t rem = mask, rem2 = mask2;
+    int last = mask ? __builtin_ctzll(mask) : 64 + __builtin_ctzll(mask2);
     auto next_page = [&]() {
       if (rem) last = take(rem);
+      else if (rem2) last = 64 + take(rem2);
       return last;
     };
-    auto page_pid = [&](int idx) { return __builtin_amdgcn_readlane(meta.pid, idx); };
-    auto page_tag = [&](int idx) { return __builtin_amdgcn_readlane(meta.tag, idx); };
+    // entry idx's field: lane idx of the first or lane idx - 64 of the second half
+    auto pick = [&](int v, int v2, int idx) {
+      const int x = __builtin_amdgcn_readlane(v, idx & 63), x2 = __builtin_amdgcn_readlane(v2, idx & 63);
+      return idx >= 64 ? x2 : x;
+    };
+    auto page_pid = [&](int idx) { return pick(meta.pid, meta2.pid, idx); };
+    auto page_tag = [&](int idx) { return pick(meta.tag, meta2.tag, idx); };
     auto page_scale = [&](int idx) {
-      return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, meta.scale), idx));
+      return __builtin_bit_cast(
+          float, pick(__builtin_bit_cast(int, meta.scale), __builtin_bit_cast(int, meta2.scale), idx));
     };
     // pq[2k], pq[2k+1]: lanes of the pages of step s+k (ring slot (s+k) % SLOTS)
     int pq[2 * C::SLOTS];
@@ -401,9 +419,9 @@ __global__ __launch_bounds__(512, 1) void mla_decode_kernel(const MArgs a) {
         constexpr int PFV = C::PF_VALUE;
         h8 bq[PFV];
         auto rd = [&](int db) {
-          const int col = a.VOFF + 16 * db;
-          const h4 b0 = mla_read_column<DQK, DV, WIDE>(sh, R, 4 * g, col, c);
-          const h4 b1 = mla_read_column<DQK, DV, WIDE>(sh, R, PS + 4 * g, col, c);
+          const int off = (R * C::TOK) * C::T1 + a.VOFF + 16 * db;
+          const h4 b0 = mla_read_column<DQK, DV, WIDE>(sh, vlane, off);
+          const h4 b1 = mla_read_column<DQK, DV, WIDE>(sh, vlane, off + PS * C::T1);
           return __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
         };
 #pragma unroll

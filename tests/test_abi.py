@@ -117,6 +117,37 @@ def test_mla_validation_errors_without_gpu():
     assert n > 0 and n % 256 == 0
 
 
+def test_mla_long_split_plan_without_gpu():
+    """MLA splits hold up to 128 table entries (a lane takes entries i and
+    i + 64): pages_per_split 128 is accepted, 129 is not, and the automatic plan
+    of 32 sequences x 1,300 entries (256 workgroups wanted, 8 per sequence)
+    takes 11 splits of 128 -- with one entry per lane it would take 21 of 64.
+    Read through the workspace size: (2 + v_dim) floats per (sequence, split,
+    head), each array rounded up to 256 bytes."""
+    from intent_attention import _native as N
+    a = N.MlaDecodeArgs()
+    a.batch, a.num_heads, a.qk_dim, a.v_dim, a.page_size = 32, 40, 576, 512, 16
+    a.table_width, a.num_pages, a.sm_scale = 1300, 4096, 0.04
+    a.q = a.out = a.page_table = a.page_counts = a.page_tags = a.c_fp8 = a.c_fp8_scale = 16
+    for i in range(8):
+        a.tag_map[i] = N.TAG_SKIP
+    a.tag_map[0] = N.TAG_FP8
+
+    def ws(splits):
+        r = lambda x: (x + 255) // 256 * 256
+        slots = a.batch * splits * a.num_heads
+        return 2 * r(4 * slots) + r(4 * slots * a.v_dim)
+
+    assert N.mla_workspace_bytes(a) == ws(11)
+    a.pages_per_split = 128
+    assert N.mla_workspace_bytes(a) == ws(11)
+    a.pages_per_split = 64
+    assert N.mla_workspace_bytes(a) == ws(21)
+    a.pages_per_split = 129
+    with pytest.raises(ValueError, match="outside"):
+        N.mla_workspace_bytes(a)
+
+
 def test_quantize_validation_errors_without_gpu():
     from intent_attention import _native as N
     a = N.QuantizeArgs()

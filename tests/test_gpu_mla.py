@@ -86,6 +86,38 @@ def test_mla_matches_oracle(dev, dqk, dv, voff, pps):
     assert err <= 1e-2, f"max abs err {err:.3e}"
 
 
+@pytest.mark.parametrize("pps", [128, 100, 65, 0])
+@pytest.mark.parametrize("wide", [False, True])
+def test_mla_long_splits(dev, pps, wide):
+    """Splits of more than 64 table entries (a lane holds entries i and i + 64
+    of its split): 150-entry tables in splits of 128 / 100 / 65 entries, one
+    sequence whose count ends inside the second half of its first split, one
+    with a ragged token bound there, and the automatic plan on a table wide
+    enough (32 sequences x 1,300 entries: 11 splits of 128) for it to take
+    more than 64 per split.
+    FP8 / INT8 pages only and with FP16 pages as well (the two ring widths)."""
+    import torch
+    from intent_attention import mla_paged_decode
+    W = 1300 if pps == 0 else 150
+    _say("mla long splits", f"pages_per_split={pps} W={W} fp16={wide}")
+    mix = {"FP16": .3, "FP8": .3, "INT8": .3, "SKIP": .1} if wide else {"FP8": .45, "INT8": .45, "SKIP": .1}
+    q, pools, table, counts, tags = _latent_case(3000 + pps + wide, 3 if pps else 32, 40, 576, 700, W, mix)
+    counts[0] = W
+    if pps:
+        counts[1] = 97                          # ends in the second half of split 0
+    valid = (counts * 16).astype(np.int32)
+    valid[-1] = 16 * 80 + 5                     # token bound inside entry 80
+    got = mla_paged_decode(torch.from_numpy(q).to(dev), _device_pools(pools, dev), torch.from_numpy(table).to(dev),
+                           torch.from_numpy(counts).to(dev), torch.from_numpy(tags).to(dev), v_dim=512,
+                           valid_tokens=torch.from_numpy(valid).to(dev), pages_per_split=pps,
+                           out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    ref = M.mla_paged_decode_oracle(q, pools, table, counts, tags, v_dim=512, valid_tokens=valid)
+    err = np.abs(got.cpu().numpy() - ref).max()
+    _say(f"  max abs err {err:.2e}")
+    assert err <= 1e-2, f"max abs err {err:.3e}"
+
+
 @pytest.mark.parametrize("lat_scale", [1e-3, 3e-4, 300.0])
 @pytest.mark.parametrize("pps", [0, 9])
 def test_mla_small_and_large_latent_magnitudes(dev, lat_scale, pps):
