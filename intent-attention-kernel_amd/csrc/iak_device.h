@@ -280,6 +280,37 @@ __global__ __launch_bounds__(256) void splitk_merge_kernel(const KArgs a) {
   if (!live) return;
   const float inv = L > 0.f ? 1.0f / L : 0.f;
   const int64_t base = (int64_t)b * a.osb + (int64_t)h * a.osh + PER * lane;
+  // 16-bit outputs whose rows keep the lane's PER values aligned go out as one
+  // store per lane (PER halves packed), the rest element by element
+  const int esz = a.out_dtype == IAK_DTYPE_F32 ? 4 : 2;
+  const bool packed = esz == 2 && PER % 2 == 0 && a.osb % PER == 0 && a.osh % PER == 0 &&
+                      (reinterpret_cast<uintptr_t>(a.out) % (2 * PER)) == 0;
+  if (packed) {
+    uint32_t wds[PER / 2 > 0 ? PER / 2 : 1];
+#pragma unroll
+    for (int j = 0; j < PER / 2; ++j) {
+      const float v0 = o[2 * j] * inv, v1 = o[2 * j + 1] * inv;
+      if (a.out_dtype == IAK_DTYPE_F16) {
+        wds[j] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v0) |
+                 ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v1) << 16);
+      } else {
+        wds[j] = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)v0) |
+                 ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)v1) << 16);
+      }
+    }
+    uint16_t* op = reinterpret_cast<uint16_t*>(a.out) + base;
+    if constexpr (PER == 8) {
+      *reinterpret_cast<u4*>(op) = u4{wds[0], wds[1], wds[2], wds[3]};
+    } else if constexpr (PER == 4) {
+      *reinterpret_cast<u2*>(op) = u2{wds[0], wds[1]};
+    } else if constexpr (PER == 2) {
+      *reinterpret_cast<uint32_t*>(op) = wds[0];
+    } else {
+#pragma unroll
+      for (int j = 0; j < PER / 2; ++j) reinterpret_cast<uint32_t*>(op)[j] = wds[j];
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const float v = o[j] * inv;
