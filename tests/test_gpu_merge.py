@@ -242,3 +242,56 @@ def test_two_tier_plan(dev):
         _say(f"  merge_in_kernel={merge} vs one tier: {d:.2e} (max |out| {scale:.2e})")
         assert d <= 1e-3 * scale
     assert float(np.abs(outs[True] - outs[False]).max()) <= 1e-5 * scale
+
+
+@pytest.mark.parametrize("out_name", ["float16", "bfloat16"])
+@pytest.mark.parametrize("D", [64, 128])
+def test_merge_kernel_packed_and_element_stores_agree(dev, out_name, D):
+    """The merge kernel writes a 16-bit output row as one packed store per lane
+    when the output keeps the lane's values aligned, else element by element.
+    The same call into an aligned output and into a view one element off (so
+    every row is misaligned) gives bit-identical values."""
+    import torch
+    from intent_attention.decode_core import make_plan
+    od = getattr(torch, out_name)
+    _say("merge stores", f"D={D} out={out_name}")
+    B, Hq, Hkv = 2, 8, 2
+    q, pools, table, counts, tags = random_case(740 + D, B, Hq, Hkv, D, 300, 90, MIX, outliers=0.01)
+    t = lambda x: torch.from_numpy(x).to(dev)  # noqa: E731
+    dp = to_device_pools(pools, dev)
+    big = torch.full((B * Hq * D + 1,), float("nan"), dtype=od, device=dev)
+    views = {"aligned": big[:B * Hq * D].view(B, Hq, D), "offset": big[1:].view(B, Hq, D)}
+    got = {}
+    for name, out in views.items():
+        plan = make_plan(t(q), dp, t(table), t(counts), t(tags), out=out, merge_in_kernel=False, pages_per_split=8)
+        assert plan.args.out % 4 == (0 if name == "aligned" else 2)
+        plan.run()
+        torch.cuda.synchronize()
+        got[name] = out.float().cpu().numpy().copy()
+    assert np.isfinite(got["aligned"]).all()
+    assert np.array_equal(got["aligned"], got["offset"])
+
+
+@pytest.mark.parametrize("out_name", ["float16", "bfloat16"])
+def test_mla_merge_packed_and_element_stores_agree(dev, out_name):
+    """As above for the MLA decode's merge (512 value dims, eight per lane)."""
+    import torch
+    sys.path.insert(0, __import__("os").path.dirname(__file__))
+    from test_gpu_mla import _latent_case, _device_pools
+    from intent_attention.mla_core import make_mla_plan
+    od = getattr(torch, out_name)
+    _say("mla merge stores", f"out={out_name}")
+    q, pools, table, counts, tags = _latent_case(77, 2, 20, 576, 200, 140, {"FP8": .45, "INT8": .45, "SKIP": .1})
+    B, H = 2, 20
+    big = torch.full((B * H * 512 + 8,), float("nan"), dtype=od, device=dev)
+    views = {"aligned": big[:B * H * 512].view(B, H, 512), "offset": big[1:1 + B * H * 512].view(B, H, 512)}
+    got = {}
+    for name, out in views.items():
+        plan = make_mla_plan(torch.from_numpy(q).to(dev), _device_pools(pools, dev), torch.from_numpy(table).to(dev),
+                             torch.from_numpy(counts).to(dev), torch.from_numpy(tags).to(dev), v_dim=512, out=out,
+                             pages_per_split=16)
+        plan.run()
+        torch.cuda.synchronize()
+        got[name] = out.float().cpu().numpy().copy()
+    assert np.isfinite(got["aligned"]).all()
+    assert np.array_equal(got["aligned"], got["offset"])
