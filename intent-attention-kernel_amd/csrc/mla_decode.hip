@@ -295,7 +295,7 @@ __global__ __launch_bounds__(512, 1) void mla_decode_kernel(const MArgs a) {
       return __builtin_bit_cast(
           float, pick(__builtin_bit_cast(int, meta.scale), __builtin_bit_cast(int, meta2.scale), idx));
     };
-    // pq[2k], pq[2k+1]: lanes of the pages of step s+k (ring slot (s+k) % SLOTS)
+    // pq[2k], pq[2k+1]: entry indexes of the pages of step s+k (ring slot (s+k) % SLOTS)
     int pq[2 * C::SLOTS];
 #pragma unroll
     for (int k = 0; k < C::SLOTS; ++k)
