@@ -116,10 +116,10 @@ def test_mla_random_configs(dev, seed):
     rng = np.random.default_rng(5000 + seed)
     dqk, dv, voff = MLA_SHAPES[int(rng.integers(0, len(MLA_SHAPES)))]
     B, H = int(rng.integers(1, 4)), int(rng.choice([1, 16, 70, 128, 130, 256]))
-    NP, W = int(rng.integers(4, 60)), int(rng.integers(1, 90))
+    NP, W = int(rng.integers(4, 60)), int(rng.integers(1, 200))
     names = list(rng.choice(["FP16", "FP8", "INT8", "SKIP"], size=int(rng.integers(1, 4)), replace=False))
     mix = {n: float(rng.random() + 0.1) for n in names}
-    pps = int(rng.choice([0, 1, 5, 16, 64]))
+    pps = int(rng.choice([0, 1, 5, 16, 64, 100, 128]))   # past 64: two entries per lane
     c = dict(seed=seed, dqk=dqk, dv=dv, voff=voff, B=B, H=H, NP=NP, W=W, mix=mix, pps=pps)
     _say("fuzz mla", c)
     q, pools, table, counts, tags = _latent_case(rng, B, H, dqk, NP, W, mix)
