@@ -325,7 +325,12 @@ __global__ __launch_bounds__(512, 1) void mla_decode_kernel(const MArgs a) {
       mla_dma_page<DQK, DV, WIDE>(sh.ring[slot][0], a, page_pid(in0), page_tag(in0), w, lane);
       mla_dma_page<DQK, DV, WIDE>(sh.ring[slot][1], a, page_pid(in1), page_tag(in1), w, lane);
 
+      // Wave priorities by phase: the staging of the next pair and the softmax
+      // (VALU and LDS work that the next barrier waits for) issue ahead of the
+      // other wave's MFMAs when the two waves of a SIMD are in different
+      // phases; the MFMA phases run at the lowest priority.
       // ---- scores of pair s: S^T[16 tok x 16 heads] per page, two chains ----
+      __builtin_amdgcn_s_setprio(0);
       f4 s0 = f4{0.f, 0.f, 0.f, 0.f}, s1 = f4{0.f, 0.f, 0.f, 0.f};
       {
         constexpr int PFS = C::PF_SCORE;
@@ -350,6 +355,7 @@ __global__ __launch_bounds__(512, 1) void mla_decode_kernel(const MArgs a) {
       }
 
       // ---- stage pair s+1 (landed before the barrier) ----
+      __builtin_amdgcn_s_setprio(3);
       if (st + 1 < nsteps)
         mla_stage_pair<DQK, DV, WIDE>(sh, (st + 1) & (C::SLOTS - 1), 1 - R, page_tag(nx0), page_tag(nx1), tid);
 #pragma unroll
@@ -358,6 +364,7 @@ __global__ __launch_bounds__(512, 1) void mla_decode_kernel(const MArgs a) {
       pq[2 * C::SLOTS - 1] = in1;
 
       // ---- softmax over the pair's 32 tokens ----
+      __builtin_amdgcn_s_setprio(1);
       const float ps0 = page_scale(cur0), ps1 = page_scale(cur1);
       s0 *= a.score_mult * ps0;
       s1 *= a.score_mult * ps1;
@@ -415,6 +422,7 @@ __global__ __launch_bounds__(512, 1) void mla_decode_kernel(const MArgs a) {
       }
 
       // ---- values of pair s: the wave's heads, every value dim ----
+      __builtin_amdgcn_s_setprio(0);
       {
         constexpr int PFV = C::PF_VALUE;
         h8 bq[PFV];
