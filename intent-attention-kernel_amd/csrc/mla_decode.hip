@@ -312,9 +312,9 @@ __global__ __launch_bounds__(512, 1) void mla_decode_kernel(const MArgs a) {
     // copies of pair s+1, then the barrier makes pair s's tile (staged in the
     // previous iteration) and pair s+1's raw bytes visible to every wave and
     // ends every read of the other tile buffer. Then pair s+SLOTS starts
-    // streaming into the ring slot pair s came from, pair s+1 is staged into
-    // the other tile buffer while pair s's score MFMAs run, and the softmax and
-    // values of pair s follow. R = s & 1 is pair s's tile buffer.
+    // streaming into the ring slot pair s came from, pair s's scores and
+    // softmax run, pair s+1 is staged into the other tile buffer, and pair s's
+    // values follow. R = s & 1 is pair s's tile buffer.
     for (int st = 0; st < nsteps; ++st) {
       const int R = st & 1;
       const int cur0 = pq[0], cur1 = pq[1], nx0 = pq[2], nx1 = pq[3];
@@ -354,10 +354,6 @@ __global__ __launch_bounds__(512, 1) void mla_decode_kernel(const MArgs a) {
         }
       }
 
-      // ---- stage pair s+1 (landed before the barrier) ----
-      __builtin_amdgcn_s_setprio(3);
-      if (st + 1 < nsteps)
-        mla_stage_pair<DQK, DV, WIDE>(sh, (st + 1) & (C::SLOTS - 1), 1 - R, page_tag(nx0), page_tag(nx1), tid);
 #pragma unroll
       for (int k = 0; k < 2 * C::SLOTS - 2; ++k) pq[k] = pq[k + 2];
       pq[2 * C::SLOTS - 2] = in0;
@@ -412,6 +408,10 @@ __global__ __launch_bounds__(512, 1) void mla_decode_kernel(const MArgs a) {
         pa[r] = (_Float16)(p0[r] * (ps0 * vm));
         pa[4 + r] = (_Float16)(p1[r] * (ps1 * vm));
       }
+      // ---- stage pair s+1 (landed before the barrier) ----
+      __builtin_amdgcn_s_setprio(3);
+      if (st + 1 < nsteps)
+        mla_stage_pair<DQK, DV, WIDE>(sh, (st + 1) & (C::SLOTS - 1), 1 - R, page_tag(nx0), page_tag(nx1), tid);
       // rescale: the O rows are heads 4g + r, whose factor sits in lane 4g + r
       if (__builtin_amdgcn_ballot_w64(grow) != 0 || emove) {
         f4 ar;
