@@ -41,6 +41,9 @@
  *                               kv_memory_manager.py:233-252, _read_page_data :286-296, set_page_format
  *                               :268-284 (demote_cold_pages :350-362, promote_hot_pages :364-377)
  *   iak_prefetch_pages          launch_prefetch_pages() prefetch.py:183-261 (its Triton kernel :111-170)
+ *   iak_dense_attention         dense_attention() reference.py:16-45 (causal, mask, original_kv_positions),
+ *                               under semantic_block_attention() reference.py:81-129 and
+ *                               intent_quant_attention_reference() intent_quant_attention.py:20-119
  *   iak_status_string           (no counterpart: the reference raises ValueError/RuntimeError in Python)
  */
 #ifndef IAK_H
@@ -53,7 +56,7 @@
 extern "C" {
 #endif
 
-#define IAK_ABI_VERSION 6
+#define IAK_ABI_VERSION 7
 
 /* Grid size from which merge_in_kernel = 2 merges inside the decode kernel. */
 #define IAK_MERGE_IN_KERNEL_MIN_WORKGROUPS 1024
@@ -461,6 +464,38 @@ typedef struct {
 } iak_mla_rows_args;
 
 iak_status iak_mla_decode_rows(const iak_mla_rows_args* args, void* stream);
+
+/* Dense softmax attention of the reference's dense_attention() (reference.py:16-45)
+ * in float32: for each (batch, query) row i,
+ *   s_j = (q_i . k_j) * sm_scale
+ *         + (-inf if causal == IAK_CAUSAL_TRIU and j > i)
+ *   s_j = -inf if causal == IAK_CAUSAL_POSITIONS and i < kv_positions[j]
+ *   s_j += mask[b, i, j]                       (bool masks add 1.0 where true)
+ *   out_i = softmax(s) . v
+ * NaN when every s_j is -inf (torch's softmax), zeros when kv_len == 0.
+ *
+ *   q    [batch, q_len, head_dim], k [batch, kv_len, head_dim], v [batch, kv_len, v_dim],
+ *   out  [batch, q_len, v_dim]: one dtype (IAK_DTYPE_*), element strides per batch and row,
+ *        unit inner stride; a batch stride of 0 broadcasts
+ *   mask (may be NULL) element (b, i, j) at b * mask_stride_b + i * mask_stride_q + j * mask_stride_k,
+ *        mask_dtype IAK_DTYPE_* or IAK_MASK_BOOL (one byte)
+ *   kv_positions [kv_len] int64 (IAK_CAUSAL_POSITIONS only)
+ *   head_dim, v_dim <= 1024. */
+enum { IAK_MASK_BOOL = 3 };
+enum { IAK_CAUSAL_NONE = 0, IAK_CAUSAL_TRIU = 1, IAK_CAUSAL_POSITIONS = 2 };
+typedef struct {
+  int32_t batch, q_len, kv_len, head_dim, v_dim, dtype;
+  const void* q; int64_t q_stride_b, q_stride_t;
+  const void* k; int64_t k_stride_b, k_stride_t;
+  const void* v; int64_t v_stride_b, v_stride_t;
+  void* out; int64_t out_stride_b, out_stride_t;
+  const void* mask; int32_t mask_dtype; int64_t mask_stride_b, mask_stride_q, mask_stride_k;
+  int32_t causal;
+  const int64_t* kv_positions;
+  float sm_scale;
+} iak_dense_attention_args;
+
+iak_status iak_dense_attention(const iak_dense_attention_args* args, void* stream);
 
 #ifdef __cplusplus
 }

@@ -330,6 +330,7 @@ iak_status scratch_address(int dev, void** out) {
 
 namespace iak {
 hipError_t launch_mla_rows(const iak_mla_rows_args& a, hipStream_t stream);   // mla_rows.hip
+hipError_t launch_dense_attention(const iak_dense_attention_args& a, hipStream_t stream);   // dense_attention.hip
 }
 
 extern "C" {
@@ -684,6 +685,34 @@ iak_status iak_mla_decode_rows(const iak_mla_rows_args* a, void* stream) {
   if (a->latent_stride < a->latent_dim && a->num_rows > 1)
     return fail(IAK_EINVAL, "latent_stride %lld is below latent_dim %d", (long long)a->latent_stride, a->latent_dim);
   const hipError_t e = iak::launch_mla_rows(*a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(IAK_EHIP, "kernel launch failed: %s", hipGetErrorString(e));
+  return IAK_OK;
+}
+
+iak_status iak_dense_attention(const iak_dense_attention_args* a, void* stream) {
+  if (!a) return fail(IAK_EINVAL, "args is NULL");
+  if (a->batch < 0 || a->q_len < 0 || a->kv_len < 0)
+    return fail(IAK_EINVAL, "negative size (batch=%d, q_len=%d, kv_len=%d)", a->batch, a->q_len, a->kv_len);
+  if (a->head_dim <= 0 || a->head_dim > 1024 || a->v_dim <= 0 || a->v_dim > 1024)
+    return fail(IAK_ENOTSUP, "head_dim %d / v_dim %d is not supported (1 .. 1024)", a->head_dim, a->v_dim);
+  if (a->dtype < 0 || a->dtype > 2) return fail(IAK_EINVAL, "unknown dtype %d", a->dtype);
+  if (a->mask && (a->mask_dtype < 0 || a->mask_dtype > IAK_MASK_BOOL))
+    return fail(IAK_EINVAL, "unknown mask dtype %d", a->mask_dtype);
+  if (a->causal < IAK_CAUSAL_NONE || a->causal > IAK_CAUSAL_POSITIONS)
+    return fail(IAK_EINVAL, "causal must be 0, 1 or 2, got %d", a->causal);
+  if ((long long)a->batch * a->q_len > 0x7FFFFFFFLL) return fail(IAK_EINVAL, "batch * q_len too large");
+  if ((long long)a->batch * a->q_len == 0) return IAK_OK;
+  if (!a->q || !a->out) return fail(IAK_EINVAL, "q/out is NULL");
+  if (a->kv_len > 0 && (!a->k || !a->v)) return fail(IAK_EINVAL, "k/v is NULL");
+  if (a->kv_len > 0 && a->causal == IAK_CAUSAL_POSITIONS && !a->kv_positions)
+    return fail(IAK_EINVAL, "kv_positions is NULL with causal = IAK_CAUSAL_POSITIONS");
+  const long long strides[] = {a->q_stride_b, a->q_stride_t, a->k_stride_b, a->k_stride_t, a->v_stride_b,
+                               a->v_stride_t, a->out_stride_b, a->out_stride_t};
+  for (long long st : strides)
+    if (st < 0) return fail(IAK_EINVAL, "negative stride %lld", st);
+  if (a->mask && (a->mask_stride_b < 0 || a->mask_stride_q < 0 || a->mask_stride_k < 0))
+    return fail(IAK_EINVAL, "negative mask stride");
+  const hipError_t e = iak::launch_dense_attention(*a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(IAK_EHIP, "kernel launch failed: %s", hipGetErrorString(e));
   return IAK_OK;
 }

@@ -39,8 +39,8 @@ from .intent_quant_decode import (
     make_precision_tensor,
 )
 from .decode_core import PagePools, make_plan, pack_page_descriptors, paged_decode
-from .reference import dense_attention
-from .intent_quant_attention import intent_quant_attention_reference
+from .reference import dense_attention, semantic_block_attention
+from .intent_quant_attention import compare_intent_quant_to_fp16_selected, intent_quant_attention_reference
 from .mla import MLABlockTable, MLAConfig, absorb_weights, mla_sparse_decode_reference, mla_triton_decode
 from .mla_core import LatentPools, mla_paged_decode
 from .triton_mla_decode import mla_decode_triton
@@ -68,7 +68,8 @@ __all__ = [
     "IntentQuantKernelConfig", "TritonKVPrecision", "fake_int8_pages_from_fp16",
     "intent_quant_decode_attention_triton", "make_page_tables_from_selected_pages", "make_precision_tensor",
     "PagePools", "make_plan", "pack_page_descriptors", "paged_decode",
-    "dense_attention", "intent_quant_attention_reference",
+    "dense_attention", "semantic_block_attention", "intent_quant_attention_reference",
+    "compare_intent_quant_to_fp16_selected",
     "MLABlockTable", "MLAConfig", "absorb_weights", "mla_sparse_decode_reference", "mla_triton_decode",
     "LatentPools", "mla_paged_decode", "mla_decode_triton",
     "quantize_pages", "fake_int8_pages_device",

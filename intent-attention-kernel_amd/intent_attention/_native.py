@@ -14,12 +14,14 @@ from typing import Optional
 _HERE = os.path.dirname(os.path.abspath(__file__))
 # IAK_LIBRARY selects another build of the same ABI (e.g. a tuning variant)
 LIB_PATH = os.environ.get("IAK_LIBRARY") or os.path.join(_HERE, "libiak.so")
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 IAK_OK, IAK_EINVAL, IAK_ENOTSUP, IAK_EHIP = 0, 1, 2, 3
 
 TAG_FP16, TAG_INT8, TAG_SKIP, TAG_FP8, TAG_INT4, TAG_INT4_RESIDUAL = 0, 1, 2, 3, 4, 5
 DTYPE_F16, DTYPE_F32, DTYPE_BF16 = 0, 1, 2
+MASK_BOOL = 3
+CAUSAL_NONE, CAUSAL_TRIU, CAUSAL_POSITIONS = 0, 1, 2
 
 c_i32, c_i64, c_void_p, c_float = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p, ctypes.c_float
 
@@ -143,13 +145,31 @@ class MlaRowsArgs(ctypes.Structure):
     ]
 
 
+class DenseAttentionArgs(ctypes.Structure):
+    """Mirror of ``iak_dense_attention_args`` (include/iak.h)."""
+
+    _fields_ = [
+        ("batch", c_i32), ("q_len", c_i32), ("kv_len", c_i32), ("head_dim", c_i32), ("v_dim", c_i32),
+        ("dtype", c_i32),
+        ("q", c_void_p), ("q_stride_b", c_i64), ("q_stride_t", c_i64),
+        ("k", c_void_p), ("k_stride_b", c_i64), ("k_stride_t", c_i64),
+        ("v", c_void_p), ("v_stride_b", c_i64), ("v_stride_t", c_i64),
+        ("out", c_void_p), ("out_stride_b", c_i64), ("out_stride_t", c_i64),
+        ("mask", c_void_p), ("mask_dtype", c_i32), ("mask_stride_b", c_i64), ("mask_stride_q", c_i64),
+        ("mask_stride_k", c_i64),
+        ("causal", c_i32),
+        ("kv_positions", c_void_p),
+        ("sm_scale", c_float),
+    ]
+
+
 EXPORTED = ("iak_abi_version", "iak_status_string", "iak_last_error",
             "iak_paged_decode_workspace", "iak_paged_decode",
             "iak_mla_decode_workspace", "iak_mla_decode", "iak_quantize_pages",
             "iak_build_page_tables", "iak_paged_decode_timed", "iak_mla_decode_timed",
             "iak_paged_decode_noalloc", "iak_transcode_pages", "iak_prefetch_pages", "iak_paged_decode_plan",
             "iak_mla_decode_rows", "iak_pack_page_descriptors",
-            "iak_pack_entry_records")
+            "iak_pack_entry_records", "iak_dense_attention")
 NOALLOC_SCRATCH_BYTES = 16 << 20   # IAK_NOALLOC_SCRATCH_BYTES
 
 _lib: Optional[ctypes.CDLL] = None
@@ -208,6 +228,8 @@ def load() -> ctypes.CDLL:
     lib.iak_build_page_tables.argtypes = [ctypes.POINTER(PageTableArgs), c_void_p]
     lib.iak_pack_page_descriptors.restype = ctypes.c_int
     lib.iak_pack_page_descriptors.argtypes = [ctypes.POINTER(PagedDecodeArgs), c_void_p, c_void_p]
+    lib.iak_dense_attention.restype = ctypes.c_int
+    lib.iak_dense_attention.argtypes = [ctypes.POINTER(DenseAttentionArgs), c_void_p]
     lib.iak_pack_entry_records.restype = ctypes.c_int
     lib.iak_pack_entry_records.argtypes = [ctypes.POINTER(PagedDecodeArgs), c_void_p, c_void_p]
     ver = lib.iak_abi_version()
@@ -317,3 +339,7 @@ def mla_decode_rows(args: MlaRowsArgs, stream: int) -> None:
 
 def build_page_tables(args: PageTableArgs, stream: int) -> None:
     check(load().iak_build_page_tables(ctypes.byref(args), stream or None))
+
+
+def dense_attention(args: DenseAttentionArgs, stream: int) -> None:
+    check(load().iak_dense_attention(ctypes.byref(args), stream or None))

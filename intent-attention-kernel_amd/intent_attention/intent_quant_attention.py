@@ -19,6 +19,10 @@ Semantics kept from the reference, step for step:
   estimates, per-block precision and reconstruction MSE, and the output's
   error against attention over the unquantised selected tokens (:87-118).
 
+``compare_intent_quant_to_fp16_selected`` (:138-165) sets the output against
+``semantic_block_attention`` over the same selected tokens and reports the
+reference's keys.
+
 The fake quantisation runs as torch ops on the input's device (the product
 ``intent_quant.fake_quantize_tensor``, the reference's arithmetic); the
 attention is ``reference.dense_attention`` on libiak's paged decode kernel.
@@ -34,7 +38,7 @@ from .block_metadata import BlockLayout
 from .decode_core import require_device
 from .intent_quant import IntentQuantizer, KVPrecision, QuantPolicy, compute_quant_error, \
     fake_dequantize_tensor, fake_quantize_tensor
-from .reference import dense_attention
+from .reference import dense_attention, semantic_block_attention
 
 
 def _empty_debug(layout: BlockLayout, kv_tokens: int) -> Dict[str, Any]:
@@ -114,3 +118,27 @@ def intent_quant_attention_reference(q: torch.Tensor, k: torch.Tensor, v: torch.
         "output_max_abs_error_vs_fp16_selected": err["max_abs_error"],
     }
     return output, debug
+
+
+def compare_intent_quant_to_fp16_selected(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layout: BlockLayout,
+                                          quantizer: IntentQuantizer) -> Dict[str, Any]:
+    """Error of the fake-quantised attention against unquantised attention over the
+    same selected tokens, with the byte estimates and per-block precisions
+    (intent_quant_attention.py:138-165)."""
+    fp16_out, fp16_debug = semantic_block_attention(q, k, v, layout, causal=False, return_debug=True)
+    quant_out, quant_debug = intent_quant_attention_reference(q, k, v, layout, quantizer, causal=False,
+                                                              return_debug=True)
+    err = compute_quant_error(fp16_out, quant_out)
+    return {
+        "output_mse": err["mse"],
+        "output_cosine_similarity": err["cosine_similarity"],
+        "output_max_abs_error": err["max_abs_error"],
+        "fp16_selected_tokens": fp16_debug["selected_token_count"],
+        "quant_selected_tokens": quant_debug["selected_tokens"],
+        "estimated_fp16_bytes": quant_debug["estimated_fp16_bytes"],
+        "estimated_quant_bytes": quant_debug["estimated_quant_bytes"],
+        "bytes_saved_pct": quant_debug["bytes_saved_pct"],
+        "precision_by_block": quant_debug["precision_by_block"],
+        "reconstruction_mse_k": quant_debug["reconstruction_mse_k"],
+        "reconstruction_mse_v": quant_debug["reconstruction_mse_v"],
+    }

@@ -1,110 +1,188 @@
-"""``dense_attention`` of the reference (reference.py:16-45) on the HIP paged decode.
+"""``dense_attention`` and ``semantic_block_attention`` of the reference
+(reference.py:16-129) on libiak's dense attention kernel.
 
-Softmax attention ``softmax(q k^T / sqrt(D)) v`` over the last two dims, as
-the reference computes it with two ``torch.matmul`` calls. Here K and V are
-laid out as 16-token float16 pages (zero-padded; the last page of each
-sequence bounded by the kernel's token count) and the attention runs on
-libiak's selected-page decode kernel: every (leading index, query) pair is a
-decode row over all of that index's pages.
+``dense_attention(q, k, v, causal, mask, original_kv_positions)`` is softmax
+attention over the last two dims, as the reference computes it with two
+``torch.matmul`` calls (reference.py:16-45):
 
-Kept from the reference: argument names and defaults, the output (shape and
-dtype of ``q``), ``causal=True`` as the upper-triangular mask of
-``torch.triu(..., diagonal=1)`` (query i sees keys 0 .. i), and the
-RuntimeError of ``torch.matmul`` on mixed dtypes.
+* scores ``(q k^T) / sqrt(D)``;
+* ``causal=True`` without positions adds ``triu(-inf, diagonal=1)`` (query i
+  sees keys 0 .. i); with ``original_kv_positions`` query i sees key j only
+  where ``positions[j] <= i`` (the reference's ``masked_fill``);
+  ``original_kv_positions`` without ``causal`` changes nothing;
+* an additive ``mask`` broadcast to the scores (a bool mask adds 1.0 where
+  true, as ``float + bool`` does in torch);
+* a query whose scores are all -inf gives NaN (torch's softmax), an empty key
+  set gives zeros.
 
-Differences, by design:
+Leading dims broadcast as in ``torch.matmul``; the output has the shape
+``[*lead, Tq, Dv]`` and the dtype of ``q``. The dtype rules of the reference's
+two matmuls are kept: ``q`` and ``k`` must share a dtype, and a ``mask`` that
+promotes the scores to another dtype than ``v``'s raises the same
+RuntimeError the reference's second matmul raises.
 
-* device tensors only (host tensors raise RuntimeError; there is no CPU
-  path in this package);
-* leading dims of q, k and v must be equal (no broadcasting) and
-  ``head_dim <= 128`` (padded to 64 or 128 with zeros, which changes no
-  score);
-* K and V are rounded to float16 pages (the kernel's FP16 pool format):
-  float32 inputs differ from the reference's float32 matmuls by that
-  rounding (relative 2^-11 per value);
-* an additive ``mask`` or ``original_kv_positions`` raise
-  NotImplementedError: the paged kernel applies only token bounds.
+The kernel (``iak_dense_attention``) computes every product and sum in
+float32 over float32, float16 or bfloat16 inputs and rounds the output once,
+where the reference rounds its scores and weights to the input dtype; for
+float32 inputs both are float32 arithmetic. head_dim and v_dim are at most
+1,024. Device tensors only: host tensors raise RuntimeError.
+
+``semantic_block_attention`` (reference.py:81-129) attends to the layout's
+selected tokens through ``dense_attention``, scoring ATTEND blocks that carry
+no score first (``_resolve_dynamic_scores`` :52-78 with the cosine probe of
+``BlockScorer.score_blocks``, block_scorer.py:17-34).
 """
 from __future__ import annotations
 
 import math
-from typing import Optional
+from typing import Any, Dict, List, Optional, Tuple, Union
 
 import torch
 
-from .decode_core import PAGE_SIZE, PagePools, paged_decode, require_device
 from . import _native as N
+from .block_metadata import BlockLayout, BlockPolicy
+from .decode_core import require_device
 
-_WIDTHS = (64, 128)
-_MAX_GROUP = 16          # query rows sharing one page-table row (the kernel's GQA limit)
+_DTYPES = {torch.float16: N.DTYPE_F16, torch.float32: N.DTYPE_F32, torch.bfloat16: N.DTYPE_BF16}
+_MAX_DIM = 1024
 
 
-def _pages_of(x: torch.Tensor, width: int) -> torch.Tensor:
-    """[L, T, D] -> float16 pages [L * P, 16, width], zero-padded in tokens and dims."""
-    L, T, D = x.shape
-    P = max(1, (T + PAGE_SIZE - 1) // PAGE_SIZE)
-    pages = torch.zeros((L, P * PAGE_SIZE, width), dtype=torch.float16, device=x.device)
-    pages[:, :T, :D] = x
-    return pages.view(L * P, PAGE_SIZE, width)
+def _dtype_name(dt: torch.dtype) -> str:
+    """torch's C++ name of a dtype, as its matmul error messages print it."""
+    return {torch.float16: "c10::Half", torch.bfloat16: "c10::BFloat16", torch.float32: "float",
+            torch.float64: "double"}.get(dt, str(dt))
+
+
+def _rows(x: torch.Tensor, lead: Tuple[int, ...]) -> torch.Tensor:
+    """[*lead', T, D] broadcast to [*lead, T, D] and viewed as [L, T, D] with a unit inner stride
+    (a view where the strides allow it, else a copy)."""
+    x = x.expand(*lead, x.shape[-2], x.shape[-1])
+    x = x.reshape(math.prod(lead), x.shape[-2], x.shape[-1])
+    if x.stride(-1) != 1 and x.shape[-1] > 1:
+        x = x.contiguous()
+    return x
 
 
 def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = False,
                     mask: Optional[torch.Tensor] = None,
                     original_kv_positions: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """softmax(q k^T / sqrt(D)) v over [..., T, D] tensors, on the HIP decode kernel."""
-    if mask is not None or original_kv_positions is not None:
-        raise NotImplementedError("dense_attention on the paged decode kernel supports token bounds only "
-                                  "(causal=True); an additive mask or original_kv_positions is not supported")
-    dev = require_device(q, k, v, what="dense attention")
-    if q.dtype != k.dtype or k.dtype != v.dtype:
-        # the reference's torch.matmul refuses mixed dtypes
-        raise RuntimeError(f"expected m1 and m2 to have the same dtype, but got: {q.dtype} != "
-                           f"{k.dtype if q.dtype != k.dtype else v.dtype}")
-    if q.dim() < 2 or k.dim() != q.dim() or v.dim() != q.dim():
-        raise ValueError(f"q, k and v must have the same number of dims (>= 2), got {q.dim()}, {k.dim()}, {v.dim()}")
-    lead = tuple(q.shape[:-2])
-    if tuple(k.shape[:-2]) != lead or tuple(v.shape[:-2]) != lead or k.shape[-2] != v.shape[-2]:
-        raise ValueError(f"q, k and v must share their leading dims and k, v their length: "
-                         f"{tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
-    D = q.shape[-1]
-    if k.shape[-1] != D or v.shape[-1] != D:
-        raise ValueError(f"head dims differ: q {D}, k {k.shape[-1]}, v {v.shape[-1]}")
-    if D > _WIDTHS[-1]:
-        raise ValueError(f"head_dim {D} exceeds the widest supported ({_WIDTHS[-1]})")
-    if q.dtype not in (torch.float16, torch.float32, torch.bfloat16):
-        raise ValueError(f"dtype {q.dtype} is not supported")
-    width = next(w for w in _WIDTHS if w >= D)
-    L = math.prod(lead) if lead else 1
+    """softmax(q k^T / sqrt(D) [+ causal mask] [+ mask]) v over [..., T, D] tensors, on the HIP kernel."""
+    dev = require_device(*(t for t in (q, k, v, mask, original_kv_positions) if t is not None),
+                         what="dense attention")
+    if q.dim() < 2 or k.dim() < 2 or v.dim() < 2:
+        raise RuntimeError("both arguments to matmul need to be at least 2D")
+    if q.dtype != k.dtype:
+        raise RuntimeError(f"expected m1 and m2 to have the same dtype, but got: {_dtype_name(q.dtype)} != "
+                           f"{_dtype_name(k.dtype)}")
+    D, Dv = q.shape[-1], v.shape[-1]
     Tq, Tk = q.shape[-2], k.shape[-2]
-    out = torch.zeros(q.shape, dtype=q.dtype, device=dev)
+    if k.shape[-1] != D:
+        raise RuntimeError(f"q and k head dims differ: {D} != {k.shape[-1]}")
+    if v.shape[-2] != Tk:
+        raise RuntimeError(f"k and v lengths differ: {Tk} != {v.shape[-2]}")
+    score_dtype = q.dtype if mask is None else torch.promote_types(q.dtype, mask.dtype)
+    if score_dtype != v.dtype:
+        raise RuntimeError(f"expected m1 and m2 to have the same dtype, but got: {_dtype_name(score_dtype)} != "
+                           f"{_dtype_name(v.dtype)}")
+    if q.dtype not in _DTYPES:
+        raise ValueError(f"dtype {q.dtype} is not supported (float16, float32, bfloat16)")
+    if D > _MAX_DIM or Dv > _MAX_DIM:
+        raise ValueError(f"head_dim {D} / v_dim {Dv} exceeds the widest supported ({_MAX_DIM})")
+    lead = tuple(torch.broadcast_shapes(q.shape[:-2], k.shape[:-2], v.shape[:-2]))
+    mask_rows = None
+    if mask is not None:
+        if mask.dtype != torch.bool and mask.dtype not in _DTYPES:
+            raise ValueError(f"mask dtype {mask.dtype} is not supported (bool, float16, float32, bfloat16)")
+        full = torch.broadcast_shapes(tuple(mask.shape), (*lead, Tq, Tk))
+        if tuple(full[-2:]) != (Tq, Tk):
+            raise RuntimeError(f"mask of shape {tuple(mask.shape)} does not broadcast to the scores "
+                               f"{(*lead, Tq, Tk)}")
+        lead = tuple(full[:-2])
+        mask_rows = _rows(mask, lead)
+    positions = None
+    if causal and original_kv_positions is not None:
+        if original_kv_positions.dtype.is_floating_point or original_kv_positions.dtype == torch.bool:
+            raise ValueError(f"original_kv_positions must be an integer tensor, got {original_kv_positions.dtype}")
+        if original_kv_positions.dim() != 1 or original_kv_positions.shape[0] != Tk:
+            raise RuntimeError(f"The size of original_kv_positions {tuple(original_kv_positions.shape)} must "
+                               f"match the number of keys ({Tk})")
+        positions = original_kv_positions.to(torch.int64).contiguous()
+
+    L = math.prod(lead)
+    out = torch.empty((*lead, Tq, Dv), dtype=q.dtype, device=dev)
     if L == 0 or Tq == 0:
         return out
-    P = max(1, (Tk + PAGE_SIZE - 1) // PAGE_SIZE)
-    kp = _pages_of(k.reshape(L, Tk, D), width)
-    vp = _pages_of(v.reshape(L, Tk, D), width)
-    tags = torch.zeros(L * P, dtype=torch.int32, device=dev)           # every page FP16
-    pools = PagePools(k_fp16=kp, v_fp16=vp)
-    qq = q.reshape(L, Tq, D)
-    if width != D:
-        qq = torch.nn.functional.pad(qq, (0, width - D))
-    qq = qq.contiguous()
-    rows = torch.arange(L, device=dev, dtype=torch.int32)[:, None] * P + torch.arange(P, device=dev,
-                                                                                      dtype=torch.int32)
-    sm = 1.0 / math.sqrt(D)
-    if not causal and Tq <= _MAX_GROUP:
-        # one page-table row per leading index, shared by its Tq queries (the GQA group)
-        o = paged_decode(qq.view(1, L * Tq, width), pools, rows.view(1, L, P).contiguous(),
-                         torch.full((1, L), P, dtype=torch.int32, device=dev), tags, sm_scale=sm,
-                         valid_tokens=torch.full((1, L), Tk, dtype=torch.int32, device=dev),
-                         tag_map=[N.TAG_FP16] + [N.TAG_SKIP] * 7)
-        return o.view(L, Tq, width)[..., :D].reshape(q.shape)
-    # one row per (leading index, query): causal rows see keys 0 .. i
-    table = rows[:, None, :].expand(L, Tq, P).reshape(1, L * Tq, P).contiguous()
-    t = torch.arange(Tq, device=dev, dtype=torch.int32)
-    bound = torch.minimum(t + 1, torch.tensor(Tk, dtype=torch.int32, device=dev)) if causal else \
-        torch.full((Tq,), Tk, dtype=torch.int32, device=dev)
-    o = paged_decode(qq.view(1, L * Tq, width), pools, table,
-                     torch.full((1, L * Tq), P, dtype=torch.int32, device=dev), tags, sm_scale=sm,
-                     valid_tokens=bound.repeat(L).view(1, L * Tq).contiguous(),
-                     tag_map=[N.TAG_FP16] + [N.TAG_SKIP] * 7)
-    return o.view(L, Tq, width)[..., :D].reshape(q.shape)
+    qr, kr, vr = _rows(q, lead), _rows(k, lead), _rows(v, lead)
+    o = out.view(L, Tq, Dv)
+    a = N.DenseAttentionArgs()
+    a.batch, a.q_len, a.kv_len, a.head_dim, a.v_dim, a.dtype = L, Tq, Tk, D, Dv, _DTYPES[q.dtype]
+    a.q, a.q_stride_b, a.q_stride_t = qr.data_ptr(), qr.stride(0), qr.stride(1)
+    a.k, a.k_stride_b, a.k_stride_t = kr.data_ptr(), kr.stride(0), kr.stride(1)
+    a.v, a.v_stride_b, a.v_stride_t = vr.data_ptr(), vr.stride(0), vr.stride(1)
+    a.out, a.out_stride_b, a.out_stride_t = o.data_ptr(), o.stride(0), o.stride(1)
+    if mask_rows is not None:
+        a.mask = mask_rows.data_ptr()
+        a.mask_dtype = N.MASK_BOOL if mask.dtype == torch.bool else _DTYPES[mask.dtype]
+        a.mask_stride_b, a.mask_stride_q, a.mask_stride_k = (mask_rows.stride(0), mask_rows.stride(1),
+                                                             mask_rows.stride(2))
+    if causal:
+        a.causal = N.CAUSAL_TRIU if positions is None else N.CAUSAL_POSITIONS
+        if positions is not None:
+            a.kv_positions = positions.data_ptr()
+    a.sm_scale = 1.0 / math.sqrt(D)
+    # the operands (and any copies made above) were allocated on this stream, so
+    # the caching allocator reuses their memory only after this kernel
+    N.dense_attention(a, torch.cuda.current_stream(dev).cuda_stream)
+    return out
+
+
+def _resolve_dynamic_scores(q: torch.Tensor, k: torch.Tensor, layout: BlockLayout) -> Dict[str, float]:
+    """Score the ATTEND blocks whose score is None (reference.py:52-78): cosine of the
+    query's mean over rows and leading dims with the block's mean key
+    (BlockScorer.score_blocks, block_scorer.py:17-34), clamped at 0, written
+    into the blocks."""
+    targets = [b for b in layout.blocks if b.policy == BlockPolicy.ATTEND and b.score is None]
+    if not targets:
+        return {}
+    qg = q.mean(dim=-2).mean(dim=(0, 1))
+    qn = qg / (qg.norm(p=2) + 1e-10)
+    reps = [k[..., b.start:b.end, :].mean(dim=-2).mean(dim=(0, 1)) for b in targets]
+    sims = [torch.dot(qn, r / (r.norm(p=2) + 1e-10)) for r in reps]
+    values = torch.stack(sims).tolist()   # one host copy for all blocks
+    dynamic: Dict[str, float] = {}
+    for block, s in zip(targets, values):
+        block.score = max(0.0, float(s))
+        dynamic[block.name] = block.score
+    return dynamic
+
+
+def semantic_block_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layout: BlockLayout,
+                             causal: bool = False, return_debug: bool = False,
+                             threshold: float = 0.5) -> Union[torch.Tensor, Tuple[torch.Tensor, Dict[str, Any]]]:
+    """Attention of q over the layout's selected tokens (reference.py:81-129); with
+    ``causal`` the selected keys keep their original positions."""
+    require_device(q, k, v, what="semantic block attention")
+    kv_tokens = k.size(-2)
+    dynamic = _resolve_dynamic_scores(q, k, layout)
+    layout.validate(kv_tokens)
+    selected: List[int] = layout.selected_token_indices()
+    if not selected:
+        out = torch.zeros_like(q)
+        if not return_debug:
+            return out
+        debug: Dict[str, Any] = {"selected_token_count": 0, "selected_block_names": [],
+                                 "total_kv_tokens": kv_tokens, "selected_kv_tokens": 0}
+        if dynamic:
+            debug["dynamic_scores"] = dynamic
+        return out, debug
+    idx = torch.tensor(selected, dtype=torch.long, device=k.device)
+    out = dense_attention(q, k.index_select(-2, idx), v.index_select(-2, idx), causal=causal,
+                          original_kv_positions=idx)
+    if not return_debug:
+        return out
+    debug = {"selected_token_count": layout.selected_token_count(),
+             "selected_block_names": [b.name for b in layout.selected_blocks()],
+             "total_kv_tokens": kv_tokens, "selected_kv_tokens": len(selected)}
+    if dynamic:
+        debug["dynamic_scores"] = dynamic
+    return out, debug

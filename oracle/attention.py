@@ -2,8 +2,12 @@
 
 Restates
 
-  reference.py:16-45                 dense_attention (non-causal path):
-                                     softmax(q k^T / sqrt(D)) v
+  reference.py:16-45                 dense_attention: softmax(q k^T / sqrt(D)) v,
+                                     with causal (triu or original KV
+                                     positions) and an additive mask
+  reference.py:81-129                semantic_block_attention (selected tokens,
+                                     ATTEND blocks scored by block_scorer.py:17-34)
+  intent_quant_attention.py:138-165  compare_intent_quant_to_fp16_selected
   intent_quant_attention.py:20-119   intent_quant_attention_reference:
                                      per selected block fake-quant -> dequant
                                      -> concatenate -> dense_attention
@@ -24,8 +28,12 @@ dtype torch would use (``exact=False``).
 
 Pinned by: a brute-force softmax on tiny inputs, the reference tests' facts
 (empty selection -> zeros, causal raises, semantic == dense over the selected
-tokens, test_reference_correctness.py:7-25, test_intent_quant_attention.py)
-and golden vectors written by the reference (tests/golden/).
+tokens, test_reference_correctness.py:7-25, test_intent_quant_attention.py,
+test_causal_attention.py) and golden vectors written by the reference
+(tests/golden/). ``dense_attention_masked`` is pinned by an explicit loop
+over each query's visible keys (tests/test_oracle_attention.py) and by
+identities: positions 0 .. Tk-1 equal the triu mask, a -inf mask entry
+equals dropping that key, a per-row constant mask changes nothing.
 """
 from __future__ import annotations
 
@@ -50,6 +58,58 @@ def dense_attention(q, k, v, exact: bool = True):
     p = np.exp(s)
     p = p / p.sum(axis=-1, keepdims=True)
     return np.matmul(p, v.astype(dt))
+
+
+def dense_attention_masked(q, k, v, causal: bool = False, mask=None, original_kv_positions=None):
+    """reference.py:16-45 in float64 with every branch: scores (q k^T) / sqrt(D);
+    causal without positions adds triu(-inf, 1); causal with positions sets
+    scores[i, j] = -inf where i < positions[j] (:31-34); then ``+ mask`` (a bool
+    mask adds 1.0); softmax (NaN where every score is -inf); zeros for no keys."""
+    q, k, v = (np.asarray(x, dtype=np.float64) for x in (q, k, v))
+    Tq, Tk = q.shape[-2], k.shape[-2]
+    s = np.matmul(q, np.swapaxes(k, -2, -1)) / math.sqrt(q.shape[-1])
+    if causal:
+        if original_kv_positions is not None:
+            pos = np.asarray(original_kv_positions)
+            s = np.where(np.arange(Tq)[:, None] < pos[None, :], -np.inf, s)
+        else:
+            s = s + np.triu(np.full((Tq, Tk), -np.inf), k=1)
+    if mask is not None:
+        s = s + np.asarray(mask).astype(np.float64)
+    if Tk == 0:
+        return np.zeros(s.shape[:-1] + (v.shape[-1],))
+    with np.errstate(invalid="ignore"):
+        m = s.max(axis=-1, keepdims=True)
+        p = np.exp(s - m)
+        p = p / p.sum(axis=-1, keepdims=True)
+    return np.matmul(p, v)
+
+
+def dynamic_block_scores(q, k, layout: BlockLayout) -> dict:
+    """reference.py:52-78 / block_scorer.py:17-34: the cosine of the query's mean
+    (over rows, then the first two dims) with each unscored ATTEND block's mean
+    key, clamped at 0 (float64)."""
+    q, k = np.asarray(q, np.float64), np.asarray(k, np.float64)
+    qg = q.mean(axis=-2).mean(axis=(0, 1))
+    qn = qg / (np.linalg.norm(qg) + 1e-10)
+    out = {}
+    for b in layout.blocks:
+        if b.policy == "ATTEND" and b.score is None:
+            r = k[..., b.start:b.end, :].mean(axis=-2).mean(axis=(0, 1))
+            out[b.name] = max(0.0, float(qn @ (r / (np.linalg.norm(r) + 1e-10))))
+    return out
+
+
+def semantic_block_attention(q, k, v, layout: BlockLayout, causal: bool = False):
+    """reference.py:81-129 (output only): attention over the selected tokens, keys at
+    their original positions. Unscored ATTEND blocks must be scored by the caller."""
+    layout.validate(np.asarray(k).shape[-2])
+    idx = np.asarray([t for b in layout.selected_blocks() for t in range(b.start, b.end)],   # block_metadata.py:75-79
+                     dtype=np.int64)
+    if idx.size == 0:
+        return np.zeros(np.asarray(q).shape)
+    k, v = np.asarray(k)[..., idx, :], np.asarray(v)[..., idx, :]
+    return dense_attention_masked(q, k, v, causal=causal, original_kv_positions=idx)
 
 
 def _promote(parts):

@@ -175,6 +175,19 @@ void invalid_launches() {
     count(iak_mla_decode_rows(&r, nullptr));
   }
   count(iak_mla_decode_rows(nullptr, nullptr));
+
+  iak_dense_attention_args da;
+  for (int i = 0; i < 300; ++i) {
+    random_bytes(da);
+    switch (rng() % 4) {   // at least one field invalid, so nothing reaches a launch
+      case 0: da.head_dim = 1025 + (int32_t)(rng() % 100); break;
+      case 1: da.causal = 3 + (int32_t)(rng() % 50); break;
+      case 2: da.dtype = 3 + (int32_t)(rng() % 50); break;
+      default: da.q_len = -1 - (int32_t)(rng() % 50); break;
+    }
+    count(iak_dense_attention(&da, nullptr));
+  }
+  count(iak_dense_attention(nullptr, nullptr));
 }
 
 }  // namespace

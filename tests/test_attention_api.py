@@ -1,14 +1,18 @@
-"""intent_quant_attention_reference and dense_attention of the product
+"""intent_quant_attention_reference, compare_intent_quant_to_fp16_selected,
+semantic_block_attention and dense_attention of the product
 (intent_attention.intent_quant_attention / intent_attention.reference), with
-the attention on the HIP paged decode.
+the attention on the HIP dense attention kernel.
 
 GPU: the reference's own outputs (golden g4: the cfg1 shape with its
 alternating FP16 / INT8 plan, and a plan with every precision including a
 SKIP-precision block, plus the default policy) within the quantised-page bar
 1e-2; the debug dictionary's keys and values; dense_attention against a
-float64 softmax over shapes, dtypes, causal masks and ragged lengths, and
-the reference's error behaviour. CPU: the errors raised before any device
-work (causal, host tensors, additive masks).
+float64 softmax over shapes, dtypes, causal masks and ragged lengths, against
+the float64 oracle with additive float / bool / -inf masks, original KV
+positions (sorted and not), broadcast leading dims and all-masked rows; the
+reference's test_causal_attention.py cases and its compare-function test on
+device tensors; the reference's error behaviour. CPU: the errors raised
+before any device work (causal, host tensors).
 """
 import math
 import os
@@ -76,7 +80,7 @@ def test_errors_before_device_work():
                                          IntentQuantizer())
     with pytest.raises(RuntimeError, match="HIP kernels only"):
         dense_attention(q, q, q)
-    with pytest.raises(NotImplementedError, match="mask"):
+    with pytest.raises(RuntimeError, match="HIP kernels only"):
         dense_attention(q, q, q, mask=torch.zeros(1, 1))
 
 
@@ -175,8 +179,8 @@ def test_dense_attention_against_float64(lead, Tq, Tk, D, dt, causal):
         s = s + torch.triu(torch.full((Tq, Tk), float("-inf"), dtype=torch.float64), diagonal=1)
     ref = (torch.softmax(s, dim=-1) @ vd) if Tk else torch.zeros_like(qd)
     err = float((out.cpu().double() - ref).abs().max())
-    # float16 pages: K/V rounded to float16 (float32 / bfloat16 inputs), the output to its dtype
-    tol = {"float32": 2e-3, "float16": 2e-3, "bfloat16": 1e-2}[dt]
+    # float32 arithmetic; the output rounded once to its dtype
+    tol = {"float32": 2e-5, "float16": 1e-3, "bfloat16": 8e-3}[dt]
     _say(f"  max abs err {err:.2e}")
     assert err <= tol
 
@@ -188,3 +192,206 @@ def test_dense_attention_dtype_mismatch_raises():
     q = torch.zeros(1, 2, 1, 64, device=dev)
     with pytest.raises(RuntimeError, match="same dtype"):
         dense_attention(q.half(), q, q)
+    with pytest.raises(RuntimeError, match="same dtype"):
+        # float16 scores + a float32 mask promote to float32, which the second matmul refuses
+        dense_attention(q.half(), q.half(), q.half(), mask=torch.zeros(1, 1, device=dev))
+
+
+_TOL = {torch.float32: 2e-5, torch.float16: 1e-3, torch.bfloat16: 8e-3}
+
+
+def _dense_case(seed, lead, Tq, Tk, D, Dv, dt, dev):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(*lead, Tq, D, generator=g).to(dt)
+    k = torch.randn(*lead, Tk, D, generator=g).to(dt)
+    v = torch.randn(*lead, Tk, Dv, generator=g).to(dt)
+    return q, k, v, g
+
+
+def _cmp(out, ref, dt, what):
+    o = out.cpu().double().numpy()
+    nan_ok = np.array_equal(np.isnan(o), np.isnan(ref))
+    err = float(np.nanmax(np.abs(o - ref))) if np.isfinite(ref).any() else 0.0
+    _say(f"  {what}: max abs err {err:.2e}, NaN pattern equal {nan_ok}")
+    assert nan_ok and err <= _TOL[dt]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16, torch.bfloat16])
+def test_dense_attention_masks_and_positions(dt):
+    """Additive masks (float with -inf entries, bool, per-batch), original KV positions
+    (sorted and unsorted, with and without a mask), v_dim != head_dim and broadcast
+    leading dims, against the float64 oracle."""
+    from intent_attention import dense_attention
+    dev = torch.device("cuda:0")
+    _say("dense_attention masks / positions", dt)
+    q, k, v, g = _dense_case(5, (2, 3), 12, 70, 64, 48, dt, dev)
+    t = lambda x: x.to(dev)  # noqa: E731
+    Tq, Tk = 12, 70
+    fmask = torch.randn(Tq, Tk, generator=g)
+    fmask[torch.rand(Tq, Tk, generator=g) < 0.3] = float("-inf")
+    fmask[:, 5] = 0.0
+    bmask = torch.rand(2, 1, Tq, Tk, generator=g) < 0.5
+    lmask = torch.randn(2, 3, Tq, Tk, generator=g)
+    pos_sorted = torch.sort(torch.randperm(200, generator=g)[:Tk]).values
+    pos_sorted[0] = 0
+    pos_perm = pos_sorted[torch.randperm(Tk, generator=g)]
+    qn, kn, vn = (x.double().numpy() for x in (q, k, v))
+    cases = [
+        ("float mask [Tq, Tk] with -inf", dict(mask=fmask.to(dt)), dict(mask=fmask.to(dt).double().numpy())),
+        ("bool mask [2, 1, Tq, Tk]", dict(mask=bmask), dict(mask=bmask.numpy())),
+        ("mask per (b, h)", dict(mask=lmask.to(dt)), dict(mask=lmask.to(dt).double().numpy())),
+        ("causal, sorted positions", dict(causal=True, original_kv_positions=pos_sorted),
+         dict(causal=True, original_kv_positions=pos_sorted.numpy())),
+        ("causal, unsorted positions", dict(causal=True, original_kv_positions=pos_perm),
+         dict(causal=True, original_kv_positions=pos_perm.numpy())),
+        ("causal, positions and mask", dict(causal=True, original_kv_positions=pos_perm, mask=fmask.to(dt)),
+         dict(causal=True, original_kv_positions=pos_perm.numpy(), mask=fmask.to(dt).double().numpy())),
+        ("positions without causal", dict(original_kv_positions=pos_perm), dict()),
+    ]
+    for what, kw, okw in cases:
+        kw = {n: (t(x) if isinstance(x, torch.Tensor) else x) for n, x in kw.items()}
+        out = dense_attention(t(q), t(k), t(v), **kw)
+        torch.cuda.synchronize()
+        assert out.shape == (2, 3, Tq, 48) and out.dtype == dt
+        _cmp(out, A.dense_attention_masked(qn, kn, vn, **okw), dt, what)
+    # k / v shared by every batch entry (leading dims broadcast as in torch.matmul)
+    out = dense_attention(t(q), t(k[:1]), t(v[:1]), mask=t(fmask.to(dt)))
+    _cmp(out, A.dense_attention_masked(qn, kn[:1], vn[:1], mask=fmask.to(dt).double().numpy()), dt, "broadcast k / v")
+    # every key of query 0 masked: NaN, as torch's softmax gives; the other rows finite
+    allm = torch.zeros(Tq, Tk)
+    allm[0] = float("-inf")
+    out = dense_attention(t(q), t(k), t(v), mask=t(allm.to(dt)))
+    torch.cuda.synchronize()
+    assert torch.isnan(out[..., 0, :]).all() and not torch.isnan(out[..., 1:, :]).any()
+    _cmp(out, A.dense_attention_masked(qn, kn, vn, mask=allm.to(dt).double().numpy()), dt, "all-masked row")
+
+
+@pytest.mark.gpu
+def test_reference_causal_attention_cases():
+    """The reference's tests/test_causal_attention.py cases on device tensors: the
+    relations it asserts (semantic == dense with original positions, 1e-5) plus
+    each output against the float64 oracle."""
+    from intent_attention import BlockLayout, BlockPolicy, SemanticBlock, dense_attention, semantic_block_attention
+    dev = torch.device("cuda:0")
+    _say("reference test_causal_attention cases")
+    g = torch.Generator().manual_seed(0)
+    r = lambda *s: torch.randn(*s, generator=g).to(dev)  # noqa: E731
+    S, BP = SemanticBlock, BlockPolicy
+
+    def check(out, ref_np, what):
+        err = float(np.abs(out.cpu().double().numpy() - ref_np).max())
+        _say(f"  {what}: max abs err vs float64 {err:.2e}")
+        assert not torch.isnan(out).any() and err <= 2e-5
+
+    def npy(*xs):
+        return [x.cpu().double().numpy() for x in xs]
+
+    # identical layout: causal selected == dense causal
+    q, k, v = r(2, 4, 8, 64), r(2, 4, 32, 64), r(2, 4, 32, 64)
+    d = dense_attention(q, k, v, causal=True)
+    sel, dbg = semantic_block_attention(q, k, v, BlockLayout([S("all", 0, 32, BP.ALWAYS)]), causal=True,
+                                        return_debug=True)
+    assert torch.allclose(d, sel, atol=1e-5)
+    check(d, A.dense_attention_masked(*npy(q, k, v), causal=True), "identical layout")
+    # prevents future attention, skip middle, non-contiguous masking: semantic == dense with positions
+    for Tk, blocks, idx in (
+            (12, [S("b", 0, 10, BP.ALWAYS)], list(range(10))),
+            (16, [S("first", 0, 4, BP.ALWAYS), S("skip", 4, 10, BP.SKIP), S("last", 10, 16, BP.ALWAYS)],
+             [0, 1, 2, 3, 10, 11, 12, 13, 14, 15]),
+            (12, [S("early", 0, 3, BP.ALWAYS), S("late", 8, 12, BP.ALWAYS)], [0, 1, 2, 8, 9, 10, 11])):
+        q, k, v = r(1, 1, 6, 8), r(1, 1, Tk, 8), r(1, 1, Tk, 8)
+        out, _ = semantic_block_attention(q, k, v, BlockLayout(blocks), causal=True, return_debug=True)
+        ix = torch.tensor(idx, device=dev)
+        od = dense_attention(q, k.index_select(-2, ix), v.index_select(-2, ix), causal=True, original_kv_positions=ix)
+        assert torch.allclose(out, od, atol=1e-5)
+        qn, kn, vn = npy(q, k, v)
+        check(out, A.dense_attention_masked(qn, kn[..., idx, :], vn[..., idx, :], causal=True,
+                                            original_kv_positions=np.array(idx)), f"positions {idx}")
+    # every query has visible keys
+    q, k, v = r(1, 1, 4, 8), r(1, 1, 8, 8), r(1, 1, 8, 8)
+    out, _ = semantic_block_attention(q, k, v, BlockLayout([S("early", 0, 3, BP.ALWAYS), S("late", 3, 8, BP.ALWAYS)]),
+                                      causal=True, return_debug=True)
+    assert not torch.isnan(out).any()
+    # decode step: one query at position 0
+    q, k, v = r(1, 1, 1, 8), r(1, 1, 16, 8), r(1, 1, 16, 8)
+    out, _ = semantic_block_attention(q, k, v, BlockLayout([S("b", 0, 16, BP.ALWAYS)]), causal=True,
+                                      return_debug=True)
+    assert torch.allclose(out, dense_attention(q, k, v, causal=True), atol=1e-5)
+    check(out, A.dense_attention_masked(*npy(q, k, v), causal=True), "decode step")
+    # all blocks selected (ATTEND with a score)
+    q, k, v = r(2, 4, 16, 64), r(2, 4, 64, 64), r(2, 4, 64, 64)
+    lay = BlockLayout([S("a", 0, 32, BP.ALWAYS), S("b", 32, 64, BP.ATTEND, score=0.9)])
+    o_sel, _ = semantic_block_attention(q, k, v, lay, causal=True, return_debug=True, threshold=0.5)
+    assert torch.allclose(dense_attention(q, k, v, causal=True), o_sel, atol=1e-5)
+    # debug metadata
+    q, k, v = r(1, 1, 4, 8), r(1, 1, 16, 8), r(1, 1, 16, 8)
+    _, dbg = semantic_block_attention(q, k, v, BlockLayout([S("test", 0, 16, BP.ALWAYS)]), causal=True,
+                                      return_debug=True)
+    assert dbg == {"selected_token_count": 16, "selected_block_names": ["test"], "total_kv_tokens": 16,
+                   "selected_kv_tokens": 16}
+
+
+@pytest.mark.gpu
+def test_semantic_block_attention_dynamic_scores():
+    """ATTEND blocks without a score are scored by the cosine probe before
+    validation (reference.py:52-78), the scores land in the blocks and the debug
+    dictionary, and the output is attention over the selected tokens."""
+    from intent_attention import BlockLayout, BlockPolicy as BP, SemanticBlock as S, semantic_block_attention
+    dev = torch.device("cuda:0")
+    _say("semantic_block_attention dynamic scores")
+    g = torch.Generator().manual_seed(3)
+    q, k, v = (torch.randn(1, 2, 4, 32, generator=g) for _ in range(3))
+    k = torch.cat([k, torch.randn(1, 2, 44, 32, generator=g)], dim=-2)
+    v = torch.cat([v, torch.randn(1, 2, 44, 32, generator=g)], dim=-2)
+    mk = lambda: BlockLayout([S("sys", 0, 8, BP.ALWAYS), S("d1", 8, 24, BP.ATTEND), S("d2", 24, 40, BP.ATTEND),  # noqa
+                              S("d3", 40, 48, BP.ATTEND, 0.7)])
+    lay = mk()
+    out, dbg = semantic_block_attention(q.to(dev), k.to(dev), v.to(dev), lay, return_debug=True)
+    torch.cuda.synchronize()
+    ref_scores = A.dynamic_block_scores(q.numpy(), k.numpy(), mk())
+    assert set(dbg["dynamic_scores"]) == {"d1", "d2"}
+    for n, s in ref_scores.items():
+        assert abs(dbg["dynamic_scores"][n] - s) <= 1e-5
+        assert lay.blocks[[b.name for b in lay.blocks].index(n)].score == dbg["dynamic_scores"][n]
+    ref = A.dense_attention_masked(q.double().numpy(), k.double().numpy(), v.double().numpy())
+    err = float(np.abs(out.cpu().double().numpy() - ref).max())
+    _say(f"  scores {dbg['dynamic_scores']}, max abs err {err:.2e}")
+    assert err <= 2e-5
+
+
+@pytest.mark.gpu
+def test_compare_function_returns_expected_keys():
+    """The reference's test_compare_function_returns_expected_keys on device tensors,
+    plus the values against the float64 oracle: the quantised output (through the
+    golden-pinned fake quantisation) against attention over the selected tokens."""
+    from intent_attention import (BlockLayout, BlockPolicy as BP, IntentQuantizer, SemanticBlock as S,
+                                  compare_intent_quant_to_fp16_selected)
+    dev = torch.device("cuda:0")
+    _say("compare_intent_quant_to_fp16_selected")
+    g = torch.Generator().manual_seed(9)
+    q, k, v = (torch.randn(1, 2, 8 if i == 0 else 64, 32, generator=g) for i in range(3))
+    lay = BlockLayout([S("always", 0, 16, BP.ALWAYS), S("attend_high", 16, 32, BP.ATTEND, score=0.9),
+                       S("attend_low", 32, 48, BP.ATTEND, score=0.3), S("skip", 48, 64, BP.SKIP)])
+    res = compare_intent_quant_to_fp16_selected(q.to(dev), k.to(dev), v.to(dev), lay,
+                                                IntentQuantizer(memory_pressure=0.4))
+    assert {"output_mse", "output_cosine_similarity", "bytes_saved_pct", "precision_by_block"} <= set(res)
+    assert res["bytes_saved_pct"] >= 0.0
+    assert res["fp16_selected_tokens"] == res["quant_selected_tokens"] == 48
+    assert set(res) == {"output_mse", "output_cosine_similarity", "output_max_abs_error", "fp16_selected_tokens",
+                        "quant_selected_tokens", "estimated_fp16_bytes", "estimated_quant_bytes", "bytes_saved_pct",
+                        "precision_by_block", "reconstruction_mse_k", "reconstruction_mse_v"}
+    olay = P.BlockLayout([P.SemanticBlock(b.name, b.start, b.end, b.policy.value, b.score) for b in lay.blocks])
+    oq = P.IntentQuantizer(memory_pressure=0.4)
+    assert res["precision_by_block"] == {b.name: oq.assign_block_precision(b).precision
+                                         for b in olay.selected_blocks()}
+    qn, kn, vn = (x.numpy() for x in (q, k, v))
+    fp16 = A.semantic_block_attention(qn, kn, vn, olay)
+    quant = A.intent_quant_attention_reference(qn, kn, vn, olay, oq)
+    d = fp16 - quant
+    mse, mx = float((d ** 2).mean()), float(np.abs(d).max())
+    _say(f"  output_mse {res['output_mse']:.3e} (oracle {mse:.3e}), max abs {res['output_max_abs_error']:.3e} "
+         f"(oracle {mx:.3e}), bytes saved {res['bytes_saved_pct']} %")
+    assert abs(res["output_mse"] - mse) <= 0.02 * mse + 1e-9
+    assert abs(res["output_max_abs_error"] - mx) <= 0.02 * mx + 1e-6
+    assert 0.0 < res["output_cosine_similarity"] <= 1.0 + 1e-6
