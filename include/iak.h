@@ -129,9 +129,11 @@ enum { IAK_DTYPE_F16 = 0, IAK_DTYPE_F32 = 1, IAK_DTYPE_BF16 = 2 };
  *                reduce four consecutive splits of one row (the split count is rounded up
  *                to a multiple of four) and combine them in LDS into one partial; the
  *                workgroup that arrives last at the row's arrival counter merges the row's
- *                partials into the output. The counters live at the end of the workspace:
- *                they must be zero before a workspace's first use, and every call leaves
- *                them zero (iak_paged_decode_noalloc ignores this field).
+ *                partials into the output. The counters live at the end of the workspace,
+ *                after the partials, so their offset depends on the plan: they must be zero
+ *                before a workspace's first use and again whenever a call with another plan
+ *                (shape or split count) reuses it; every call leaves its own counters zero
+ *                (iak_paged_decode_noalloc ignores this field).
  *   page_desc    NULL, or [num_pages] 32-byte page descriptors (32-byte aligned) written by
  *                iak_pack_page_descriptors: the page's native tag and scales in one line, read
  *                instead of page_tags, tag_map and the scale arrays (which may then be NULL;

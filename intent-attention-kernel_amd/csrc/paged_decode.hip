@@ -625,6 +625,15 @@ __device__ void merge_in_kernel(const KArgs& a, const Split& sp, const Wave<D, Q
   if (t == 0) last = atomicAdd(a.counters + row, 1) == nwg - 1;
   __syncthreads();
   if (!last) return;
+  // Acquire side of the handoff: drop any stale copy of the partials from this
+  // workgroup's caches before reading them (a cache invalidate; the partials
+  // themselves are also read with sc1 loads). The release side has no fence:
+  // an agent-scope release is a write-back of the whole L2 (it doubled the cfg3
+  // step); the partials are written through to memory instead (sc1 atomic
+  // stores, acknowledged by the vmcnt wait before the barrier above), which is
+  // gfx950's behaviour for agent-scope atomic stores, not a guarantee of the
+  // HIP memory model.
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 
   // the row's merge: output (head h, dim d) from the nwg workgroup partials,
   // OU outputs per thread and U partials per batch with every load of a batch

@@ -10,6 +10,8 @@ missing libiak.so raise.
 from __future__ import annotations
 
 import math
+import weakref
+from collections import OrderedDict
 from dataclasses import dataclass, fields
 from typing import Dict, Optional, Sequence
 
@@ -152,9 +154,18 @@ def make_plan(q: torch.Tensor, pools: PagePools, page_table: torch.Tensor, page_
               valid_tokens: Optional[torch.Tensor] = None,
               merge_in_kernel: Optional[bool] = None,
               page_descriptors: Optional[torch.Tensor] = None,
-              entry_records: Optional[torch.Tensor] = None) -> "DecodePlan":
+              entry_records: Optional[torch.Tensor] = None,
+              auto_records: bool = True) -> "DecodePlan":
     """Validate the arguments of ``paged_decode`` once; the returned plan
     re-launches the decode on the same tensors with ``run()``.
+
+    ``auto_records`` (default on): when ``run()`` finds the page table, the
+    tags and the scale tensors unchanged since the previous run (torch's
+    version counters of those tensors), it packs entry records once and reads
+    them from then on, until one of those tensors changes; results are
+    bit-identical either way. Tensors written other than by torch's in-place
+    ops must be marked (``torch.autograd.graph.increment_version``) or the
+    plan told (``invalidate_records``): this package's own writers do so.
 
     ``page_descriptors`` (optional): [num_pages, 8] int32 descriptors from
     ``DecodePlan.pack_descriptors`` (or ``pack_page_descriptors``), read in
@@ -176,6 +187,8 @@ def make_plan(q: torch.Tensor, pools: PagePools, page_table: torch.Tensor, page_
     if page_tags.dim() != 1:
         raise ValueError(f"page_precision must have shape [num_pages], got {tuple(page_tags.shape)}")
     NP = int(page_tags.shape[0])
+    in_ptrs = (page_table.data_ptr(), page_counts.data_ptr(), page_tags.data_ptr(),
+               valid_tokens.data_ptr() if valid_tokens is not None else None)
     extra = () if valid_tokens is None else (valid_tokens,)
     dev = require_device(q, page_table, page_counts, page_tags, *extra, *pools.tensors().values())
     if valid_tokens is not None:
@@ -259,10 +272,17 @@ def make_plan(q: torch.Tensor, pools: PagePools, page_table: torch.Tensor, page_
     a.merge_in_kernel = MERGE_IN_KERNEL_AUTO if merge_in_kernel is None else (1 if merge_in_kernel else 0)
 
     plan = DecodePlan(a, dev, out, keep=(q, page_table, page_counts, page_tags, valid_tokens, pools))
+    plan.reads_in_place = (page_table.data_ptr() == in_ptrs[0] and page_counts.data_ptr() == in_ptrs[1]
+                           and page_tags.data_ptr() == in_ptrs[2]
+                           and (valid_tokens is None or valid_tokens.data_ptr() == in_ptrs[3]))
     if page_descriptors is not None:
         plan.use_descriptors(page_descriptors)
     if entry_records is not None:
         plan.use_records(entry_records)
+    if auto_records and page_descriptors is None and entry_records is None and W > 0:
+        scales = [getattr(pools, n) for n in ("k_fp8_scale", "v_fp8_scale", "k_int8_scale", "v_int8_scale",
+                                              "k_int4_scale", "v_int4_scale", "k_int4r_scale", "v_int4r_scale")]
+        plan._track = tuple(weakref.ref(t) for t in (page_table, page_tags, *scales) if t is not None)
     return plan
 
 
@@ -314,6 +334,13 @@ class DecodePlan:
             self._filled.record(torch.cuda.current_stream(device))
         self._desc: Optional[torch.Tensor] = None
         self._recs: Optional[torch.Tensor] = None
+        # automatic entry records: the tensors the records snapshot, the state
+        # (their version counters) of the last run, and that of the packed records
+        self._track: tuple = ()
+        self._last_state: Optional[tuple] = None
+        self._auto_recs: Optional[torch.Tensor] = None
+        self._auto_state: Optional[tuple] = None
+        self.reads_in_place = False   # table, counts, tags (and token bounds) read where the caller keeps them
 
     def pack_descriptors(self, out: Optional[torch.Tensor] = None, stream: Optional[int] = None) -> torch.Tensor:
         """Pack this plan's page tags (through its tag map), and the scales each
@@ -344,12 +371,16 @@ class DecodePlan:
         if out is None:
             out = torch.empty(shape, dtype=torch.int32, device=self.device)
         self._check_records(out)
+        self._track = ()     # records given by the caller: no automatic ones
+        self._pack_records_into(out, stream)
+        return out
+
+    def _pack_records_into(self, out: torch.Tensor, stream: Optional[int]) -> None:
         s = torch.cuda.current_stream(self.device).cuda_stream if stream is None else stream
         saved = (self.args.page_desc, self.args.entry_records)
         N.pack_entry_records(self.args, out.data_ptr(), s)
         self.args.page_desc, self.args.entry_records = saved
-        self.use_records(out)
-        return out
+        self._set_records(out)
 
     def _check_records(self, recs: torch.Tensor) -> None:
         shape = self._records_shape()
@@ -360,7 +391,12 @@ class DecodePlan:
 
     def use_records(self, recs: Optional[torch.Tensor]) -> None:
         """Read ``recs`` (packed for this plan's table, pages and pools) in place
-        of the table entries, tags, tag map and scales; None goes back to them."""
+        of the table entries, tags, tag map and scales; None goes back to them.
+        Either way the plan stops packing records by itself."""
+        self._track = ()
+        self._set_records(recs)
+
+    def _set_records(self, recs: Optional[torch.Tensor]) -> None:
         if recs is not None:
             self._check_records(recs)
         self._recs = recs
@@ -368,9 +404,14 @@ class DecodePlan:
 
     def use_descriptors(self, desc: Optional[torch.Tensor]) -> None:
         """Read ``desc`` (packed for the same pages and pools) in place of the
-        tags, tag map and scales; None goes back to them."""
+        tags, tag map and scales; None goes back to them. The plan stops
+        packing entry records by itself."""
         if desc is not None:
             _check_descriptors(desc, int(self.args.num_pages), self.device)
+        self._track = ()
+        if self._auto_state is not None:
+            self._set_records(None)
+            self._auto_state = None
         self._desc = desc
         self.args.page_desc = desc.data_ptr() if desc is not None else None
 
@@ -381,5 +422,106 @@ class DecodePlan:
         if self._filled is not None:
             torch.cuda.ExternalStream(s, device=self.device).wait_event(self._filled)
             self._filled = None
+        if self._track:
+            self._auto_records(s)
         ev = None if events is None else (events[0].cuda_event, events[1].cuda_event)
         N.paged_decode(self.args, self._ws.data_ptr() if self._ws is not None else 0, self.workspace_bytes, s, ev)
+
+    def _auto_records(self, stream: int) -> None:
+        """Read packed entry records while the table, tags and scales stay as they
+        were: packed (on ``stream``) at the second run that finds them unchanged,
+        dropped as soon as one of them changes. The record buffer is the plan's
+        for its lifetime and is packed again in place."""
+        tensors = [r() for r in self._track]
+        if any(t is None for t in tensors):   # a tracked tensor is gone: this plan is not reused
+            self._track = ()
+            return
+        state = tuple(t._version for t in tensors)
+        if self._auto_state is not None and state != self._auto_state:
+            self._set_records(None)
+            self._auto_state = None
+        if self._auto_state is None and state == self._last_state:
+            if self._auto_recs is None:
+                self._auto_recs = torch.empty(self._records_shape(), dtype=torch.int32, device=self.device)
+            self._pack_records_into(self._auto_recs, stream)
+            self._auto_state = state
+        self._last_state = state
+
+    def invalidate_records(self) -> None:
+        """Forget the automatically packed entry records (the table, tags or
+        scales were written by means torch's version counters do not see)."""
+        if self._auto_state is not None:
+            self._set_records(None)
+        self._auto_state = None
+        self._last_state = None
+
+    def run_with(self, q: torch.Tensor, out: torch.Tensor) -> None:
+        """Run on the current stream with another query and output of the plan's
+        shape and dtypes: q and out [B, Hq, D] or [B, Hq, 1, D], out with a unit
+        last stride. A query the kernel cannot read in place (misaligned) is
+        copied first."""
+        a = self.args
+        want = (a.batch, a.num_q_heads, a.head_dim)
+        for name, t, dt in (("q", q, a.q_dtype), ("out", out, a.out_dtype)):
+            shp = tuple(t.shape)
+            if ((shp != want and shp != (want[0], want[1], 1, want[2])) or _DT.get(t.dtype) != dt
+                    or t.device != self.device):
+                raise ValueError(f"{name} must be {want} (or [B, H, 1, D]) of the plan's dtype and device, "
+                                 f"got {t.dtype} {shp}")
+        if out.stride(-1) != 1:
+            raise ValueError("out must have a unit last stride")
+        qvec = 4 if q.dtype == torch.float32 else 8
+        if q.stride(-1) != 1 or q.data_ptr() % 16 or q.stride(0) % qvec or q.stride(1) % qvec:
+            q = torch.empty(q.shape, dtype=q.dtype, device=q.device).copy_(q)
+        a.q, a.q_stride_b, a.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
+        a.out, a.out_stride_b, a.out_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
+        self.out = out
+        self.run()
+
+    @property
+    def reads_records(self) -> bool:
+        """True when the next run reads entry records (packed by ``pack_records``
+        or automatically)."""
+        return self._recs is not None
+
+
+class PlanCache:
+    """Decode plans of repeated calls over the same pool, table and tag tensors,
+    for the reference entry points (which validate and allocate on every call).
+
+    A plan is found by the identity of its key tensors (held as weak
+    references, so the cache keeps no pool alive) plus the call's other
+    settings; each hit re-points the plan at the call's query and output
+    (``DecodePlan.run_with``). Only plans that read the caller's tensors in
+    place are cached: a plan that had to copy one (non-contiguous metadata)
+    would not see later writes to it. At most ``size`` plans, least recently
+    used first out."""
+
+    def __init__(self, size: int = 8) -> None:
+        self.size = size
+        self._d: "OrderedDict[tuple, tuple]" = OrderedDict()
+
+    def clear(self) -> None:
+        self._d.clear()
+
+    def get(self, tensors: tuple, extra: tuple) -> Optional["DecodePlan"]:
+        key = (tuple(map(id, tensors)), extra)
+        ent = self._d.get(key)
+        if ent is None:
+            return None
+        refs, plan = ent
+        for r, t in zip(refs, tensors):
+            if (r() if r is not None else None) is not t:
+                del self._d[key]
+                return None
+        self._d.move_to_end(key)
+        return plan
+
+    def put(self, tensors: tuple, extra: tuple, plan: "DecodePlan") -> None:
+        if not plan.reads_in_place:
+            return
+        plan._keep = ()        # the caller's tensors: weak references only
+        self._d[(tuple(map(id, tensors)), extra)] = (
+            tuple(weakref.ref(t) if t is not None else None for t in tensors), plan)
+        while len(self._d) > self.size:
+            self._d.popitem(last=False)

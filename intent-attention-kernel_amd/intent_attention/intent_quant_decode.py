@@ -27,7 +27,7 @@ from typing import Optional, Tuple
 import torch
 
 from . import _native as N
-from .decode_core import PagePools, paged_decode
+from .decode_core import PagePools, PlanCache, make_plan
 
 
 class TritonKVPrecision(IntEnum):
@@ -146,6 +146,17 @@ def intent_quant_decode_attention_triton(
         raise ValueError("page_ids width must match config.max_selected_pages")
     if out is None:
         out = torch.empty_like(q)
+    tensors = (k_pages_fp16, v_pages_fp16, k_pages_i8, v_pages_i8, k_i8_scales, v_i8_scales, page_ids, page_count,
+               page_precision)
+    if native_pools is not None:
+        tensors += tuple(getattr(native_pools, n) for n in _NATIVE_FIELDS)
+    extra = (bsz, heads, dim, q.dtype, out.dtype, q.device, cfg, pages_per_split,
+             None if native_pools is None else native_pools.int4_group)
+    plan = _PLANS.get(tensors, extra)
+    if plan is not None:
+        # the same pools, ids, counts and tags as an earlier call: only q and out are new
+        plan.run_with(q, out)
+        return out
 
     pools = PagePools(k_fp16=k_pages_fp16, v_fp16=v_pages_fp16, k_int8=k_pages_i8, v_int8=v_pages_i8,
                       k_int8_scale=k_i8_scales, v_int8_scale=v_i8_scales)
@@ -160,9 +171,23 @@ def intent_quant_decode_attention_triton(
                                (TritonKVPrecision.INT4_RESIDUAL, N.TAG_INT4_RESIDUAL)):
             if pools.has(native):
                 tag_map[int(caller)] = native
-    return paged_decode(q, pools, page_ids, page_count, page_precision, tag_map=tag_map,
-                        negative_ids=False, sm_scale=1.0 / math.sqrt(dim), out=out,
-                        pages_per_split=pages_per_split, map_other_tags=True)
+    plan = make_plan(q, pools, page_ids, page_count, page_precision, tag_map=tag_map,
+                     negative_ids=False, sm_scale=1.0 / math.sqrt(dim), out=out,
+                     pages_per_split=pages_per_split, map_other_tags=True)
+    plan.run()
+    _PLANS.put(tensors, extra, plan)
+    return out
+
+
+_NATIVE_FIELDS = ("k_fp8", "v_fp8", "k_fp8_scale", "v_fp8_scale", "k_int4", "v_int4", "k_int4_scale",
+                  "v_int4_scale", "k_int4r", "v_int4r", "k_int4r_scale", "v_int4r_scale")
+# validated plans of earlier calls (decode_core.PlanCache); clear_plan_cache() empties it
+_PLANS = PlanCache()
+
+
+def clear_plan_cache() -> None:
+    """Drop the validated plans ``intent_quant_decode_attention_triton`` keeps for repeated calls."""
+    _PLANS.clear()
 
 
 def fake_int8_pages_from_fp16(pages: torch.Tensor, *, eps: float = 1e-6) -> Tuple[torch.Tensor, torch.Tensor]:

@@ -203,6 +203,7 @@ class KVMemoryManager:
         a.pages, a.pool_pages = ids.data_ptr(), fp16.shape[0]
         a.fp16, a.int8, a.scales = fp16.data_ptr(), int8.data_ptr(), scales.data_ptr()
         N.transcode_pages(a, torch.cuda.current_stream(self.device).cuda_stream)
+        torch.autograd.graph.increment_version([fp16, int8, scales])   # written through raw pointers
 
     def _zero_rows(self, pids: Sequence[int]) -> None:
         """Pool rows of pages that hold no data: zero FP16 rows, zero codes, scale 1

@@ -37,6 +37,9 @@ def _launch(pages: torch.Tensor, tag: int, mode: int, codes: torch.Tensor, scale
     a.codes, a.scales = codes.data_ptr(), scales.data_ptr()
     a.scale_dtype = N.DTYPE_F32 if scales.dtype == torch.float32 else N.DTYPE_F16
     N.quantize_pages(a, torch.cuda.current_stream(pages.device).cuda_stream)
+    # the kernel writes through raw pointers: tell torch's version counters (decode
+    # plans that packed these scales into entry records see the change)
+    torch.autograd.graph.increment_version([codes, scales])
 
 
 def _check_pages(pages: torch.Tensor) -> torch.Tensor:

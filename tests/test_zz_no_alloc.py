@@ -4,7 +4,10 @@ a caller workspace and the merge kernel (merge_in_kernel = 0, the form the
 no-alloc entry point always takes), through the C ABI: two calls in a row, the
 second with a smaller input, each bit-identical to the workspace entry point
 (the same kernels and split plan) and within the quantised-page bar of the oracle; a
-call whose partials exceed the scratch is rejected before any launch."""
+call whose partials exceed the scratch is rejected before any launch; and the
+call captured in a HIP graph (after one eager call), replayed three times with
+the query and the page table changed in between, each replay bit-identical to
+iak_paged_decode on the same inputs."""
 import sys
 
 import numpy as np
@@ -21,14 +24,17 @@ def _say(*a):
     sys.stdout.flush()
 
 
-def _case(dev, seed, B, Hq, Hkv, W, NP, pps):
+def _case(dev, seed, B, Hq, Hkv, W, NP, pps, with_tensors=False):
     import torch
     from intent_attention.decode_core import make_plan
     mix = {"FP16": .25, "FP8": .2, "INT8": .2, "INT4": .2, "INT4_RESIDUAL": .15}
     q, pools, table, counts, tags = random_case(seed, B, Hq, Hkv, 128, NP, W, mix, outliers=0.01)
     t = lambda x: torch.from_numpy(x).to(dev)  # noqa: E731
-    plan = make_plan(t(q), to_device_pools(pools, dev), t(table), t(counts), t(tags), out_dtype=torch.float32,
-                     pages_per_split=pps, merge_in_kernel=False)
+    tq, tt = t(q), t(table)
+    plan = make_plan(tq, to_device_pools(pools, dev), tt, t(counts), t(tags), out_dtype=torch.float32,
+                     pages_per_split=pps, merge_in_kernel=False, auto_records=False)
+    if with_tensors:
+        return plan, (q, pools, table, counts, tags), (tq, tt)
     return plan, (q, pools, table, counts, tags)
 
 
@@ -71,3 +77,39 @@ def test_noalloc_rejects_partials_above_the_scratch():
     assert plan.workspace_bytes > N.NOALLOC_SCRATCH_BYTES
     with pytest.raises(ValueError, match="no-alloc scratch"):
         N.paged_decode_noalloc(plan.args, torch.cuda.current_stream(dev).cuda_stream)
+
+
+def test_noalloc_under_graph_capture():
+    import torch
+    from intent_attention import _native as N
+    dev = torch.device("cuda:0")
+    _say("noalloc graph capture: seed=63 B=3 Hq=16 Hkv=4 W=120")
+    plan, host, (tq, tt) = _case(dev, 63, 3, 16, 4, 120, 96, 16, with_tensors=True)
+    assert 0 < plan.workspace_bytes <= N.NOALLOC_SCRATCH_BYTES
+    # eager call first: the scratch address of this GPU is looked up outside the capture
+    N.paged_decode_noalloc(plan.args, torch.cuda.current_stream(dev).cuda_stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        N.paged_decode_noalloc(plan.args, torch.cuda.current_stream(dev).cuda_stream)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(7)
+    for rep in range(3):
+        if rep == 1:       # new query values in place
+            tq.copy_(torch.from_numpy(rng.standard_normal(tuple(tq.shape)).astype(np.float16)).to(dev))
+        if rep == 2:       # a new page table in place
+            tt.copy_(torch.from_numpy(rng.integers(0, 96, size=tuple(tt.shape)).astype(np.int32)).to(dev))
+        plan.out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = plan.out.clone()
+        plan.out.fill_(float("nan"))
+        plan.run()          # iak_paged_decode with the caller's workspace, eager
+        torch.cuda.synchronize()
+        same = torch.equal(got, plan.out)
+        _say(f"  replay {rep}: bit-identical to iak_paged_decode {same}")
+        assert same and not torch.isnan(got).any()
+    ref = Dm.paged_decode_oracle(tq.cpu().numpy(), host[1], tt.cpu().numpy(), host[3], host[4])
+    assert float(np.abs(got.cpu().numpy() - ref).max()) <= 1e-2
+    del g
