@@ -281,32 +281,43 @@ def build_workload(name: str, device: torch.device, seed: int = 1234, chunk_page
 # decode kernel's sources it was measured on (kernel_source_digest); a build whose
 # sources differ reports traffic null (stale) until the counters are run again.
 MEASURED_TRAFFIC = {
-    "cfg3": {"bytes": 2_105_525_407 + 5_054_464, "src": "f8105d4ff5579d3b",
+    "cfg3": {"bytes": 2_105_410_636 + 5_054_464, "src": "4a40bfc181a9e975",
              "source": "profiles/paged_decode_cfg3_hbm_traffic.txt"},
-    "cfg4": {"bytes": 189_782_532 + 2_129_920, "src": "f8105d4ff5579d3b",
+    "cfg4": {"bytes": 189_782_173 + 2_129_920, "src": "4a40bfc181a9e975",
              "source": "profiles/paged_decode_cfg4_kernel_stats.txt"},
     # the same decodes reading 32-byte page descriptors (--page-descriptors) or
     # 32-byte entry records (--entry-records)
-    "cfg3-desc": {"bytes": 2_080_271_186 + 5_054_464, "src": "f8105d4ff5579d3b",
+    "cfg3-desc": {"bytes": 2_080_208_921 + 5_054_464, "src": "4a40bfc181a9e975",
                   "source": "profiles/paged_decode_cfg3_hbm_traffic.txt"},
-    "cfg4-desc": {"bytes": 182_747_286 + 2_129_920, "src": "f8105d4ff5579d3b",
+    "cfg4-desc": {"bytes": 182_747_550 + 2_129_920, "src": "4a40bfc181a9e975",
                   "source": "profiles/paged_decode_cfg4_kernel_stats.txt"},
-    "cfg3-records": {"bytes": 2_005_563_668 + 5_054_464, "src": "f8105d4ff5579d3b",
+    "cfg3-records": {"bytes": 2_005_600_819 + 5_054_464, "src": "4a40bfc181a9e975",
                      "source": "profiles/paged_decode_cfg3_hbm_traffic.txt"},
-    "cfg4-records": {"bytes": 178_927_947 + 2_129_920, "src": "f8105d4ff5579d3b",
+    "cfg4-records": {"bytes": 178_928_491 + 2_129_920, "src": "4a40bfc181a9e975",
                      "source": "profiles/paged_decode_cfg4_kernel_stats.txt"},
 }
 KERNEL_SOURCES = ("paged_decode.hip", "iak_device.h", "iak_internal.h")
+MLA_KERNEL_SOURCES = ("mla_decode.hip", "iak_device.h", "iak_internal.h")
 
 
-def kernel_source_digest() -> str:
-    """sha256 (first 16 hex digits) of the decode kernel's source files."""
+def source_digest(files) -> str:
+    """sha256 (first 16 hex digits) of the named csrc source files, in order."""
     import hashlib
     h = hashlib.sha256()
-    for f in KERNEL_SOURCES:
+    for f in files:
         with open(os.path.join(ROOT, "intent-attention-kernel_amd", "csrc", f), "rb") as fh:
             h.update(fh.read())
     return h.hexdigest()[:16]
+
+
+def kernel_source_digest() -> str:
+    """Digest of the decode kernel's source files (profiles/ summaries name it)."""
+    return source_digest(KERNEL_SOURCES)
+
+
+def mla_source_digest() -> str:
+    """Digest of the MLA kernel's source files (profiles/ summaries name it)."""
+    return source_digest(MLA_KERNEL_SOURCES)
 
 
 def measured_traffic(config: str):
@@ -539,6 +550,7 @@ def run_mla(args, cpu=None) -> None:
         "roofline": {"bound": "mfma", "achieved": round(kernel_tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(kernel_tflops / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None,
                      "kernel": "mla_decode_kernel", "kernel_us": round(kernel_ms * 1e3, 2),
+                     "kernel_source_digest": mla_source_digest(),
                      "step_frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
                      "hbm_gbps": round(cost["bytes"] / (kernel_ms * 1e-3) / 1e9, 1)},
     }
@@ -1214,6 +1226,7 @@ def run_decode(args, cpu=None) -> None:
                      "frac": round(kernel_gbps / HBM_PEAK_GBPS, 4),
                      "traffic": measured_traffic(traffic_key)[0],
                      "kernel": "paged_decode_kernel", "kernel_us": round(kernel_ms * 1e3, 2),
+                     "kernel_source_digest": kernel_source_digest(),
                      "kernel_bytes": kernel_bytes, "kernel_metadata_format": kernel_fmt,
                      "step_frac": round(achieved / HBM_PEAK_GBPS, 4)},
     }

@@ -569,8 +569,11 @@ __device__ void write_result(const KArgs& a, const Split& sp, Wave<D, QT != IAK_
 // and read with agent-scope atomic stores and loads, which the L2 writes
 // through to memory and re-reads from it (the sc1 scope bit), and the stores
 // are acknowledged (s_waitcnt vmcnt(0)) before the barrier that precedes the
-// arrival. No agent-scope fence is used: its release half writes back the
-// whole L2 (buffer_wbl2), which took the cfg3 decode from 333 to 645 us.
+// arrival. No agent-scope release fence is used: it writes back the whole L2
+// (buffer_wbl2), which took the cfg3 decode from 333 to 645 us; the merging
+// workgroup takes an agent-scope acquire (buffer_inv sc1, a cache invalidate)
+// after it sees the last arrival. The release side therefore rests on gfx950's
+// write-through of sc1 atomic stores, not on the HIP memory model.
 // `red`: LDS [4 waves][16 heads][D] floats (the K transpose buffers, done with).
 template <int D, int QT>
 __device__ void merge_in_kernel(const KArgs& a, const Split& sp, const Wave<D, QT != IAK_DTYPE_F16>& w, int c,
