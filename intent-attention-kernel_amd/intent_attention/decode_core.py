@@ -10,6 +10,7 @@ missing libiak.so raise.
 from __future__ import annotations
 
 import math
+import threading
 import weakref
 from collections import OrderedDict
 from dataclasses import dataclass, fields
@@ -340,6 +341,8 @@ class DecodePlan:
         self._last_state: Optional[tuple] = None
         self._auto_recs: Optional[torch.Tensor] = None
         self._auto_state: Optional[tuple] = None
+        self._auto_stream: Optional[int] = None   # the stream every automatic pack and read runs on
+        self._lock = threading.Lock()             # run_with: one caller at a time re-points the arguments
         self.reads_in_place = False   # table, counts, tags (and token bounds) read where the caller keeps them
 
     def pack_descriptors(self, out: Optional[torch.Tensor] = None, stream: Optional[int] = None) -> torch.Tensor:
@@ -431,11 +434,18 @@ class DecodePlan:
         """Read packed entry records while the table, tags and scales stay as they
         were: packed (on ``stream``) at the second run that finds them unchanged,
         dropped as soon as one of them changes. The record buffer is the plan's
-        for its lifetime and is packed again in place."""
+        for its lifetime and is packed again in place, so every pack and every
+        run that reads it stay on one stream: a run on another stream turns the
+        automatic records off for this plan."""
         tensors = [r() for r in self._track]
-        if any(t is None for t in tensors):   # a tracked tensor is gone: this plan is not reused
+        if any(t is None for t in tensors) or (self._auto_stream is not None and stream != self._auto_stream):
+            # a tracked tensor is gone, or the plan moved to another stream
             self._track = ()
+            if self._auto_state is not None:
+                self._set_records(None)
+                self._auto_state = None
             return
+        self._auto_stream = stream
         state = tuple(t._version for t in tensors)
         if self._auto_state is not None and state != self._auto_state:
             self._set_records(None)
@@ -473,10 +483,11 @@ class DecodePlan:
         qvec = 4 if q.dtype == torch.float32 else 8
         if q.stride(-1) != 1 or q.data_ptr() % 16 or q.stride(0) % qvec or q.stride(1) % qvec:
             q = torch.empty(q.shape, dtype=q.dtype, device=q.device).copy_(q)
-        a.q, a.q_stride_b, a.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
-        a.out, a.out_stride_b, a.out_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
-        self.out = out
-        self.run()
+        with self._lock:   # the argument block is shared: set it and launch as one step
+            a.q, a.q_stride_b, a.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
+            a.out, a.out_stride_b, a.out_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
+            self.out = out
+            self.run()
 
     @property
     def reads_records(self) -> bool:
@@ -491,11 +502,12 @@ class PlanCache:
 
     A plan is found by the identity of its key tensors (held as weak
     references, so the cache keeps no pool alive) plus the call's other
-    settings; each hit re-points the plan at the call's query and output
-    (``DecodePlan.run_with``). Only plans that read the caller's tensors in
-    place are cached: a plan that had to copy one (non-contiguous metadata)
-    would not see later writes to it. At most ``size`` plans, least recently
-    used first out."""
+    settings, the current stream among them (a plan's workspace is reused by
+    every run, which is safe only in one stream's order); each hit re-points
+    the plan at the call's query and output (``DecodePlan.run_with``). Only
+    plans that read the caller's tensors in place are cached: a plan that had
+    to copy one (non-contiguous metadata) would not see later writes to it.
+    At most ``size`` plans, least recently used first out."""
 
     def __init__(self, size: int = 8) -> None:
         self.size = size

@@ -173,8 +173,9 @@ def fused_selected_quant_decode(
                page_precision, page_counts)
     if native_pools is not None:
         tensors += tuple(getattr(native_pools, n) for n in _NATIVE_FIELDS)
-    extra = (B, H, D, query.dtype, query.device, config, pages_per_split,
-             None if native_pools is None else native_pools.int4_group)
+    stream = torch.cuda.current_stream(query.device).cuda_stream if query.is_cuda else None
+    extra = (B, H, D, query.dtype, query.device, stream, config,
+             pages_per_split, None if native_pools is None else native_pools.int4_group)
     out = torch.empty((B, H, 1, D), dtype=torch.float16, device=query.device)
     plan = _PLANS.get(tensors, extra)
     if plan is not None:

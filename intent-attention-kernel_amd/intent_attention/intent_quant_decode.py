@@ -150,8 +150,9 @@ def intent_quant_decode_attention_triton(
                page_precision)
     if native_pools is not None:
         tensors += tuple(getattr(native_pools, n) for n in _NATIVE_FIELDS)
-    extra = (bsz, heads, dim, q.dtype, out.dtype, q.device, cfg, pages_per_split,
-             None if native_pools is None else native_pools.int4_group)
+    stream = torch.cuda.current_stream(q.device).cuda_stream if q.is_cuda else None
+    extra = (bsz, heads, dim, q.dtype, out.dtype, q.device, stream, cfg,
+             pages_per_split, None if native_pools is None else native_pools.int4_group)
     plan = _PLANS.get(tensors, extra)
     if plan is not None:
         # the same pools, ids, counts and tags as an earlier call: only q and out are new

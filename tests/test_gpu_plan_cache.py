@@ -178,3 +178,50 @@ def test_reference_api_reuses_plans(dev, api):
     gc.collect()
     assert probe() is None
     mod.clear_plan_cache()
+
+
+def test_streams_keep_plans_apart(dev):
+    """A plan's automatic records stay on the stream that packed them: a run on
+    another stream turns them off (still correct); the reference entry point
+    keeps one plan per stream, since a plan's workspace is reused by every run."""
+    import importlib
+    import torch
+    from intent_attention import FusedDecodeConfig, fused_selected_quant_decode
+    from intent_attention.decode_core import make_plan
+    fmod = importlib.import_module("intent_attention.fused_selected_quant_decode")
+    _say("plans and streams")
+    q, pools, table, counts, tags = _case(303)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)  # noqa: E731
+    dp = to_device_pools(pools, dev)
+    tq, tt, tc, tg = t(q), t(table), t(counts), t(tags)
+    plan = make_plan(tq, dp, tt, tc, tg, out_dtype=torch.float32, pages_per_split=16)
+    plan.run()
+    plan.run()
+    torch.cuda.synchronize()
+    assert plan.reads_records
+    want = plan.out.clone()
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        plan.out.fill_(float("nan"))
+        plan.run()
+    torch.cuda.synchronize()
+    assert not plan.reads_records and torch.equal(plan.out, want)
+
+    fmod.clear_plan_cache()
+    rng = np.random.default_rng(9)
+    B, H, D, NP, W = 1, 2, 64, 24, 12
+    ftags = rng.choice([Dm.FP16, Dm.INT8], size=NP).astype(np.int32)
+    fp = build_pools(rng, NP, D, ftags)
+    args = [t(fp["k_fp16"]), t(fp["v_fp16"]), t(fp["k_i8"]), t(fp["v_i8"]), t(fp["k_i8_scale"]),
+            t(fp["v_i8_scale"]), t(rng.integers(0, NP, size=(B, H, W)).astype(np.int32)), t(ftags),
+            t(np.full((B, H), W, np.int32))]
+    cfg = FusedDecodeConfig(head_dim=D, max_selected_pages=W)
+    qq = t(rng.standard_normal((B, H, 1, D)).astype(np.float16))
+    a = fused_selected_quant_decode(qq, *args, cfg)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        b = fused_selected_quant_decode(qq, *args, cfg)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b) and len(fmod._PLANS._d) == 2
+    fmod.clear_plan_cache()
