@@ -80,6 +80,17 @@ class PagePools:
         return bool(need) and all(getattr(self, n) is not None for n in need)
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def current_stream_handle(device: torch.device) -> int:
+    """The raw hipStream_t of torch's current stream on ``device`` (the cheap lookup
+    when this torch build has it)."""
+    if _raw_stream is not None:
+        return _raw_stream(device.index if device.index is not None else torch.cuda.current_device())
+    return torch.cuda.current_stream(device).cuda_stream
+
+
 def require_device(*tensors: torch.Tensor, what: str = "fused selected-quant decode") -> torch.device:
     """All tensors on one ROCm device, or RuntimeError (no host path exists)."""
     devs = {t.device for t in tensors if isinstance(t, torch.Tensor)}
@@ -421,7 +432,7 @@ class DecodePlan:
     def run(self, stream: Optional[int] = None, events: Optional[tuple] = None) -> None:
         """Launch on ``stream`` (default: torch's current stream). ``events``: an
         optional pair of torch.cuda.Event recorded around the split kernel alone."""
-        s = torch.cuda.current_stream(self.device).cuda_stream if stream is None else stream
+        s = current_stream_handle(self.device) if stream is None else stream
         if self._filled is not None:
             torch.cuda.ExternalStream(s, device=self.device).wait_event(self._filled)
             self._filled = None
@@ -465,11 +476,11 @@ class DecodePlan:
         self._auto_state = None
         self._last_state = None
 
-    def run_with(self, q: torch.Tensor, out: torch.Tensor) -> None:
-        """Run on the current stream with another query and output of the plan's
-        shape and dtypes: q and out [B, Hq, D] or [B, Hq, 1, D], out with a unit
-        last stride. A query the kernel cannot read in place (misaligned) is
-        copied first."""
+    def run_with(self, q: torch.Tensor, out: torch.Tensor, stream: Optional[int] = None) -> None:
+        """Run on ``stream`` (default: torch's current stream) with another query
+        and output of the plan's shape and dtypes: q and out [B, Hq, D] or
+        [B, Hq, 1, D], out with a unit last stride. A query the kernel cannot
+        read in place (misaligned) is copied first."""
         a = self.args
         want = (a.batch, a.num_q_heads, a.head_dim)
         for name, t, dt in (("q", q, a.q_dtype), ("out", out, a.out_dtype)):
@@ -487,7 +498,7 @@ class DecodePlan:
             a.q, a.q_stride_b, a.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
             a.out, a.out_stride_b, a.out_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
             self.out = out
-            self.run()
+            self.run(stream)
 
     @property
     def reads_records(self) -> bool:

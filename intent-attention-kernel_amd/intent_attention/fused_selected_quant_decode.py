@@ -39,7 +39,7 @@ import numpy as np
 import torch
 
 from . import _native as N
-from .decode_core import PagePools, PlanCache, make_plan
+from .decode_core import PagePools, PlanCache, current_stream_handle, make_plan
 
 
 class FusedKVPrecision(IntEnum):
@@ -173,14 +173,14 @@ def fused_selected_quant_decode(
                page_precision, page_counts)
     if native_pools is not None:
         tensors += tuple(getattr(native_pools, n) for n in _NATIVE_FIELDS)
-    stream = torch.cuda.current_stream(query.device).cuda_stream if query.is_cuda else None
+    stream = current_stream_handle(query.device) if query.is_cuda else None
     extra = (B, H, D, query.dtype, query.device, stream, config,
              pages_per_split, None if native_pools is None else native_pools.int4_group)
     out = torch.empty((B, H, 1, D), dtype=torch.float16, device=query.device)
     plan = _PLANS.get(tensors, extra)
     if plan is not None:
         # the same pools, table, tags and counts as an earlier call: only the query and output are new
-        plan.run_with(query, out)
+        plan.run_with(query, out, stream)
         return out
     pools = PagePools(k_fp16=k_pages_fp16, v_fp16=v_pages_fp16, k_int8=k_pages_int8, v_int8=v_pages_int8,
                       k_int8_scale=k_scales, v_int8_scale=v_scales)

@@ -27,7 +27,7 @@ from typing import Optional, Tuple
 import torch
 
 from . import _native as N
-from .decode_core import PagePools, PlanCache, make_plan
+from .decode_core import PagePools, PlanCache, current_stream_handle, make_plan
 
 
 class TritonKVPrecision(IntEnum):
@@ -150,13 +150,13 @@ def intent_quant_decode_attention_triton(
                page_precision)
     if native_pools is not None:
         tensors += tuple(getattr(native_pools, n) for n in _NATIVE_FIELDS)
-    stream = torch.cuda.current_stream(q.device).cuda_stream if q.is_cuda else None
+    stream = current_stream_handle(q.device) if q.is_cuda else None
     extra = (bsz, heads, dim, q.dtype, out.dtype, q.device, stream, cfg,
              pages_per_split, None if native_pools is None else native_pools.int4_group)
     plan = _PLANS.get(tensors, extra)
     if plan is not None:
         # the same pools, ids, counts and tags as an earlier call: only q and out are new
-        plan.run_with(q, out)
+        plan.run_with(q, out, stream)
         return out
 
     pools = PagePools(k_fp16=k_pages_fp16, v_fp16=v_pages_fp16, k_int8=k_pages_i8, v_int8=v_pages_i8,

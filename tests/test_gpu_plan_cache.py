@@ -200,9 +200,12 @@ def test_streams_keep_plans_apart(dev):
     torch.cuda.synchronize()
     assert plan.reads_records
     want = plan.out.clone()
+    from intent_attention.decode_core import current_stream_handle
     side = torch.cuda.Stream(device=dev)
+    assert current_stream_handle(dev) == torch.cuda.current_stream(dev).cuda_stream
     side.wait_stream(torch.cuda.current_stream(dev))
     with torch.cuda.stream(side):
+        assert current_stream_handle(dev) == side.cuda_stream
         plan.out.fill_(float("nan"))
         plan.run()
     torch.cuda.synchronize()
