@@ -25,7 +25,8 @@ The kernel (``iak_dense_attention``) computes every product and sum in
 float32 over float32, float16 or bfloat16 inputs and rounds the output once,
 where the reference rounds its scores and weights to the input dtype; for
 float32 inputs both are float32 arithmetic. head_dim and v_dim are at most
-1,024. Device tensors only: host tensors raise RuntimeError.
+1,024. Device tensors only: host tensors raise RuntimeError. The output
+carries no autograd history (inference only).
 
 ``semantic_block_attention`` (reference.py:81-129) attends to the layout's
 selected tokens through ``dense_attention``, scoring ATTEND blocks that carry

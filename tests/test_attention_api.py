@@ -157,6 +157,9 @@ DENSE = [
     ((1, 3), 24, 24, 64, "float16", True),
     ((2,), 5, 50, 32, "float32", True),
     ((1, 1), 3, 0, 64, "float32", False),
+    ((2,), 4, 200, 576, "float16", True),        # DeepSeek's latent + RoPE width
+    ((1,), 3, 70, 1024, "bfloat16", False),      # the widest head the kernel takes
+    ((3,), 2, 33, 1, "float32", False),
 ]
 
 
@@ -179,8 +182,10 @@ def test_dense_attention_against_float64(lead, Tq, Tk, D, dt, causal):
         s = s + torch.triu(torch.full((Tq, Tk), float("-inf"), dtype=torch.float64), diagonal=1)
     ref = (torch.softmax(s, dim=-1) @ vd) if Tk else torch.zeros_like(qd)
     err = float((out.cpu().double() - ref).abs().max())
-    # float32 arithmetic; the output rounded once to its dtype
-    tol = {"float32": 2e-5, "float16": 1e-3, "bfloat16": 8e-3}[dt]
+    # float32 arithmetic (2e-5), then one rounding of the output to its dtype: half an ulp
+    # of the largest output, 2^-11 relative for float16 and 2^-8 for bfloat16
+    half_ulp = {"float32": 0.0, "float16": 2.0 ** -11, "bfloat16": 2.0 ** -8}[dt]
+    tol = 2e-5 + half_ulp * float(ref.abs().max()) if Tk else 0.0
     _say(f"  max abs err {err:.2e}")
     assert err <= tol
 
