@@ -913,6 +913,35 @@ def cpu_jobs_for(config: str):
     return None, ()
 
 
+def cfg1_attention_step(dev: torch.device, wl: dict):
+    """One intent_quant_attention_reference call at cfg1's shape on the product API
+    (the selected pages as 16-token blocks, FP16 / INT8 alternating by page id,
+    float16 values carried in float32 as the reference's runnable form needs):
+    the CPU protocol's `iqa_reference` path, on the GPU."""
+    from intent_attention import (BlockLayout, BlockPolicy, KVPrecision, QuantPolicy, SemanticBlock,
+                                  intent_quant_attention_reference)
+    c = CFG1
+    H, D, P = c["H"], c["D"], c["pages"]
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(1, H, 1, D, generator=g).half().float().to(dev)
+    k = torch.randn(1, H, P * PS, D, generator=g).half().float().to(dev)
+    v = torch.randn(1, H, P * PS, D, generator=g).half().float().to(dev)
+    pages = sorted(wl["pages"])
+    blocks, plan = [], {}
+    for r, p in enumerate(pages):
+        pol = BlockPolicy.ALWAYS if p < c["always"] else (BlockPolicy.RECENT if p >= P - c["recent"]
+                                                           else BlockPolicy.ATTEND)
+        blocks.append(SemanticBlock(f"p{p}", p * PS, (p + 1) * PS, pol, 0.9 if pol == BlockPolicy.ATTEND else None))
+        plan[f"p{p}"] = KVPrecision.FP16 if r % 2 == 0 else KVPrecision.INT8
+
+    class Plan:
+        def assign_block_precision(self, block):
+            return QuantPolicy(plan[block.name])
+
+    layout, quantizer = BlockLayout(blocks), Plan()
+    return lambda: intent_quant_attention_reference(q, k, v, layout, quantizer)
+
+
 def run_cfg1(args, cpu=None, cfg1_paths=None) -> None:
     """cfg1: the reference's CPU-runnable shape on the
     GPU. A step is one fused_selected_quant_decode over the routed pages, timed
@@ -932,6 +961,7 @@ def run_cfg1(args, cpu=None, cfg1_paths=None) -> None:
     stream = torch.cuda.current_stream(dev)
     res = _time_steps(plan.run, args, stream)
     api = _time_steps(lambda: fused_selected_quant_decode(*cfg1_args(wl)), args, stream)
+    iqa = _time_steps(cfg1_attention_step(dev, wl), args, stream)
     kev = kernel_events(args.steps, stream)
     for k in kev:
         plan.run(events=k)
@@ -948,6 +978,7 @@ def run_cfg1(args, cpu=None, cfg1_paths=None) -> None:
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5), "us_per_step": round(ms * 1e3, 2),
         "us_per_step_p10_p50_p90": res["spread"],
         "api_us_per_step": round(api["ms"] * 1e3, 2),
+        "intent_quant_attention_us_per_step": round(iqa["ms"] * 1e3, 2),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
         "data": "synthetic (seeded N(0,1) float16 Q/K/V; INT8 pages by the fused fake_int8_pages_from_fp16)",
         "config": {"workload": "cfg1: B=1 H=8/8 D=64 ctx=1024 (64 pages), 32 selected by BlockRouter (4 ALWAYS, "

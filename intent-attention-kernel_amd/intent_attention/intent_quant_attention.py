@@ -23,9 +23,12 @@ Semantics kept from the reference, step for step:
 ``semantic_block_attention`` over the same selected tokens and reports the
 reference's keys.
 
-The fake quantisation runs as torch ops on the input's device (the product
-``intent_quant.fake_quantize_tensor``, the reference's arithmetic); the
-attention is ``reference.dense_attention`` on libiak's paged decode kernel.
+The fake quantisation runs as torch ops on the input's device, batched: the
+selected blocks of one precision and length are reconstructed together with
+one granule per block and channel (the arithmetic of
+``intent_quant.fake_quantize_tensor``, element for element; its error
+metrics, which this function never reads, are not computed). The attention
+is ``reference.dense_attention`` on libiak's dense attention kernel.
 Device tensors only: host tensors raise RuntimeError.
 """
 from __future__ import annotations
@@ -36,8 +39,7 @@ import torch
 
 from .block_metadata import BlockLayout
 from .decode_core import require_device
-from .intent_quant import IntentQuantizer, KVPrecision, QuantPolicy, compute_quant_error, \
-    fake_dequantize_tensor, fake_quantize_tensor
+from .intent_quant import IntentQuantizer, KVPrecision, QuantPolicy, _tdiv, compute_quant_error
 from .reference import dense_attention, semantic_block_attention
 
 
@@ -50,6 +52,34 @@ def _empty_debug(layout: BlockLayout, kv_tokens: int) -> Dict[str, Any]:
         "output_mse_vs_fp16_selected": 0.0, "output_cosine_vs_fp16_selected": 1.0,
         "output_max_abs_error_vs_fp16_selected": 0.0,
     }
+
+
+def _recon_stack(x: torch.Tensor, precision: KVPrecision) -> torch.Tensor:
+    """Fake-quant reconstruction of n stacked blocks ``x [n, ..., T, D]``, one
+    scale per block and channel (absmax over every dim but the first and the
+    last): what ``fake_quantize_tensor`` returns for each block on its own
+    (intent_quant.py:221-312), computed for all n at once."""
+    if precision == KVPrecision.FP16:
+        return x.half()
+    if precision == KVPrecision.SKIP:
+        return torch.zeros_like(x)
+    dims = tuple(range(1, x.ndim - 1))
+
+    def scale_of(t: torch.Tensor) -> torch.Tensor:
+        return _tdiv(t.abs().amax(dim=dims, keepdim=True), 127.0).clamp(min=1e-8)
+
+    scale = scale_of(x)
+    if precision == KVPrecision.FP8:
+        return (x / scale).to(torch.float8_e4m3fn).float() * scale
+    if precision in (KVPrecision.INT8, KVPrecision.INT4):
+        qmax = 127 if precision == KVPrecision.INT8 else 7
+        return (x / scale).clamp(-qmax, qmax).round().to(torch.int8).float() * scale
+    if precision == KVPrecision.INT4_RESIDUAL:
+        base = (x / scale).clamp(-7, 7).round().to(torch.int8).float() * scale
+        resid = x - base
+        rscale = scale_of(resid)
+        return base + (resid / rscale).clamp(-7, 7).round().to(torch.int8).float() * rscale
+    raise ValueError(f"Unknown precision: {precision}")
 
 
 def intent_quant_attention_reference(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layout: BlockLayout,
@@ -72,28 +102,34 @@ def intent_quant_attention_reference(q: torch.Tensor, k: torch.Tensor, v: torch.
 
     head_dim = q.size(-1)
     precision_by_block: Dict[str, str] = {}
-    k_parts: List[torch.Tensor] = []
-    v_parts: List[torch.Tensor] = []
-    k_err: Dict[str, float] = {}
-    v_err: Dict[str, float] = {}
     fp16_bytes = 0
     quant_bytes = 0
-    for block in blocks:
-        bk = k[..., block.start:block.end, :].contiguous()
-        bv = v[..., block.start:block.end, :].contiguous()
+    # the policy per block (layout order), then one batched reconstruction per
+    # (precision, block length) group
+    groups: Dict[tuple, List[int]] = {}
+    precs: List[KVPrecision] = []
+    for i, block in enumerate(blocks):
         n = block.end - block.start
         policy: QuantPolicy = quantizer.assign_block_precision(block)
         precision_by_block[block.name] = policy.precision.value
         fp16_bytes += 2 * n * head_dim * 2
         quant_bytes += int(round(2 * n * head_dim * policy.estimated_bytes_per_value))
-        kq, kmeta = fake_quantize_tensor(bk, policy.precision)
-        vq, vmeta = fake_quantize_tensor(bv, policy.precision)
-        kd, vd = fake_dequantize_tensor(kq, kmeta), fake_dequantize_tensor(vq, vmeta)
-        k_parts.append(kd)
-        v_parts.append(vd)
-        if policy.precision != KVPrecision.SKIP:
-            k_err[block.name] = compute_quant_error(bk, kd)["mse"]
-            v_err[block.name] = compute_quant_error(bv, vd)["mse"]
+        precs.append(policy.precision)
+        groups.setdefault((policy.precision, n), []).append(i)
+    k_parts: List[torch.Tensor] = [None] * len(blocks)
+    v_parts: List[torch.Tensor] = [None] * len(blocks)
+    for (prec, _n), idx in groups.items():
+        for src, parts in ((k, k_parts), (v, v_parts)):
+            rec = _recon_stack(torch.stack([src[..., blocks[i].start:blocks[i].end, :] for i in idx]), prec)
+            for j, i in enumerate(idx):
+                parts[i] = rec[j]
+    k_err: Dict[str, float] = {}
+    v_err: Dict[str, float] = {}
+    if return_debug:
+        for i, block in enumerate(blocks):
+            if precs[i] != KVPrecision.SKIP:
+                k_err[block.name] = compute_quant_error(k[..., block.start:block.end, :], k_parts[i])["mse"]
+                v_err[block.name] = compute_quant_error(v[..., block.start:block.end, :], v_parts[i])["mse"]
 
     output = dense_attention(q, torch.cat(k_parts, dim=-2), torch.cat(v_parts, dim=-2), causal=False)
     if not return_debug:

@@ -190,3 +190,25 @@ def test_empty_span_has_no_pages():
     meta = ia.routing_to_kernel_metadata(blocks, 16)
     assert meta["selected_page_ids"] == [2]
     assert meta["block_precision_by_page"] == {"2": "INT8"}
+
+
+def test_batched_block_reconstruction_equals_per_block():
+    """intent_quant_attention_reference reconstructs the selected blocks of one
+    precision and length together; each block's slice is bit-identical to the
+    product fake_quantize_tensor on that block alone (the G1-pinned arithmetic),
+    for every precision, float16 and float32 inputs, with an outlier channel."""
+    import torch
+    from intent_attention import KVPrecision, fake_quantize_tensor
+    from intent_attention.intent_quant_attention import _recon_stack
+    g = torch.Generator().manual_seed(5)
+    for dt in (torch.float32, torch.float16):
+        blocks = [torch.randn(2, 3, 16, 32, generator=g).to(dt) for _ in range(5)]
+        blocks[2][..., 7] *= 40.0
+        blocks[4].zero_()
+        for prec in KVPrecision:
+            got = _recon_stack(torch.stack(blocks), prec)
+            for j, b in enumerate(blocks):
+                want, _ = fake_quantize_tensor(b, prec)
+                assert got[j].dtype == want.dtype
+                assert torch.equal(got[j], want) or (torch.isnan(want).any() and
+                                                      torch.equal(torch.nan_to_num(got[j]), torch.nan_to_num(want))), (dt, prec, j)
