@@ -44,6 +44,7 @@
  *   iak_dense_attention         dense_attention() reference.py:16-45 (causal, mask, original_kv_positions),
  *                               under semantic_block_attention() reference.py:81-129 and
  *                               intent_quant_attention_reference() intent_quant_attention.py:20-119
+ *   iak_dense_attention_workspace (no counterpart: sizes the optional split-over-keys partial buffer)
  *   iak_status_string           (no counterpart: the reference raises ValueError/RuntimeError in Python)
  */
 #ifndef IAK_H
@@ -56,7 +57,7 @@
 extern "C" {
 #endif
 
-#define IAK_ABI_VERSION 7
+#define IAK_ABI_VERSION 8
 
 /* Grid size from which merge_in_kernel = 2 merges inside the decode kernel. */
 #define IAK_MERGE_IN_KERNEL_MIN_WORKGROUPS 1024
@@ -482,7 +483,14 @@ iak_status iak_mla_decode_rows(const iak_mla_rows_args* args, void* stream);
  *   mask (may be NULL) element (b, i, j) at b * mask_stride_b + i * mask_stride_q + j * mask_stride_k,
  *        mask_dtype IAK_DTYPE_* or IAK_MASK_BOOL (one byte)
  *   kv_positions [kv_len] int64 (IAK_CAUSAL_POSITIONS only)
- *   head_dim, v_dim <= 1024. */
+ *   head_dim, v_dim <= 1024.
+ * workspace (may be NULL): with it, a call with few rows and many keys splits
+ * each row's keys over several workgroups and merges their partials in a
+ * second kernel; it must then hold iak_dense_attention_workspace() bytes
+ * (16-byte aligned; 0 bytes means the shape is not split and the workspace is
+ * unused). Without it every row runs in one workgroup. The results agree to
+ * float32 rounding of the summation order. Calls that share a workspace on
+ * different streams race. */
 enum { IAK_MASK_BOOL = 3 };
 enum { IAK_CAUSAL_NONE = 0, IAK_CAUSAL_TRIU = 1, IAK_CAUSAL_POSITIONS = 2 };
 typedef struct {
@@ -497,7 +505,11 @@ typedef struct {
   float sm_scale;
 } iak_dense_attention_args;
 
-iak_status iak_dense_attention(const iak_dense_attention_args* args, void* stream);
+/* Bytes of device workspace that lets iak_dense_attention split these rows (0: no split). */
+iak_status iak_dense_attention_workspace(const iak_dense_attention_args* args, size_t* bytes);
+
+iak_status iak_dense_attention(const iak_dense_attention_args* args, void* workspace, size_t workspace_bytes,
+                               void* stream);
 
 #ifdef __cplusplus
 }

@@ -330,7 +330,9 @@ iak_status scratch_address(int dev, void** out) {
 
 namespace iak {
 hipError_t launch_mla_rows(const iak_mla_rows_args& a, hipStream_t stream);   // mla_rows.hip
-hipError_t launch_dense_attention(const iak_dense_attention_args& a, hipStream_t stream);   // dense_attention.hip
+hipError_t launch_dense_attention(const iak_dense_attention_args& a, void* workspace,
+                                  hipStream_t stream);                     // dense_attention.hip
+size_t dense_attention_workspace(const iak_dense_attention_args& a);     // dense_attention.hip
 }
 
 extern "C" {
@@ -689,7 +691,7 @@ iak_status iak_mla_decode_rows(const iak_mla_rows_args* a, void* stream) {
   return IAK_OK;
 }
 
-iak_status iak_dense_attention(const iak_dense_attention_args* a, void* stream) {
+static iak_status validate_dense(const iak_dense_attention_args* a) {
   if (!a) return fail(IAK_EINVAL, "args is NULL");
   if (a->batch < 0 || a->q_len < 0 || a->kv_len < 0)
     return fail(IAK_EINVAL, "negative size (batch=%d, q_len=%d, kv_len=%d)", a->batch, a->q_len, a->kv_len);
@@ -712,7 +714,29 @@ iak_status iak_dense_attention(const iak_dense_attention_args* a, void* stream) 
     if (st < 0) return fail(IAK_EINVAL, "negative stride %lld", st);
   if (a->mask && (a->mask_stride_b < 0 || a->mask_stride_q < 0 || a->mask_stride_k < 0))
     return fail(IAK_EINVAL, "negative mask stride");
-  const hipError_t e = iak::launch_dense_attention(*a, static_cast<hipStream_t>(stream));
+  return IAK_OK;
+}
+
+iak_status iak_dense_attention_workspace(const iak_dense_attention_args* a, size_t* bytes) {
+  if (!bytes) return fail(IAK_EINVAL, "bytes is NULL");
+  const iak_status st = validate_dense(a);
+  if (st != IAK_OK) return st;
+  *bytes = (long long)a->batch * a->q_len == 0 ? 0 : iak::dense_attention_workspace(*a);
+  return IAK_OK;
+}
+
+iak_status iak_dense_attention(const iak_dense_attention_args* a, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  const iak_status st = validate_dense(a);
+  if (st != IAK_OK) return st;
+  if ((long long)a->batch * a->q_len == 0) return IAK_OK;
+  if (workspace) {
+    const size_t need = iak::dense_attention_workspace(*a);
+    if (workspace_bytes < need)
+      return fail(IAK_EINVAL, "workspace of %zu bytes is smaller than the %zu bytes required", workspace_bytes, need);
+    if (!aligned16(workspace)) return fail(IAK_EINVAL, "workspace must be 16-byte aligned");
+  }
+  const hipError_t e = iak::launch_dense_attention(*a, workspace, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(IAK_EHIP, "kernel launch failed: %s", hipGetErrorString(e));
   return IAK_OK;
 }

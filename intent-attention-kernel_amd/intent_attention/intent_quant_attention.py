@@ -1,5 +1,5 @@
 """``intent_quant_attention_reference`` of the reference
-(intent_quant_attention.py:20-119) with its attention on the HIP decode.
+(intent_quant_attention.py:20-119) with its attention on the HIP dense-attention kernel.
 
 Semantics kept from the reference, step for step:
 
@@ -33,6 +33,7 @@ Device tensors only: host tensors raise RuntimeError.
 """
 from __future__ import annotations
 
+import functools
 from typing import Any, Dict, List
 
 import torch
@@ -54,16 +55,18 @@ def _empty_debug(layout: BlockLayout, kv_tokens: int) -> Dict[str, Any]:
     }
 
 
-def _recon_stack(x: torch.Tensor, precision: KVPrecision) -> torch.Tensor:
-    """Fake-quant reconstruction of n stacked blocks ``x [n, ..., T, D]``, one
-    scale per block and channel (absmax over every dim but the first and the
+def _recon_stack(x: torch.Tensor, precision: KVPrecision, block_dim: int = 0) -> torch.Tensor:
+    """Fake-quant reconstruction of n blocks stacked along ``block_dim`` of ``x``
+    (``[n, ..., T, D]`` by default, or ``[..., n, T, D]`` with block_dim -3), one
+    scale per block and channel (absmax over every dim but the block dim and the
     last): what ``fake_quantize_tensor`` returns for each block on its own
     (intent_quant.py:221-312), computed for all n at once."""
     if precision == KVPrecision.FP16:
         return x.half()
     if precision == KVPrecision.SKIP:
         return torch.zeros_like(x)
-    dims = tuple(range(1, x.ndim - 1))
+    bd = block_dim % x.ndim
+    dims = tuple(d for d in range(x.ndim - 1) if d != bd)
 
     def scale_of(t: torch.Tensor) -> torch.Tensor:
         return _tdiv(t.abs().amax(dim=dims, keepdim=True), 127.0).clamp(min=1e-8)
@@ -80,6 +83,43 @@ def _recon_stack(x: torch.Tensor, precision: KVPrecision) -> torch.Tensor:
         rscale = scale_of(resid)
         return base + (resid / rscale).clamp(-7, 7).round().to(torch.int8).float() * rscale
     raise ValueError(f"Unknown precision: {precision}")
+
+
+def _reconstruct_selected(k: torch.Tensor, v: torch.Tensor, blocks: List, precs: List[KVPrecision]):
+    """The reference's ``torch.cat`` of every selected block's fake-quant
+    reconstruction (intent_quant_attention.py:56-84), built with one gather
+    and one scatter per (precision, length) group: returns (K, V) over the
+    selected tokens in block order, the token index and each block's start."""
+    # the dtype torch.cat promotes the reconstructions to: FP16 blocks are float16,
+    # SKIP blocks keep the input dtype (zeros_like), the others are float32
+    out_dtype = functools.reduce(torch.promote_types, {
+        torch.float16 if p == KVPrecision.FP16 else (k.dtype if p == KVPrecision.SKIP else torch.float32)
+        for p in precs})
+    groups: Dict[tuple, List[int]] = {}
+    for i, (b, p) in enumerate(zip(blocks, precs)):
+        groups.setdefault((p, b.end - b.start), []).append(i)
+    starts = [0]
+    for b in blocks:
+        starts.append(starts[-1] + b.end - b.start)
+    # the token index and each group's positions in it, uploaded in one copy
+    tok_list = [t for b in blocks for t in range(b.start, b.end)]
+    pos_lists = [[starts[i] + t for i in idx for t in range(n)] for (_, n), idx in groups.items()]
+    flat = torch.tensor(tok_list + [p for pl in pos_lists for p in pl], dtype=torch.long).to(k.device)
+    tok = flat[:len(tok_list)]
+    lead = tuple(k.shape[:-2])
+    k_rec = torch.empty((*lead, starts[-1], k.size(-1)), dtype=out_dtype, device=k.device)
+    v_rec = torch.empty((*tuple(v.shape[:-2]), starts[-1], v.size(-1)), dtype=out_dtype, device=v.device)
+    off = len(tok_list)
+    for ((prec, n), idx), pl in zip(groups.items(), pos_lists):
+        pos = flat[off:off + len(pl)]
+        off += len(pl)
+        src_tok = flat[pos]
+        for src, dst in ((k, k_rec), (v, v_rec)):
+            x = src.index_select(-2, src_tok)                       # [..., len(idx) * n, D]
+            x = x.reshape(*x.shape[:-2], len(idx), n, x.shape[-1])
+            rec = _recon_stack(x, prec, block_dim=-3)
+            dst.index_copy_(-2, pos, rec.reshape(*rec.shape[:-3], len(idx) * n, rec.shape[-1]).to(out_dtype))
+    return k_rec, v_rec, tok, starts
 
 
 def intent_quant_attention_reference(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layout: BlockLayout,
@@ -106,7 +146,6 @@ def intent_quant_attention_reference(q: torch.Tensor, k: torch.Tensor, v: torch.
     quant_bytes = 0
     # the policy per block (layout order), then one batched reconstruction per
     # (precision, block length) group
-    groups: Dict[tuple, List[int]] = {}
     precs: List[KVPrecision] = []
     for i, block in enumerate(blocks):
         n = block.end - block.start
@@ -115,28 +154,25 @@ def intent_quant_attention_reference(q: torch.Tensor, k: torch.Tensor, v: torch.
         fp16_bytes += 2 * n * head_dim * 2
         quant_bytes += int(round(2 * n * head_dim * policy.estimated_bytes_per_value))
         precs.append(policy.precision)
-        groups.setdefault((policy.precision, n), []).append(i)
-    k_parts: List[torch.Tensor] = [None] * len(blocks)
-    v_parts: List[torch.Tensor] = [None] * len(blocks)
-    for (prec, _n), idx in groups.items():
-        for src, parts in ((k, k_parts), (v, v_parts)):
-            rec = _recon_stack(torch.stack([src[..., blocks[i].start:blocks[i].end, :] for i in idx]), prec)
-            for j, i in enumerate(idx):
-                parts[i] = rec[j]
+    k_rec, v_rec, tok, starts = _reconstruct_selected(k, v, blocks, precs)
     k_err: Dict[str, float] = {}
     v_err: Dict[str, float] = {}
     if return_debug:
         for i, block in enumerate(blocks):
             if precs[i] != KVPrecision.SKIP:
-                k_err[block.name] = compute_quant_error(k[..., block.start:block.end, :], k_parts[i])["mse"]
-                v_err[block.name] = compute_quant_error(v[..., block.start:block.end, :], v_parts[i])["mse"]
+                kd = k_rec[..., starts[i]:starts[i + 1], :]
+                vd = v_rec[..., starts[i]:starts[i + 1], :]
+                if precs[i] == KVPrecision.FP16:
+                    kd, vd = kd.half(), vd.half()
+                k_err[block.name] = compute_quant_error(k[..., block.start:block.end, :], kd)["mse"]
+                v_err[block.name] = compute_quant_error(v[..., block.start:block.end, :], vd)["mse"]
 
-    output = dense_attention(q, torch.cat(k_parts, dim=-2), torch.cat(v_parts, dim=-2), causal=False)
+    output = dense_attention(q, k_rec, v_rec, causal=False)
     if not return_debug:
         return output
 
-    sel_k = torch.cat([k[..., b.start:b.end, :].contiguous() for b in blocks], dim=-2)
-    sel_v = torch.cat([v[..., b.start:b.end, :].contiguous() for b in blocks], dim=-2)
+    sel_k = k.index_select(-2, tok)
+    sel_v = v.index_select(-2, tok)
     fp16_out = dense_attention(q, sel_k, sel_v, causal=False)
     err = compute_quant_error(fp16_out, output)
     saved = (1.0 - quant_bytes / max(fp16_bytes, 1)) * 100.0 if fp16_bytes > 0 else 0.0

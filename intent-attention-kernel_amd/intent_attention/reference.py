@@ -131,9 +131,14 @@ def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: b
         if positions is not None:
             a.kv_positions = positions.data_ptr()
     a.sm_scale = 1.0 / math.sqrt(D)
-    # the operands (and any copies made above) were allocated on this stream, so
-    # the caching allocator reuses their memory only after this kernel
-    N.dense_attention(a, torch.cuda.current_stream(dev).cuda_stream)
+    # few rows with many keys: a workspace lets the kernel split each row's keys
+    # over several workgroups (decode shapes); the operands, any copies made
+    # above and the workspace were allocated on this stream, so the caching
+    # allocator reuses their memory only after these kernels
+    ws_bytes = N.dense_attention_workspace(a)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+    N.dense_attention(a, torch.cuda.current_stream(dev).cuda_stream,
+                      ws.data_ptr() if ws is not None else 0, ws_bytes)
     return out
 
 

@@ -185,9 +185,41 @@ void invalid_launches() {
       case 2: da.dtype = 3 + (int32_t)(rng() % 50); break;
       default: da.q_len = -1 - (int32_t)(rng() % 50); break;
     }
-    count(iak_dense_attention(&da, nullptr));
+    count(iak_dense_attention(&da, nullptr, 0, nullptr));
   }
-  count(iak_dense_attention(nullptr, nullptr));
+  count(iak_dense_attention(nullptr, nullptr, 0, nullptr));
+
+  // workspace sizes of random and of valid shapes (host queries), and a split
+  // shape with a workspace one byte short (rejected before the launch)
+  size_t wsb = 0;
+  for (int i = 0; i < 2000; ++i) {
+    random_bytes(da);
+    if (rng() % 2) {
+      da.batch = pick_int(); da.q_len = pick_int(); da.kv_len = pick_int();
+      da.head_dim = pick_int(); da.v_dim = pick_int(); da.dtype = pick_int() & 3;
+      da.causal = pick_int() & 3; da.mask = nullptr;
+    }
+    count(iak_dense_attention_workspace(&da, &wsb));
+  }
+  count(iak_dense_attention_workspace(nullptr, &wsb));
+  std::memset(&da, 0, sizeof(da));
+  da.batch = 2; da.q_len = 1; da.kv_len = 8192; da.head_dim = 128; da.v_dim = 128;
+  da.q = da.k = da.v = reinterpret_cast<const void*>(0x1000); da.out = reinterpret_cast<void*>(0x1000);
+  da.sm_scale = 0.125f;
+  count(iak_dense_attention_workspace(&da, nullptr));
+  if (iak_dense_attention_workspace(&da, &wsb) != IAK_OK || wsb == 0) {
+    std::printf("abi-asan: a 2-row, 8192-key shape should ask for a split workspace\n");
+    std::exit(1);
+  }
+  if (iak_dense_attention(&da, reinterpret_cast<void*>(0x1000), wsb - 1, nullptr) != IAK_EINVAL) {
+    std::printf("abi-asan: a short dense workspace was not rejected\n");
+    std::exit(1);
+  }
+  da.kv_len = 100;
+  if (iak_dense_attention_workspace(&da, &wsb) != IAK_OK || wsb != 0) {
+    std::printf("abi-asan: a 100-key shape should not be split\n");
+    std::exit(1);
+  }
 }
 
 }  // namespace

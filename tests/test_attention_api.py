@@ -160,6 +160,13 @@ DENSE = [
     ((2,), 4, 200, 576, "float16", True),        # DeepSeek's latent + RoPE width
     ((1,), 3, 70, 1024, "bfloat16", False),      # the widest head the kernel takes
     ((3,), 2, 33, 1, "float32", False),
+    # grids of many rows take fewer waves per row (16 up to 256 rows, 8 up to 512, then 4);
+    # few rows with 512 keys or more split each row's keys over workgroups
+    ((2, 3), 2, 3000, 128, "bfloat16", True),     # 12 rows x 11 key ranges, most of them fully masked
+    ((1, 2), 3, 5000, 1024, "float16", False),    # 6 rows of the widest head over 19 ranges
+    ((4, 8), 64, 96, 64, "float16", True),        # 2,048 rows: 4 waves per row
+    ((2, 4), 48, 130, 128, "float32", False),     # 384 rows: 8 waves per row
+    ((2,), 300, 40, 1024, "float32", False),      # 600 rows of the widest head: 4 waves per row
 ]
 
 
@@ -188,6 +195,43 @@ def test_dense_attention_against_float64(lead, Tq, Tk, D, dt, causal):
     tol = 2e-5 + half_ulp * float(ref.abs().max()) if Tk else 0.0
     _say(f"  max abs err {err:.2e}")
     assert err <= tol
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_dense_attention_split_matches_single_pass(dt, monkeypatch):
+    """The split-over-keys path and the one-workgroup-per-row path (no
+    workspace) agree to float32 summation order, also with a mask and causal
+    key positions."""
+    from intent_attention import dense_attention
+    from intent_attention import _native as N
+    dev = torch.device("cuda:0")
+    _say("dense_attention split vs single pass", dt)
+    q, k, v, g = _dense_case(8, (2, 4), 3, 4097, 96, 80, dt, dev)
+    mask = torch.randn(3, 4097, generator=g).to(dt).to(dev)
+    pos = torch.randperm(4097, generator=g).to(dev)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    assert N.dense_attention_workspace(_probe_args(qd, kd, vd)) > 0
+    for kw in (dict(), dict(mask=mask, causal=True, original_kv_positions=pos)):
+        split = dense_attention(qd, kd, vd, **kw)
+        with monkeypatch.context() as mp:
+            mp.setattr(N, "dense_attention_workspace", lambda a: 0)
+            single = dense_attention(qd, kd, vd, **kw)
+        torch.cuda.synchronize()
+        err = float((split.float() - single.float()).abs().max())
+        _say(f"  {sorted(kw)}: max |split - single| {err:.2e}")
+        assert torch.isnan(split).sum() == torch.isnan(single).sum() == 0
+        assert err <= (1e-5 if dt == torch.float32 else 8e-3)
+
+
+def _probe_args(q, k, v):
+    """DenseAttentionArgs of the leading-dims-flattened shapes, for the workspace query."""
+    from intent_attention import _native as N
+    a = N.DenseAttentionArgs()
+    L = math.prod(q.shape[:-2])
+    a.batch, a.q_len, a.kv_len, a.head_dim, a.v_dim, a.dtype = L, q.shape[-2], k.shape[-2], q.shape[-1], v.shape[-1], 0
+    a.q, a.k, a.v, a.out = q.data_ptr(), k.data_ptr(), v.data_ptr(), q.data_ptr()
+    return a
 
 
 @pytest.mark.gpu
@@ -222,23 +266,24 @@ def _cmp(out, ref, dt, what):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("Tq,Tk", [(12, 70), (2, 3000)])
 @pytest.mark.parametrize("dt", [torch.float32, torch.float16, torch.bfloat16])
-def test_dense_attention_masks_and_positions(dt):
+def test_dense_attention_masks_and_positions(dt, Tq, Tk):
     """Additive masks (float with -inf entries, bool, per-batch), original KV positions
     (sorted and unsorted, with and without a mask), v_dim != head_dim and broadcast
-    leading dims, against the float64 oracle."""
+    leading dims, against the float64 oracle; 3,000 keys over 12 rows take the
+    split-over-keys path (partials merged by a second kernel)."""
     from intent_attention import dense_attention
     dev = torch.device("cuda:0")
-    _say("dense_attention masks / positions", dt)
-    q, k, v, g = _dense_case(5, (2, 3), 12, 70, 64, 48, dt, dev)
+    _say("dense_attention masks / positions", dt, f"Tq={Tq} Tk={Tk}")
+    q, k, v, g = _dense_case(5, (2, 3), Tq, Tk, 64, 48, dt, dev)
     t = lambda x: x.to(dev)  # noqa: E731
-    Tq, Tk = 12, 70
     fmask = torch.randn(Tq, Tk, generator=g)
     fmask[torch.rand(Tq, Tk, generator=g) < 0.3] = float("-inf")
     fmask[:, 5] = 0.0
     bmask = torch.rand(2, 1, Tq, Tk, generator=g) < 0.5
     lmask = torch.randn(2, 3, Tq, Tk, generator=g)
-    pos_sorted = torch.sort(torch.randperm(200, generator=g)[:Tk]).values
+    pos_sorted = torch.sort(torch.randperm(max(200, 3 * Tk), generator=g)[:Tk]).values
     pos_sorted[0] = 0
     pos_perm = pos_sorted[torch.randperm(Tk, generator=g)]
     qn, kn, vn = (x.double().numpy() for x in (q, k, v))

@@ -212,3 +212,37 @@ def test_batched_block_reconstruction_equals_per_block():
                 assert got[j].dtype == want.dtype
                 assert torch.equal(got[j], want) or (torch.isnan(want).any() and
                                                       torch.equal(torch.nan_to_num(got[j]), torch.nan_to_num(want))), (dt, prec, j)
+
+
+def test_grouped_reconstruction_equals_cat_of_blocks():
+    """The selected K/V that intent_quant_attention_reference attends over (one
+    gather and one scatter per precision and length group) equals the torch.cat
+    of each block's own fake_quantize_tensor in block order, dtype included
+    (the reference's loop, intent_quant_attention.py:56-84): mixed precisions,
+    ragged block lengths, blocks out of token order, float16 and float32."""
+    import torch
+    from intent_attention import KVPrecision, fake_quantize_tensor
+    from intent_attention.block_metadata import BlockPolicy, SemanticBlock
+    from intent_attention.intent_quant_attention import _reconstruct_selected
+    g = torch.Generator().manual_seed(11)
+    spans = [(40, 56), (0, 16), (16, 20), (60, 76), (20, 24), (80, 83), (24, 40)]
+    cases = [
+        [KVPrecision.INT4, KVPrecision.FP16, KVPrecision.INT8, KVPrecision.INT4,
+         KVPrecision.INT8, KVPrecision.SKIP, KVPrecision.FP8],
+        [KVPrecision.FP16] * 7,
+        [KVPrecision.SKIP, KVPrecision.INT4, KVPrecision.SKIP, KVPrecision.INT4,
+         KVPrecision.SKIP, KVPrecision.INT4, KVPrecision.SKIP],
+    ]
+    for dt in (torch.float32, torch.float16):
+        k = torch.randn(2, 3, 90, 32, generator=g).to(dt)
+        v = torch.randn(2, 3, 90, 48, generator=g).to(dt)
+        k[..., 5] *= 30.0
+        blocks = [SemanticBlock(f"b{i}", s, e, BlockPolicy.ATTEND) for i, (s, e) in enumerate(spans)]
+        for precs in cases:
+            kr, vr, tok, starts = _reconstruct_selected(k, v, blocks, precs)
+            want_k = torch.cat([fake_quantize_tensor(k[..., b.start:b.end, :], p)[0] for b, p in zip(blocks, precs)], dim=-2)
+            want_v = torch.cat([fake_quantize_tensor(v[..., b.start:b.end, :], p)[0] for b, p in zip(blocks, precs)], dim=-2)
+            assert kr.dtype == want_k.dtype and vr.dtype == want_v.dtype, (dt, precs)
+            assert torch.equal(kr, want_k) and torch.equal(vr, want_v), (dt, precs)
+            assert tok.tolist() == [t for s, e in spans for t in range(s, e)]
+            assert starts[-1] == kr.size(-2)
