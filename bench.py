@@ -862,6 +862,61 @@ def run_transcode(args, cpu=None) -> None:
     print(json.dumps(out), flush=True)
 
 
+# dense_attention (the reference's reference.py:16-45, under intent_quant_attention_reference):
+# shapes (leading rows, q_len, kv_len, head_dim, dtype); the first is cfg1's attention
+DENSE_CONFIGS = {
+    "dense": [((1, 8), 1, 512, 64, torch.float32), ((1, 8), 1, 8192, 128, torch.float16),
+              ((1, 32), 1, 4096, 128, torch.bfloat16), ((4, 8), 128, 128, 64, torch.float16)],
+}
+
+
+def run_dense(args) -> None:
+    """dense_attention per shape: the C ABI call on resident inputs (kernel(s) only,
+    the split workspace allocated once) and the Python entry point. The bytes are
+    K + V + Q + O once each (algorithmic; rows of one batch re-read K and V)."""
+    from intent_attention import _native as N
+    from intent_attention import dense_attention
+    from intent_attention.reference import _DTYPES
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    g = torch.Generator(device=dev).manual_seed(7)
+    rows = []
+    for lead, tq, tk, d, dt in DENSE_CONFIGS[args.config]:
+        L = math.prod(lead)
+        q = torch.randn(L, tq, d, device=dev, generator=g).to(dt)
+        k = torch.randn(L, tk, d, device=dev, generator=g).to(dt)
+        v = torch.randn(L, tk, d, device=dev, generator=g).to(dt)
+        out = torch.empty(L, tq, d, device=dev, dtype=dt)
+        a = N.DenseAttentionArgs()
+        a.batch, a.q_len, a.kv_len, a.head_dim, a.v_dim, a.dtype = L, tq, tk, d, d, _DTYPES[dt]
+        a.q, a.q_stride_b, a.q_stride_t = q.data_ptr(), q.stride(0), q.stride(1)
+        a.k, a.k_stride_b, a.k_stride_t = k.data_ptr(), k.stride(0), k.stride(1)
+        a.v, a.v_stride_b, a.v_stride_t = v.data_ptr(), v.stride(0), v.stride(1)
+        a.out, a.out_stride_b, a.out_stride_t = out.data_ptr(), out.stride(0), out.stride(1)
+        a.sm_scale = 1.0 / math.sqrt(d)
+        wsb = N.dense_attention_workspace(a)
+        ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=dev)
+        h = stream.cuda_stream
+        kern = _time_steps(lambda: N.dense_attention(a, h, ws.data_ptr() if wsb else 0, wsb), args, stream)
+        qv, kv_, vv = q.view(*lead, tq, d), k.view(*lead, tk, d), v.view(*lead, tk, d)
+        api = _time_steps(lambda: dense_attention(qv, kv_, vv), args, stream)
+        ab = (2 * L * tk * d + 2 * L * tq * d) * torch.finfo(dt).bits // 8
+        rows.append({"shape": {"rows": L * tq, "q_len": tq, "kv_len": tk, "head_dim": d, "dtype": str(dt)[6:]},
+                     "split_workspace_bytes": wsb, "us_per_call": round(kern["ms"] * 1e3, 2),
+                     "us_p10_p50_p90": kern["spread"], "api_us_per_call": round(api["ms"] * 1e3, 2),
+                     "algorithmic_bytes": ab, "gbps": round(ab / (kern["ms"] * 1e-3) / 1e9, 1)})
+        print(f"[bench] dense {rows[-1]['shape']}: {rows[-1]['us_per_call']} us", file=sys.stderr, flush=True)
+    head = rows[1]
+    print(json.dumps({
+        "metric": "dense_attention µs per call (the reference's reference.py:16-45 in float32)",
+        "value": head["us_per_call"], "unit": "us", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded N(0,1))",
+        "config": {"workload": "dense_attention shapes; value = 8 rows x 8,192 keys x 128 (float16), split over keys"},
+        "kernel_source_digest": source_digest(["dense_attention.hip", "iak_device.h"]),
+        "shapes": rows}), flush=True)
+
+
 def kernel_events(n: int, stream) -> list:
     """n pairs of timing events, each recorded once so its HIP event exists
     (torch creates events lazily); the library re-records them around the split
@@ -1013,7 +1068,7 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="cfg3",
                     choices=sorted(CONFIGS) + ["cfg1"] + sorted(MLA_CONFIGS) + sorted(QUANT_CONFIGS)
-                    + sorted(TABLE_CONFIGS) + sorted(TRANSCODE_CONFIGS))
+                    + sorted(TABLE_CONFIGS) + sorted(TRANSCODE_CONFIGS) + sorted(DENSE_CONFIGS))
     ap.add_argument("--pages-per-split", type=int, default=0)
     ap.add_argument("--cpu-budget", type=float, default=CPU_BUDGET_S,
                     help="seconds of oracle work per CPU-baseline leg (one thread, then all cores)")
@@ -1067,6 +1122,9 @@ def main() -> None:
 
     if args.config == "cfg1":
         run_cfg1(args, cpu, cfg1_paths)
+        return
+    if args.config in DENSE_CONFIGS:
+        run_dense(args)
         return
     if args.config in MLA_CONFIGS:
         run_mla(args, cpu)
