@@ -36,6 +36,7 @@ from __future__ import annotations
 import functools
 from typing import Any, Dict, List
 
+import numpy as np
 import torch
 
 from .block_metadata import BlockLayout
@@ -89,37 +90,54 @@ def _reconstruct_selected(k: torch.Tensor, v: torch.Tensor, blocks: List, precs:
     """The reference's ``torch.cat`` of every selected block's fake-quant
     reconstruction (intent_quant_attention.py:56-84), built with one gather
     and one scatter per (precision, length) group: returns (K, V) over the
-    selected tokens in block order, the token index and each block's start."""
-    # the dtype torch.cat promotes the reconstructions to: FP16 blocks are float16,
-    # SKIP blocks keep the input dtype (zeros_like), the others are float32
-    out_dtype = functools.reduce(torch.promote_types, {
-        torch.float16 if p == KVPrecision.FP16 else (k.dtype if p == KVPrecision.SKIP else torch.float32)
-        for p in precs})
+    selected tokens in block order, the token index and each block's start.
+    The scales are per channel (absmax over every dim but the last), so when K
+    and V share their leading shape and dtype they go through one chain,
+    side by side along the channel dim, and come back as two views of one
+    buffer."""
+    def out_dtype(x: torch.Tensor) -> torch.dtype:
+        # the dtype torch.cat promotes x's reconstructions to: FP16 blocks are
+        # float16, SKIP blocks keep x's dtype (zeros_like), the others are
+        # codes.float() * scale, i.e. float32 promoted with x's dtype
+        return functools.reduce(torch.promote_types, {
+            torch.float16 if p == KVPrecision.FP16 else
+            (x.dtype if p == KVPrecision.SKIP else torch.promote_types(torch.float32, x.dtype)) for p in precs})
+    lens = np.array([b.end - b.start for b in blocks], dtype=np.int64)
+    first = np.array([b.start for b in blocks], dtype=np.int64)
+    starts = np.concatenate(([0], np.cumsum(lens)))
+    total = int(starts[-1])
+    # token index of every selected position, and each group's positions, uploaded in one copy
+    tok_np = np.repeat(first - starts[:-1], lens) + np.arange(total, dtype=np.int64)
     groups: Dict[tuple, List[int]] = {}
-    for i, (b, p) in enumerate(zip(blocks, precs)):
-        groups.setdefault((p, b.end - b.start), []).append(i)
-    starts = [0]
-    for b in blocks:
-        starts.append(starts[-1] + b.end - b.start)
-    # the token index and each group's positions in it, uploaded in one copy
-    tok_list = [t for b in blocks for t in range(b.start, b.end)]
-    pos_lists = [[starts[i] + t for i in idx for t in range(n)] for (_, n), idx in groups.items()]
-    flat = torch.tensor(tok_list + [p for pl in pos_lists for p in pl], dtype=torch.long).to(k.device)
-    tok = flat[:len(tok_list)]
-    lead = tuple(k.shape[:-2])
-    k_rec = torch.empty((*lead, starts[-1], k.size(-1)), dtype=out_dtype, device=k.device)
-    v_rec = torch.empty((*tuple(v.shape[:-2]), starts[-1], v.size(-1)), dtype=out_dtype, device=v.device)
-    off = len(tok_list)
-    for ((prec, n), idx), pl in zip(groups.items(), pos_lists):
-        pos = flat[off:off + len(pl)]
-        off += len(pl)
-        src_tok = flat[pos]
-        for src, dst in ((k, k_rec), (v, v_rec)):
+    for i, (n, p) in enumerate(zip(lens.tolist(), precs)):
+        groups.setdefault((p, n), []).append(i)
+    pos_np = [(starts[idx][:, None] + np.arange(n, dtype=np.int64)[None, :]).reshape(-1)
+              for (_, n), idx in groups.items()]
+    flat = torch.from_numpy(np.concatenate([tok_np] + pos_np))
+    if k.is_cuda:
+        # staged in pinned memory (torch's caching host allocator keeps the
+        # buffer until the copy has run), so the upload does not wait for the
+        # work already queued on the stream
+        flat = flat.pin_memory().to(k.device, non_blocking=True)
+    tok = flat[:total]
+    fused = k.shape[:-1] == v.shape[:-1] and k.dtype == v.dtype
+    srcs = [torch.cat([k, v], dim=-1)] if fused else [k, v]
+    recs = [torch.empty((*x.shape[:-2], total, x.size(-1)), dtype=out_dtype(x), device=k.device) for x in srcs]
+    off = total
+    for ((prec, n), idx), pn in zip(groups.items(), pos_np):
+        pos = flat[off:off + len(pn)]
+        off += len(pn)
+        src_tok = tok.index_select(0, pos)
+        for src, dst in zip(srcs, recs):
             x = src.index_select(-2, src_tok)                       # [..., len(idx) * n, D]
             x = x.reshape(*x.shape[:-2], len(idx), n, x.shape[-1])
             rec = _recon_stack(x, prec, block_dim=-3)
-            dst.index_copy_(-2, pos, rec.reshape(*rec.shape[:-3], len(idx) * n, rec.shape[-1]).to(out_dtype))
-    return k_rec, v_rec, tok, starts
+            dst.index_copy_(-2, pos, rec.reshape(*rec.shape[:-3], len(idx) * n, rec.shape[-1]).to(dst.dtype))
+    if fused:
+        k_rec, v_rec = recs[0][..., :k.size(-1)], recs[0][..., k.size(-1):]
+    else:
+        k_rec, v_rec = recs
+    return k_rec, v_rec, tok, starts.tolist()
 
 
 def intent_quant_attention_reference(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layout: BlockLayout,

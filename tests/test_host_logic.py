@@ -246,3 +246,9 @@ def test_grouped_reconstruction_equals_cat_of_blocks():
             assert torch.equal(kr, want_k) and torch.equal(vr, want_v), (dt, precs)
             assert tok.tolist() == [t for s, e in spans for t in range(s, e)]
             assert starts[-1] == kr.size(-2)
+            # K and V of different dtypes take separate chains: the same results
+            v2 = v.double() if dt == torch.float32 else v.float()
+            kr2, vr2, _, _ = _reconstruct_selected(k, v2, blocks, precs)
+            want_v2 = torch.cat([fake_quantize_tensor(v2[..., b.start:b.end, :], p)[0]
+                                 for b, p in zip(blocks, precs)], dim=-2)
+            assert torch.equal(kr2.to(want_k.dtype), want_k) and torch.equal(vr2.to(want_v2.dtype), want_v2)
