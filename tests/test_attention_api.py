@@ -445,3 +445,55 @@ def test_compare_function_returns_expected_keys():
     assert abs(res["output_mse"] - mse) <= 0.02 * mse + 1e-9
     assert abs(res["output_max_abs_error"] - mx) <= 0.02 * mx + 1e-6
     assert 0.0 < res["output_cosine_similarity"] <= 1.0 + 1e-6
+
+
+@pytest.mark.gpu
+def test_dense_attention_fuzz():
+    """Seeded random shapes around the kernel's thresholds (split over keys from
+    1,024 keys on fewer than 512 rows, 4 / 8 / 16 waves per workgroup, head
+    widths 1 .. 1,024, v_dim != head_dim), every dtype, with and without masks,
+    triu or KV-position causality and broadcast leading dims, against the
+    float64 oracle."""
+    from intent_attention import dense_attention
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(2026)
+    dts = [torch.float32, torch.float16, torch.bfloat16]
+    for case in range(24):
+        dt = dts[case % 3]
+        lead = tuple(int(x) for x in rng.integers(1, 4, size=int(rng.integers(1, 3))))
+        Tq = int(rng.choice([1, 1, 2, 5, 33]))
+        Tk = int(rng.choice([1, 17, 300, 1023, 1024, 1500, 4100]))
+        D = int(rng.choice([1, 32, 64, 96, 128, 200, 576]))
+        Dv = int(rng.choice([D, 48, 128]))
+        q, k, v, g = _dense_case(100 + case, lead, Tq, Tk, D, Dv, dt, dev)
+        kw, okw = {}, {}
+        mode = case % 4
+        if mode == 1:
+            m = torch.randn(Tq, Tk, generator=g)
+            m[torch.rand(Tq, Tk, generator=g) < 0.2] = float("-inf")
+            m[:, 0] = 0.0
+            kw["mask"], okw["mask"] = m.to(dt), m.to(dt).double().numpy()
+        elif mode == 2:
+            kw["causal"] = okw["causal"] = True
+        elif mode == 3:
+            pos = torch.randperm(max(Tk, 2 * Tq), generator=g)[:Tk]
+            pos[int(rng.integers(0, Tk))] = 0   # a key every query sees
+            kw["causal"] = okw["causal"] = True
+            kw["original_kv_positions"], okw["original_kv_positions"] = pos, pos.numpy()
+        shared_kv = bool(rng.integers(0, 2)) and len(lead) == 2
+        kk, vv = (k[:, :1], v[:, :1]) if shared_kv else (k, v)
+        _say(f"  fuzz {case}: lead={lead} Tq={Tq} Tk={Tk} D={D} Dv={Dv} {dt} mode={mode} shared_kv={shared_kv}")
+        t = lambda x: x.to(dev) if isinstance(x, torch.Tensor) else x  # noqa: E731
+        out = dense_attention(t(q), t(kk), t(vv), **{n: t(x) for n, x in kw.items()})
+        torch.cuda.synchronize()
+        assert out.shape == (*lead, Tq, Dv) and out.dtype == dt
+        ref = A.dense_attention_masked(q.double().numpy(), kk.double().numpy(), vv.double().numpy(), **okw)
+        o = out.cpu().double().numpy()
+        assert np.array_equal(np.isnan(o), np.isnan(ref)) and not np.isnan(ref).any()
+        err = float(np.abs(o - ref).max())
+        # float32 arithmetic, then one rounding of the output to its dtype (half an ulp
+        # of the largest output: 2^-11 relative for float16, 2^-8 for bfloat16)
+        half_ulp = {torch.float32: 0.0, torch.float16: 2.0 ** -11, torch.bfloat16: 2.0 ** -8}[dt]
+        tol = 2e-5 + half_ulp * float(np.abs(ref).max())
+        _say(f"    max abs err {err:.2e} (bar {tol:.2e})")
+        assert err <= tol, (case, err, tol)
