@@ -1015,6 +1015,14 @@ def run_cfg1(args, cpu=None, cfg1_paths=None) -> None:
                      negative_ids=True, sm_scale=1.0 / math.sqrt(c["D"]), out=out[:, :, 0, :], auto_records=False)
     stream = torch.cuda.current_stream(dev)
     res = _time_steps(plan.run, args, stream)
+    # the same step captured once in a HIP graph and replayed (a serving loop
+    # without the per-launch host work)
+    plan.run()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        plan.run()
+    gres = _time_steps(graph.replay, args, stream)
     api = _time_steps(lambda: fused_selected_quant_decode(*cfg1_args(wl)), args, stream)
     iqa = _time_steps(cfg1_attention_step(dev, wl), args, stream)
     kev = kernel_events(args.steps, stream)
@@ -1033,6 +1041,7 @@ def run_cfg1(args, cpu=None, cfg1_paths=None) -> None:
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5), "us_per_step": round(ms * 1e3, 2),
         "us_per_step_p10_p50_p90": res["spread"],
         "api_us_per_step": round(api["ms"] * 1e3, 2),
+        "graph_replay_us_per_step": round(gres["ms"] * 1e3, 2),
         "intent_quant_attention_us_per_step": round(iqa["ms"] * 1e3, 2),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
         "data": "synthetic (seeded N(0,1) float16 Q/K/V; INT8 pages by the fused fake_int8_pages_from_fp16)",

@@ -228,3 +228,43 @@ def test_streams_keep_plans_apart(dev):
     torch.cuda.synchronize()
     assert torch.equal(a, b) and len(fmod._PLANS._d) == 2
     fmod.clear_plan_cache()
+
+
+@pytest.mark.parametrize("merge", [False, True])
+def test_plan_replays_in_a_hip_graph(dev, merge):
+    """A plan's step captured in a HIP graph (torch.cuda.CUDAGraph) for a
+    launch-bound serving loop: the capture holds the split kernel and the
+    merge (kernel, or in-kernel with its self-resetting arrival counters) and
+    no allocation, memset or host synchronisation. Each replay, after an
+    in-place update of the query and with eager work and synchronisations
+    between replays, matches an eager plan over the same tensors bit for bit
+    and the oracle within the quantised bar."""
+    import torch
+    from intent_attention.decode_core import make_plan
+    _say("plan in a HIP graph, merge in kernel:", merge)
+    q, pools, table, counts, tags = _case(307)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)  # noqa: E731
+    dp = to_device_pools(pools, dev)
+    tq, tt, tc, tg = t(q), t(table), t(counts), t(tags)
+    kw = dict(out_dtype=torch.float32, pages_per_split=16, merge_in_kernel=merge, auto_records=False)
+    plan = make_plan(tq, dp, tt, tc, tg, **kw)
+    eager = make_plan(tq, dp, tt, tc, tg, **kw)
+    plan.run()                        # first run outside the capture (workspace fill waited on)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        plan.run()
+    rng = np.random.default_rng(11)
+    for i in range(4):
+        qn = rng.standard_normal(q.shape).astype(np.float16)
+        tq.copy_(t(qn))
+        plan.out.fill_(float("nan"))
+        graph.replay()
+        eager.run()
+        torch.cuda.synchronize()
+        assert torch.equal(plan.out, eager.out), i
+        ref = Dm.paged_decode_oracle(qn.astype(np.float32), pools, table, counts, tags)
+        err = float(np.abs(plan.out.cpu().numpy() - ref).max())
+        _say(f"  replay {i}: bit-identical to eager, max abs err vs oracle {err:.2e}")
+        assert err <= TOL_QUANT
+    del graph
