@@ -483,7 +483,7 @@ iak_status iak_mla_decode_rows(const iak_mla_rows_args* args, void* stream);
  *   mask (may be NULL) element (b, i, j) at b * mask_stride_b + i * mask_stride_q + j * mask_stride_k,
  *        mask_dtype IAK_DTYPE_* or IAK_MASK_BOOL (one byte)
  *   kv_positions [kv_len] int64 (IAK_CAUSAL_POSITIONS only)
- *   head_dim, v_dim <= 1024.
+ *   head_dim, v_dim <= 1024; kv_len <= INT32_MAX - 4096.
  * workspace (may be NULL): with it, a call with few rows and many keys splits
  * each row's keys over several workgroups and merges their partials in a
  * second kernel; it must then hold iak_dense_attention_workspace() bytes

@@ -698,6 +698,9 @@ static iak_status validate_dense(const iak_dense_attention_args* a) {
   if (a->head_dim <= 0 || a->head_dim > 1024 || a->v_dim <= 0 || a->v_dim > 1024)
     return fail(IAK_ENOTSUP, "head_dim %d / v_dim %d is not supported (1 .. 1024)", a->head_dim, a->v_dim);
   if (a->dtype < 0 || a->dtype > 2) return fail(IAK_EINVAL, "unknown dtype %d", a->dtype);
+  // the kernel's key indexes run up to 128 past kv_len in 32-bit arithmetic
+  if (a->kv_len > 0x7FFFFFFF - 4096)
+    return fail(IAK_ENOTSUP, "kv_len %d is not supported (at most %d)", a->kv_len, 0x7FFFFFFF - 4096);
   if (a->mask && (a->mask_dtype < 0 || a->mask_dtype > IAK_MASK_BOOL))
     return fail(IAK_EINVAL, "unknown mask dtype %d", a->mask_dtype);
   if (a->causal < IAK_CAUSAL_NONE || a->causal > IAK_CAUSAL_POSITIONS)

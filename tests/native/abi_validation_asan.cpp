@@ -215,6 +215,11 @@ void invalid_launches() {
     std::printf("abi-asan: a short dense workspace was not rejected\n");
     std::exit(1);
   }
+  da.kv_len = 0x7FFFFFFF - 64;   // key indexes would pass INT32_MAX: rejected
+  if (iak_dense_attention(&da, nullptr, 0, nullptr) != IAK_ENOTSUP) {
+    std::printf("abi-asan: a kv_len near INT32_MAX was not rejected\n");
+    std::exit(1);
+  }
   da.kv_len = 100;
   if (iak_dense_attention_workspace(&da, &wsb) != IAK_OK || wsb != 0) {
     std::printf("abi-asan: a 100-key shape should not be split\n");
