@@ -679,6 +679,9 @@ iak_status iak_mla_decode_rows(const iak_mla_rows_args* a, void* stream) {
     return fail(IAK_ENOTSUP, "latent_dim %d is not supported (1 .. 1024)", a->latent_dim);
   if (a->page_size <= 0) return fail(IAK_EINVAL, "page_size must be positive, got %d", a->page_size);
   if ((long long)a->batch * a->q_len > 0x7FFFFFFFLL) return fail(IAK_EINVAL, "batch * q_len too large");
+  // the kernel's page index runs a few waves past num_selected in 32-bit arithmetic
+  if (a->num_selected > 0x7FFFFFFF - 4096)
+    return fail(IAK_ENOTSUP, "num_selected %d is not supported (at most %d)", a->num_selected, 0x7FFFFFFF - 4096);
   for (int dt : {a->q_dtype, a->latent_dtype})
     if (dt < 0 || dt > 2) return fail(IAK_EINVAL, "unknown dtype %d", dt);
   if ((long long)a->batch * a->q_len == 0) return IAK_OK;
