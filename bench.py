@@ -917,6 +917,57 @@ def run_dense(args) -> None:
         "shapes": rows}), flush=True)
 
 
+# mla_decode_triton's latent context (the reference's triton_mla_decode.py:47-186,
+# float32 row kernel): (batch, latent rows of C, page size, pages listed, d_c, dtype)
+MLA_ROWS_CONFIGS = {
+    "mla-rows": [(32, 16384, 64, 128, 576, torch.float16), (1, 4096, 64, 32, 576, torch.float32),
+                 (4, 8192, 16, 256, 512, torch.bfloat16), (2, 1024, 64, 8, 576, torch.float32)],
+}
+
+
+def run_mla_rows(args) -> None:
+    """mla_latent_context per shape: the C ABI call on resident inputs (kernels
+    only, the split workspace allocated once) and the Python entry point. The
+    bytes are the listed latent rows once, Q and the context (algorithmic)."""
+    from intent_attention import _native as N
+    from intent_attention.triton_mla_decode import _DT, mla_latent_context
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    g = torch.Generator(device=dev).manual_seed(11)
+    rows = []
+    for B, T, ps, npages, dc, dt in MLA_ROWS_CONFIGS[args.config]:
+        q = torch.randn(B, 1, dc, device=dev, generator=g).to(dt)
+        C = torch.randn(T, dc, device=dev, generator=g).to(dt)
+        ids = torch.randperm(T // ps, device=dev, generator=g)[:npages].to(torch.int32)
+        ctx = torch.empty(B, 1, dc, dtype=torch.float32, device=dev)
+        a = N.MlaRowsArgs()
+        a.batch, a.q_len, a.latent_dim, a.page_size, a.num_selected, a.num_rows = B, 1, dc, ps, npages, T
+        a.q, a.q_dtype, a.q_stride_b, a.q_stride_t = q.data_ptr(), _DT[dt], q.stride(0), q.stride(1)
+        a.latents, a.latent_dtype, a.latent_stride = C.data_ptr(), _DT[dt], C.stride(0)
+        a.page_ids, a.context, a.sm_scale = ids.data_ptr(), ctx.data_ptr(), 1.0 / math.sqrt(dc)
+        wsb = N.mla_decode_rows_workspace(a)
+        ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=dev)
+        h = stream.cuda_stream
+        kern = _time_steps(lambda: N.mla_decode_rows(a, h, ws.data_ptr() if wsb else 0, wsb), args, stream)
+        api = _time_steps(lambda: mla_latent_context(q, C, ids, ps), args, stream)
+        ab = (npages * ps * dc + 2 * B * dc) * torch.finfo(dt).bits // 8 + B * dc * 4
+        rows.append({"shape": {"batch": B, "latent_rows": npages * ps, "page_size": ps, "d_c": dc,
+                               "dtype": str(dt)[6:]},
+                     "split_workspace_bytes": wsb, "us_per_call": round(kern["ms"] * 1e3, 2),
+                     "us_p10_p50_p90": kern["spread"], "api_us_per_call": round(api["ms"] * 1e3, 2),
+                     "algorithmic_bytes": ab, "gbps": round(ab / (kern["ms"] * 1e-3) / 1e9, 1)})
+        print(f"[bench] mla rows {rows[-1]['shape']}: {rows[-1]['us_per_call']} us", file=sys.stderr, flush=True)
+    head = rows[0]
+    print(json.dumps({
+        "metric": "mla_decode_triton latent context µs per call (the reference's triton_mla_decode.py in float32)",
+        "value": head["us_per_call"], "unit": "us", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded N(0,1))",
+        "config": {"workload": "mla_latent_context shapes; value = 32 sequences x 8,192 latent rows x 576 (float16)"},
+        "kernel_source_digest": source_digest(["mla_rows.hip", "iak_device.h"]),
+        "shapes": rows}), flush=True)
+
+
 def kernel_events(n: int, stream) -> list:
     """n pairs of timing events, each recorded once so its HIP event exists
     (torch creates events lazily); the library re-records them around the split
@@ -1077,7 +1128,8 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="cfg3",
                     choices=sorted(CONFIGS) + ["cfg1"] + sorted(MLA_CONFIGS) + sorted(QUANT_CONFIGS)
-                    + sorted(TABLE_CONFIGS) + sorted(TRANSCODE_CONFIGS) + sorted(DENSE_CONFIGS))
+                    + sorted(TABLE_CONFIGS) + sorted(TRANSCODE_CONFIGS) + sorted(DENSE_CONFIGS)
+                    + sorted(MLA_ROWS_CONFIGS))
     ap.add_argument("--pages-per-split", type=int, default=0)
     ap.add_argument("--cpu-budget", type=float, default=CPU_BUDGET_S,
                     help="seconds of oracle work per CPU-baseline leg (one thread, then all cores)")
@@ -1134,6 +1186,9 @@ def main() -> None:
         return
     if args.config in DENSE_CONFIGS:
         run_dense(args)
+        return
+    if args.config in MLA_ROWS_CONFIGS:
+        run_mla_rows(args)
         return
     if args.config in MLA_CONFIGS:
         run_mla(args, cpu)

@@ -27,6 +27,7 @@
  *                               (the latent context; mla_sparse_decode_reference mla.py:61-92,
  *                               mla_triton_decode mla.py:95-136)
  *   iak_mla_decode_workspace    (no counterpart: sizes the split-K partial buffer)
+ *   iak_mla_decode_rows_workspace (no counterpart: sizes the optional split-over-keys partial buffer)
  *   iak_mla_decode_rows         the latent context of mla_decode_triton() in the reference's float32
  *                               arithmetic: its Triton kernel triton_mla_decode.py:47-107 and
  *                               _mla_decode_cpu :155-186 (also under mla_sparse_decode_reference /
@@ -57,7 +58,7 @@
 extern "C" {
 #endif
 
-#define IAK_ABI_VERSION 8
+#define IAK_ABI_VERSION 9
 
 /* Grid size from which merge_in_kernel = 2 merges inside the decode kernel. */
 #define IAK_MERGE_IN_KERNEL_MIN_WORKGROUPS 1024
@@ -455,7 +456,14 @@ iak_status iak_prefetch_pages(const iak_prefetch_args* args, void* stream);
  *   latents  [num_rows, latent_dim] (latent_dtype), element row stride latent_stride
  *   page_ids [num_selected] int32, shared by every row
  *   context  [batch, q_len, latent_dim] float32, contiguous (written)
- *   latent_dim <= 1024; any page_size >= 1. */
+ *   latent_dim <= 1024; any page_size >= 1; num_selected * page_size <= INT32_MAX - 4096.
+ * workspace (may be NULL): with it, a call with fewer than 512 rows and at least
+ * 256 listed latent rows splits each row's keys over several workgroups and
+ * merges their partials in a second kernel; it must then hold
+ * iak_mla_decode_rows_workspace() bytes (16-byte aligned; 0 bytes: not split).
+ * Without it every row runs in one workgroup. The results agree to float32
+ * rounding of the summation order. Calls that share a workspace on different
+ * streams race. */
 typedef struct {
   int32_t batch, q_len, latent_dim, page_size, num_selected;
   int64_t num_rows;
@@ -466,7 +474,11 @@ typedef struct {
   float sm_scale;
 } iak_mla_rows_args;
 
-iak_status iak_mla_decode_rows(const iak_mla_rows_args* args, void* stream);
+/* Bytes of device workspace that lets iak_mla_decode_rows split these rows (0: no split). */
+iak_status iak_mla_decode_rows_workspace(const iak_mla_rows_args* args, size_t* bytes);
+
+iak_status iak_mla_decode_rows(const iak_mla_rows_args* args, void* workspace, size_t workspace_bytes,
+                               void* stream);
 
 /* Dense softmax attention of the reference's dense_attention() (reference.py:16-45)
  * in float32: for each (batch, query) row i,

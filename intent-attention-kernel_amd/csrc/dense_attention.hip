@@ -15,7 +15,7 @@
 //
 // Work split. A (batch, query) row's keys go to `splits` workgroups of
 // consecutive key ranges (`chunk` keys each); splits > 1 only when the caller
-// gives a workspace and there are few rows with many keys (decode shapes),
+// gives a workspace and there are few rows with 256 keys or more (decode shapes),
 // and a second kernel then merges the partials (max, denominator, context)
 // by log-sum-exp. A workgroup has WAVES waves (16 when the grid is short, so
 // it still has many key rows in flight); wave w takes KEYS consecutive keys
@@ -35,6 +35,19 @@
 namespace iak {
 
 namespace {
+
+// the split over keys: rows with at least SPLIT_MIN_KEYS keys, ranges of at
+// least RANGE_MIN_KEYS keys
+#ifndef SPLIT_MIN_KEYS
+#define SPLIT_MIN_KEYS 256
+#endif
+#ifndef RANGE_MIN_KEYS
+#define RANGE_MIN_KEYS 64
+#endif
+// workgroups the split aims at
+#ifndef SPLIT_TARGET_WGS
+#define SPLIT_TARGET_WGS 256
+#endif
 
 // element types: float, _Float16, and bfloat16 held as its 16 bits
 struct bf16_bits { uint16_t b; };
@@ -388,15 +401,16 @@ void launch_typed(const iak_dense_attention_args& a, const DenseSplit& sp, hipSt
   if (sp.splits > 1) hipLaunchKernelGGL(dense_merge_kernel<T>, dim3((unsigned)rows), dim3(256), 0, stream, a, sp);
 }
 
-// Splits per row: rows with 1,024 keys or more on a short grid (fewer than
-// 512 rows) go over about 1,024 workgroups in ranges of at least 256 keys
+// Splits per row: rows with SPLIT_MIN_KEYS keys or more on a short grid (fewer
+// than 512 rows) go over about SPLIT_TARGET_WGS workgroups in ranges of at
+// least RANGE_MIN_KEYS keys
 // (at most MAX_SPLITS ranges).
 DenseSplit split_plan(const iak_dense_attention_args& a) {
   DenseSplit sp{1, a.kv_len, nullptr};
   const int64_t rows = (int64_t)a.batch * a.q_len;
-  if (rows <= 0 || rows >= 512 || a.kv_len < 1024) return sp;
-  int64_t s = (1024 + rows - 1) / rows;
-  const int64_t by_keys = a.kv_len / 256;
+  if (rows <= 0 || rows >= 512 || a.kv_len < SPLIT_MIN_KEYS) return sp;
+  int64_t s = (SPLIT_TARGET_WGS + rows - 1) / rows;
+  const int64_t by_keys = a.kv_len / RANGE_MIN_KEYS;
   if (s > by_keys) s = by_keys;
   if (s <= 1) return sp;
   const int64_t chunk = ((int64_t)a.kv_len + s - 1) / s;

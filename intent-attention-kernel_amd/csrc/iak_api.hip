@@ -329,7 +329,8 @@ iak_status scratch_address(int dev, void** out) {
 }  // namespace
 
 namespace iak {
-hipError_t launch_mla_rows(const iak_mla_rows_args& a, hipStream_t stream);   // mla_rows.hip
+hipError_t launch_mla_rows(const iak_mla_rows_args& a, void* workspace, hipStream_t stream);   // mla_rows.hip
+size_t mla_rows_workspace(const iak_mla_rows_args& a);                                      // mla_rows.hip
 hipError_t launch_dense_attention(const iak_dense_attention_args& a, void* workspace,
                                   hipStream_t stream);                     // dense_attention.hip
 size_t dense_attention_workspace(const iak_dense_attention_args& a);     // dense_attention.hip
@@ -670,7 +671,7 @@ iak_status iak_prefetch_pages(const iak_prefetch_args* a, void* stream) {
   return IAK_OK;
 }
 
-iak_status iak_mla_decode_rows(const iak_mla_rows_args* a, void* stream) {
+static iak_status validate_mla_rows(const iak_mla_rows_args* a) {
   if (!a) return fail(IAK_EINVAL, "args is NULL");
   if (a->batch < 0 || a->q_len < 0 || a->num_selected < 0 || a->num_rows < 0)
     return fail(IAK_EINVAL, "negative size (batch=%d, q_len=%d, num_selected=%d, num_rows=%lld)", a->batch, a->q_len,
@@ -679,9 +680,11 @@ iak_status iak_mla_decode_rows(const iak_mla_rows_args* a, void* stream) {
     return fail(IAK_ENOTSUP, "latent_dim %d is not supported (1 .. 1024)", a->latent_dim);
   if (a->page_size <= 0) return fail(IAK_EINVAL, "page_size must be positive, got %d", a->page_size);
   if ((long long)a->batch * a->q_len > 0x7FFFFFFFLL) return fail(IAK_EINVAL, "batch * q_len too large");
-  // the kernel's page index runs a few waves past num_selected in 32-bit arithmetic
-  if (a->num_selected > 0x7FFFFFFF - 4096)
-    return fail(IAK_ENOTSUP, "num_selected %d is not supported (at most %d)", a->num_selected, 0x7FFFFFFF - 4096);
+  // the kernel's key indexes (num_selected * page_size keys) run up to 128 past the
+  // last key in 32-bit arithmetic
+  if ((long long)a->num_selected * a->page_size > 0x7FFFFFFF - 4096)
+    return fail(IAK_ENOTSUP, "num_selected * page_size = %lld keys is not supported (at most %d)",
+                (long long)a->num_selected * a->page_size, 0x7FFFFFFF - 4096);
   for (int dt : {a->q_dtype, a->latent_dtype})
     if (dt < 0 || dt > 2) return fail(IAK_EINVAL, "unknown dtype %d", dt);
   if ((long long)a->batch * a->q_len == 0) return IAK_OK;
@@ -689,7 +692,29 @@ iak_status iak_mla_decode_rows(const iak_mla_rows_args* a, void* stream) {
   if (a->num_selected > 0 && (!a->page_ids || !a->latents)) return fail(IAK_EINVAL, "page_ids/latents is NULL");
   if (a->latent_stride < a->latent_dim && a->num_rows > 1)
     return fail(IAK_EINVAL, "latent_stride %lld is below latent_dim %d", (long long)a->latent_stride, a->latent_dim);
-  const hipError_t e = iak::launch_mla_rows(*a, static_cast<hipStream_t>(stream));
+  if (a->num_selected > 0 && a->num_rows <= 0) return fail(IAK_EINVAL, "num_rows is 0 with pages listed");
+  return IAK_OK;
+}
+
+iak_status iak_mla_decode_rows_workspace(const iak_mla_rows_args* a, size_t* bytes) {
+  if (!bytes) return fail(IAK_EINVAL, "bytes is NULL");
+  const iak_status st = validate_mla_rows(a);
+  if (st != IAK_OK) return st;
+  *bytes = (long long)a->batch * a->q_len == 0 ? 0 : iak::mla_rows_workspace(*a);
+  return IAK_OK;
+}
+
+iak_status iak_mla_decode_rows(const iak_mla_rows_args* a, void* workspace, size_t workspace_bytes, void* stream) {
+  const iak_status st = validate_mla_rows(a);
+  if (st != IAK_OK) return st;
+  if ((long long)a->batch * a->q_len == 0) return IAK_OK;
+  if (workspace) {
+    const size_t need = iak::mla_rows_workspace(*a);
+    if (workspace_bytes < need)
+      return fail(IAK_EINVAL, "workspace of %zu bytes is smaller than the %zu bytes required", workspace_bytes, need);
+    if (!aligned16(workspace)) return fail(IAK_EINVAL, "workspace must be 16-byte aligned");
+  }
+  const hipError_t e = iak::launch_mla_rows(*a, workspace, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(IAK_EHIP, "kernel launch failed: %s", hipGetErrorString(e));
   return IAK_OK;
 }

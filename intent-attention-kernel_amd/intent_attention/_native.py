@@ -14,7 +14,7 @@ from typing import Optional
 _HERE = os.path.dirname(os.path.abspath(__file__))
 # IAK_LIBRARY selects another build of the same ABI (e.g. a tuning variant)
 LIB_PATH = os.environ.get("IAK_LIBRARY") or os.path.join(_HERE, "libiak.so")
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 IAK_OK, IAK_EINVAL, IAK_ENOTSUP, IAK_EHIP = 0, 1, 2, 3
 
@@ -169,7 +169,8 @@ EXPORTED = ("iak_abi_version", "iak_status_string", "iak_last_error",
             "iak_build_page_tables", "iak_paged_decode_timed", "iak_mla_decode_timed",
             "iak_paged_decode_noalloc", "iak_transcode_pages", "iak_prefetch_pages", "iak_paged_decode_plan",
             "iak_mla_decode_rows", "iak_pack_page_descriptors",
-            "iak_pack_entry_records", "iak_dense_attention", "iak_dense_attention_workspace")
+            "iak_pack_entry_records", "iak_dense_attention", "iak_dense_attention_workspace",
+            "iak_mla_decode_rows_workspace")
 NOALLOC_SCRATCH_BYTES = 16 << 20   # IAK_NOALLOC_SCRATCH_BYTES
 
 _lib: Optional[ctypes.CDLL] = None
@@ -224,7 +225,9 @@ def load() -> ctypes.CDLL:
     lib.iak_prefetch_pages.argtypes = [ctypes.POINTER(PrefetchArgs), c_void_p]
     lib.iak_build_page_tables.restype = ctypes.c_int
     lib.iak_mla_decode_rows.restype = ctypes.c_int
-    lib.iak_mla_decode_rows.argtypes = [ctypes.POINTER(MlaRowsArgs), c_void_p]
+    lib.iak_mla_decode_rows.argtypes = [ctypes.POINTER(MlaRowsArgs), c_void_p, ctypes.c_size_t, c_void_p]
+    lib.iak_mla_decode_rows_workspace.restype = ctypes.c_int
+    lib.iak_mla_decode_rows_workspace.argtypes = [ctypes.POINTER(MlaRowsArgs), ctypes.POINTER(ctypes.c_size_t)]
     lib.iak_build_page_tables.argtypes = [ctypes.POINTER(PageTableArgs), c_void_p]
     lib.iak_pack_page_descriptors.restype = ctypes.c_int
     lib.iak_pack_page_descriptors.argtypes = [ctypes.POINTER(PagedDecodeArgs), c_void_p, c_void_p]
@@ -335,8 +338,14 @@ def prefetch_pages(args: PrefetchArgs, stream: int) -> None:
     check(load().iak_prefetch_pages(ctypes.byref(args), stream or None))
 
 
-def mla_decode_rows(args: MlaRowsArgs, stream: int) -> None:
-    check(load().iak_mla_decode_rows(ctypes.byref(args), stream or None))
+def mla_decode_rows_workspace(args: MlaRowsArgs) -> int:
+    n = ctypes.c_size_t(0)
+    check(load().iak_mla_decode_rows_workspace(ctypes.byref(args), ctypes.byref(n)))
+    return int(n.value)
+
+
+def mla_decode_rows(args: MlaRowsArgs, stream: int, workspace: int = 0, workspace_bytes: int = 0) -> None:
+    check(load().iak_mla_decode_rows(ctypes.byref(args), workspace or None, workspace_bytes, stream or None))
 
 
 def build_page_tables(args: PageTableArgs, stream: int) -> None:

@@ -58,7 +58,8 @@ def mla_latent_context(q_absorb: torch.Tensor, C: torch.Tensor, page_table: torc
     # page p is rows p*page_size .. (p+1)*page_size - 1 of C, the last page of
     # C possibly shorter (the reference slices C[p*ps:(p+1)*ps])
     n_src = (C.shape[0] + page_size - 1) // page_size
-    if int(ids.min()) < 0 or int(ids.max()) >= n_src:
+    lo, hi = torch.stack(torch.aminmax(ids)).tolist()          # one device-to-host read
+    if lo < 0 or hi >= n_src:
         raise ValueError(f"page ids must lie in [0, {n_src})")
     if q_absorb.stride(2) != 1:
         q_absorb = q_absorb.contiguous()
@@ -71,7 +72,11 @@ def mla_latent_context(q_absorb: torch.Tensor, C: torch.Tensor, page_table: torc
         q_absorb.stride(1)
     a.latents, a.latent_dtype, a.latent_stride = C.data_ptr(), _DT[C.dtype], C.stride(0)
     a.page_ids, a.context, a.sm_scale = ids.data_ptr(), ctx.data_ptr(), 1.0 / math.sqrt(d_c)
-    N.mla_decode_rows(a, torch.cuda.current_stream(dev).cuda_stream)
+    # few rows over many latent rows: a workspace lets the kernel split each
+    # row's keys over several workgroups (allocated on this stream, as the rest)
+    ws_bytes = N.mla_decode_rows_workspace(a)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+    N.mla_decode_rows(a, torch.cuda.current_stream(dev).cuda_stream, ws.data_ptr() if ws is not None else 0, ws_bytes)
     return ctx
 
 

@@ -172,9 +172,41 @@ void invalid_launches() {
     if (rng() % 2) r.latent_dim = 1025 + (int32_t)(rng() % 100);
     else r.page_size = 0;
     if (r.batch > 0 && r.q_len > 0 && r.latent_dim > 0 && r.latent_dim <= 1024 && r.page_size > 0) r.batch = -1;
-    count(iak_mla_decode_rows(&r, nullptr));
+    count(iak_mla_decode_rows(&r, nullptr, 0, nullptr));
   }
-  count(iak_mla_decode_rows(nullptr, nullptr));
+  count(iak_mla_decode_rows(nullptr, nullptr, 0, nullptr));
+  // workspace sizes of random shapes (host queries), a split shape with a
+  // workspace one byte short, and a key count past the 32-bit limit
+  size_t rwb = 0;
+  for (int i = 0; i < 2000; ++i) {
+    random_bytes(r);
+    if (rng() % 2) {
+      r.batch = pick_int(); r.q_len = pick_int(); r.latent_dim = pick_int(); r.page_size = pick_int();
+      r.num_selected = pick_int(); r.num_rows = pick_int(); r.q_dtype = pick_int() & 3; r.latent_dtype = pick_int() & 3;
+    }
+    count(iak_mla_decode_rows_workspace(&r, &rwb));
+  }
+  count(iak_mla_decode_rows_workspace(nullptr, &rwb));
+  std::memset(&r, 0, sizeof(r));
+  r.batch = 4; r.q_len = 1; r.latent_dim = 576; r.page_size = 64; r.num_selected = 128; r.num_rows = 16384;
+  r.latent_stride = 576;
+  r.q = r.latents = reinterpret_cast<const void*>(0x1000);
+  r.page_ids = reinterpret_cast<const int32_t*>(0x1000);
+  r.context = reinterpret_cast<float*>(0x1000);
+  count(iak_mla_decode_rows_workspace(&r, nullptr));
+  if (iak_mla_decode_rows_workspace(&r, &rwb) != IAK_OK || rwb == 0) {
+    std::printf("abi-asan: 4 rows over 8192 latent rows should ask for a split workspace\n");
+    std::exit(1);
+  }
+  if (iak_mla_decode_rows(&r, reinterpret_cast<void*>(0x1000), rwb - 1, nullptr) != IAK_EINVAL) {
+    std::printf("abi-asan: a short latent-row workspace was not rejected\n");
+    std::exit(1);
+  }
+  r.page_size = 1 << 20; r.num_selected = 4096;   // 2^32 keys
+  if (iak_mla_decode_rows(&r, nullptr, 0, nullptr) != IAK_ENOTSUP) {
+    std::printf("abi-asan: num_selected * page_size past INT32_MAX was not rejected\n");
+    std::exit(1);
+  }
 
   iak_dense_attention_args da;
   for (int i = 0; i < 300; ++i) {

@@ -450,7 +450,7 @@ def test_compare_function_returns_expected_keys():
 @pytest.mark.gpu
 def test_dense_attention_fuzz():
     """Seeded random shapes around the kernel's thresholds (split over keys from
-    1,024 keys on fewer than 512 rows, 4 / 8 / 16 waves per workgroup, head
+    256 keys on fewer than 512 rows, 4 / 8 / 16 waves per workgroup, head
     widths 1 .. 1,024, v_dim != head_dim), every dtype, with and without masks,
     triu or KV-position causality and broadcast leading dims, against the
     float64 oracle."""

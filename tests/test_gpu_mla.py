@@ -362,3 +362,60 @@ def test_mla_block_table_api(dev):
     big = max(1.0, float(np.abs(ref).max()))
     assert np.abs(out_t.cpu().numpy() - ref).max() <= 2e-5 * big                    # float32 throughout
     assert np.abs(out_r.float().cpu().numpy() - ref).max() <= (2e-5 + 2.0 ** -11) * big   # + the f16 output
+
+
+@pytest.mark.parametrize("d_c,page_size,dtype,npages", [(576, 64, "float16", 40), (512, 16, "bfloat16", 100),
+                                                        (1024, 7, "float32", 200), (33, 1, "float32", 1500),
+                                                        (256, 32, "float32", 300)])
+def test_mla_decode_triton_split_over_keys(dev, d_c, page_size, dtype, npages):
+    """Rows with 256 listed latent rows or more on a short grid take the
+    split-over-keys path (partials merged by a second kernel): the ragged last
+    page of C listed, repeated and out-of-order ids, against the reference loop
+    (float64) on the same input values."""
+    import torch
+    from intent_attention import mla_decode_triton
+    from intent_attention import _native as N
+    _say("mla_decode_triton split", f"d_c={d_c} page_size={page_size} {dtype} pages={npages}")
+    rng = np.random.default_rng(d_c * 7 + page_size)
+    dt = getattr(torch, dtype)
+    n_src = npages // 2 + 3
+    T = n_src * page_size - (page_size // 2)                    # the last page is shorter
+    qa = torch.from_numpy(rng.standard_normal((2, 2, d_c)).astype(np.float32)).to(dev).to(dt)
+    C = torch.from_numpy(rng.standard_normal((T, d_c)).astype(np.float32)).to(dev).to(dt)
+    W = torch.from_numpy((rng.standard_normal((d_c, 24)) / np.sqrt(d_c)).astype(np.float32)).to(dev)
+    ids = rng.integers(0, n_src, size=npages).astype(np.int32)
+    ids[npages // 3] = n_src - 1                                 # the short page
+    pt = torch.from_numpy(ids).to(dev)
+    a = N.MlaRowsArgs()
+    a.batch, a.q_len, a.latent_dim, a.page_size, a.num_selected, a.num_rows = 2, 2, d_c, page_size, npages, T
+    a.q, a.latents, a.page_ids, a.context, a.latent_stride = 16, 16, 16, 16, d_c
+    assert N.mla_decode_rows_workspace(a) > 0                   # the shape is split
+    out = mla_decode_triton(qa, C, W, pt, page_size=page_size)
+    ref = M.mla_decode_cpu_loop(qa.float().cpu().numpy(), C.float().cpu().numpy(), W.cpu().numpy(), ids, page_size)
+    got = out.float().cpu().numpy()
+    out_ulp = {"float32": 0.0, "float16": 2.0 ** -11, "bfloat16": 2.0 ** -8}[dtype]
+    bar = (2e-5 + out_ulp) * max(1.0, float(np.abs(ref).max()))
+    err = float(np.abs(got - ref).max())
+    _say(f"  max abs err {err:.2e} (bar {bar:.2e})")
+    assert err <= bar
+
+
+def test_mla_rows_split_matches_single_pass(dev, monkeypatch):
+    """The split-over-keys path and the one-workgroup-per-row path (no
+    workspace) of the float32 latent context agree to float32 summation order."""
+    import torch
+    from intent_attention import _native as N
+    from intent_attention.triton_mla_decode import mla_latent_context
+    _say("mla rows split vs single pass")
+    rng = np.random.default_rng(4)
+    qa = torch.from_numpy(rng.standard_normal((3, 1, 576)).astype(np.float32)).to(dev)
+    C = torch.from_numpy(rng.standard_normal((64 * 200, 576)).astype(np.float32)).to(dev)
+    pt = torch.from_numpy(rng.permutation(200)[:150].astype(np.int32)).to(dev)
+    split = mla_latent_context(qa, C, pt, 64)
+    with monkeypatch.context() as mp:
+        mp.setattr(N, "mla_decode_rows_workspace", lambda a: 0)
+        single = mla_latent_context(qa, C, pt, 64)
+    torch.cuda.synchronize()
+    err = float((split - single).abs().max())
+    _say(f"  max |split - single| {err:.2e}")
+    assert err <= 1e-5 * max(1.0, float(single.abs().max()))
