@@ -412,6 +412,7 @@ DenseSplit split_plan(const iak_dense_attention_args& a) {
   int64_t s = (SPLIT_TARGET_WGS + rows - 1) / rows;
   const int64_t by_keys = a.kv_len / RANGE_MIN_KEYS;
   if (s > by_keys) s = by_keys;
+  if (s > MAX_SPLITS) s = MAX_SPLITS;   // the merge holds the split weights in the LDS
   if (s <= 1) return sp;
   const int64_t chunk = ((int64_t)a.kv_len + s - 1) / s;
   sp.splits = (int)(((int64_t)a.kv_len + chunk - 1) / chunk);

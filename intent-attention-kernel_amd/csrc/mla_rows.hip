@@ -397,6 +397,7 @@ RowSplit plan_for(const iak_mla_rows_args& a, int R) {
   int64_t s = (SPLIT_TARGET_WGS + groups - 1) / groups;
   const int64_t by_keys = nkeys / RANGE_MIN_KEYS;
   if (s > by_keys) s = by_keys;
+  if (s > MAX_SPLITS) s = MAX_SPLITS;   // the merge holds the split weights in the LDS
   if (s <= 1) return sp;
   const int64_t chunk = (nkeys + s - 1) / s;
   sp.splits = (int)((nkeys + chunk - 1) / chunk);
