@@ -419,3 +419,25 @@ def test_mla_rows_split_matches_single_pass(dev, monkeypatch):
     err = float((split - single).abs().max())
     _say(f"  max |split - single| {err:.2e}")
     assert err <= 1e-5 * max(1.0, float(single.abs().max()))
+
+
+@pytest.mark.parametrize("q_dt,c_dt,npages", [("float16", "bfloat16", 40), ("bfloat16", "float32", 3),
+                                              ("float32", "float16", 30)])
+def test_mla_latent_context_mixed_dtypes(dev, q_dt, c_dt, npages):
+    """The float32 latent context reads the query and the latents each in its
+    own dtype (the query's read once per row, the latents' per key), split and
+    one-pass shapes, against the float64 loop on the same values."""
+    import torch
+    from intent_attention.triton_mla_decode import mla_latent_context
+    _say("mla latent context, q", q_dt, "C", c_dt, "pages", npages)
+    rng = np.random.default_rng(npages)
+    d_c, ps = 576, 64
+    qa = torch.from_numpy(rng.standard_normal((2, 2, d_c)).astype(np.float32)).to(dev).to(getattr(torch, q_dt))
+    C = torch.from_numpy(rng.standard_normal((64 * ps, d_c)).astype(np.float32)).to(dev).to(getattr(torch, c_dt))
+    ids = rng.integers(0, 64, size=npages).astype(np.int32)
+    ctx = mla_latent_context(qa, C, torch.from_numpy(ids).to(dev), ps)
+    eye = np.eye(d_c, dtype=np.float32)   # the loop's projection by the identity gives the context itself
+    ref = M.mla_decode_cpu_loop(qa.float().cpu().numpy(), C.float().cpu().numpy(), eye, ids, ps)
+    err = float(np.abs(ctx.cpu().numpy() - ref).max())
+    _say(f"  max abs err {err:.2e}")
+    assert ctx.dtype == torch.float32 and err <= 2e-5 * max(1.0, float(np.abs(ref).max()))
