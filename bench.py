@@ -968,6 +968,75 @@ def run_mla_rows(args) -> None:
         "shapes": rows}), flush=True)
 
 
+# the selected-block fake-quant reconstruction under intent_quant_attention_reference
+# (the reference's intent_quant_attention.py:56-84, fake_quantize_tensor per block) in
+# float32: (leading rows, tokens, head_dim, [(block tokens, precision), ...]); the first
+# is cfg1's (32 pages of 16 tokens, FP16 / INT8 alternating), the second the reference
+# benchmark's layout (three quarter-context blocks) at 32 heads x 4,096 tokens
+FAKE_QUANT_CONFIGS = {
+    "fake-quant": [(8, 512, 64, [(16, p) for _ in range(16) for p in ("FP16", "INT8")]),
+                   (32, 4096, 128, [(1024, "INT8"), (1024, "INT4_RESIDUAL"), (1024, "FP8")]),
+                   (32, 4096, 128, [(64, "INT8")] * 64),
+                   (8, 4096, 64, [(256, "FP8")] * 16)],
+}
+
+
+def run_fake_quant(args) -> None:
+    """The selected-block reconstruction per shape: the C ABI call on resident
+    inputs and block table (kernels only, the split workspace allocated once)
+    and the Python entry point (_reconstruct_selected: block table upload,
+    output and workspace allocation, launch). The bytes are the selected K and V
+    values read once and their reconstruction written once (algorithmic)."""
+    from intent_attention import KVPrecision
+    from intent_attention import _native as N
+    from intent_attention.block_metadata import BlockPolicy, SemanticBlock
+    from intent_attention.intent_quant_attention import _FQ_CODE, _reconstruct_selected
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    g = torch.Generator(device=dev).manual_seed(5)
+    rows = []
+    for lead, T, d, spec in FAKE_QUANT_CONFIGS[args.config]:
+        k = torch.randn(lead, T, d, device=dev, generator=g)
+        v = torch.randn(lead, T, d, device=dev, generator=g)
+        lens = [n for n, _ in spec]
+        precs = [KVPrecision(p) for _, p in spec]
+        starts = [sum(lens[:i]) for i in range(len(lens))]
+        total = sum(lens)
+        meta = torch.tensor([[st, n, st, _FQ_CODE[p]] for st, n, p in zip(starts, lens, precs)],
+                            dtype=torch.int32, device=dev)
+        out = torch.empty(lead, total, 2 * d, device=dev)
+        a = N.FakeQuantBlocksArgs()
+        a.lead, a.num_blocks, a.k_dim, a.v_dim = lead, len(spec), d, d
+        a.k, a.k_stride_l, a.k_stride_t = k.data_ptr(), k.stride(0), k.stride(1)
+        a.v, a.v_stride_l, a.v_stride_t = v.data_ptr(), v.stride(0), v.stride(1)
+        a.blocks, a.max_block_tokens = meta.data_ptr(), max(lens)
+        a.out, a.out_stride_l, a.out_stride_t = out.data_ptr(), out.stride(0), out.stride(1)
+        wsb = N.fake_quant_blocks_workspace(a)
+        ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=dev)
+        h = stream.cuda_stream
+        kern = _time_steps(lambda: N.fake_quant_blocks(a, h, ws.data_ptr() if wsb else 0, wsb), args, stream)
+        blocks = [SemanticBlock(f"b{i}", st, st + n, BlockPolicy.ATTEND, 1.0) for i, (st, n) in enumerate(zip(starts, lens))]
+        api = _time_steps(lambda: _reconstruct_selected(k, v, blocks, precs), args, stream)
+        ab = 2 * lead * total * 2 * d * 4
+        rows.append({"shape": {"lead": lead, "tokens": total, "channels": 2 * d, "blocks": len(spec),
+                               "block_tokens": sorted(set(lens)), "precisions": sorted({p for _, p in spec})},
+                     "split_workspace_bytes": wsb, "us_per_call": round(kern["ms"] * 1e3, 2),
+                     "us_p10_p50_p90": kern["spread"], "api_us_per_call": round(api["ms"] * 1e3, 2),
+                     "algorithmic_bytes": ab, "gbps": round(ab / (kern["ms"] * 1e-3) / 1e9, 1)})
+        print(f"[bench] fake-quant {rows[-1]['shape']}: {rows[-1]['us_per_call']} us", file=sys.stderr, flush=True)
+    head = rows[1]
+    print(json.dumps({
+        "metric": "selected-block fake-quant reconstruction µs per call (the reference's "
+                  "intent_quant_attention.py:56-84 in float32)",
+        "value": head["us_per_call"], "unit": "us", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded N(0,1))",
+        "config": {"workload": "reconstruction shapes; value = 32 heads x 3 blocks of 1,024 tokens x 256 channels "
+                               "(INT8, INT4_RESIDUAL, FP8), split"},
+        "kernel_source_digest": source_digest(["fake_quant.hip"]),
+        "shapes": rows}), flush=True)
+
+
 def kernel_events(n: int, stream) -> list:
     """n pairs of timing events, each recorded once so its HIP event exists
     (torch creates events lazily); the library re-records them around the split
@@ -1129,7 +1198,7 @@ def main() -> None:
     ap.add_argument("--config", default="cfg3",
                     choices=sorted(CONFIGS) + ["cfg1"] + sorted(MLA_CONFIGS) + sorted(QUANT_CONFIGS)
                     + sorted(TABLE_CONFIGS) + sorted(TRANSCODE_CONFIGS) + sorted(DENSE_CONFIGS)
-                    + sorted(MLA_ROWS_CONFIGS))
+                    + sorted(MLA_ROWS_CONFIGS) + sorted(FAKE_QUANT_CONFIGS))
     ap.add_argument("--pages-per-split", type=int, default=0)
     ap.add_argument("--cpu-budget", type=float, default=CPU_BUDGET_S,
                     help="seconds of oracle work per CPU-baseline leg (one thread, then all cores)")
@@ -1189,6 +1258,9 @@ def main() -> None:
         return
     if args.config in MLA_ROWS_CONFIGS:
         run_mla_rows(args)
+        return
+    if args.config in FAKE_QUANT_CONFIGS:
+        run_fake_quant(args)
         return
     if args.config in MLA_CONFIGS:
         run_mla(args, cpu)

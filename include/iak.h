@@ -46,6 +46,10 @@
  *                               under semantic_block_attention() reference.py:81-129 and
  *                               intent_quant_attention_reference() intent_quant_attention.py:20-119
  *   iak_dense_attention_workspace (no counterpart: sizes the optional split-over-keys partial buffer)
+ *   iak_fake_quant_blocks       the per-block fake_quantize_tensor() reconstructions and their torch.cat
+ *                               in intent_quant_attention_reference() intent_quant_attention.py:56-84
+ *                               (intent_quant.py:221-312), float32 K and V
+ *   iak_fake_quant_blocks_workspace (no counterpart: sizes the optional split of long blocks)
  *   iak_status_string           (no counterpart: the reference raises ValueError/RuntimeError in Python)
  */
 #ifndef IAK_H
@@ -58,7 +62,7 @@
 extern "C" {
 #endif
 
-#define IAK_ABI_VERSION 9
+#define IAK_ABI_VERSION 10
 
 /* Grid size from which merge_in_kernel = 2 merges inside the decode kernel. */
 #define IAK_MERGE_IN_KERNEL_MIN_WORKGROUPS 1024
@@ -522,6 +526,42 @@ iak_status iak_dense_attention_workspace(const iak_dense_attention_args* args, s
 
 iak_status iak_dense_attention(const iak_dense_attention_args* args, void* workspace, size_t workspace_bytes,
                                void* stream);
+
+/* Fake-quant reconstruction of the selected blocks of float32 K and V, as
+ * intent_quant_attention_reference() concatenates them (intent_quant_attention.py:56-84,
+ * fake_quantize_tensor intent_quant.py:221-312): block i's tokens blocks[i][0] ..
+ * blocks[i][0] + blocks[i][1] - 1 of K and V, reconstructed at precision blocks[i][3]
+ * (IAK_FQ_*) with one scale per channel (absmax over every leading row and token of
+ * the block), land at tokens blocks[i][2] .. of out, K's channels first, then V's.
+ *   k [lead, T, k_dim], v [lead, T, v_dim] float32, element strides per leading row and
+ *     token, unit channel stride; k_dim + v_dim <= 2^20
+ *   blocks [num_blocks][4] int32 on the device (num_blocks < 2^22); the caller keeps the token ranges inside
+ *     K, V and out (the kernel does not check them)
+ *   out [lead, total, k_dim + v_dim] float32, element strides per leading row and token
+ *   max_block_tokens: the longest block's token count, or an upper bound on it (it sizes
+ *     the split below; a wrong value changes the speed, never the result)
+ * Every division is the IEEE float32 quotient and every code rounds to nearest even,
+ * as torch's float32 arithmetic, so the result equals the reference's bit for bit
+ * (an integer code of zero gives +0, as .to(int8).float() does).
+ * Without a workspace one workgroup takes each (block, 64 channels); with one of the
+ * size iak_fake_quant_blocks_workspace() gives (0: no split for these arguments), a
+ * block of many rows (leading rows x tokens) is split over several workgroups per
+ * channel group, whose per-channel maxima meet in the workspace over three launches. */
+enum { IAK_FQ_FP16 = 0, IAK_FQ_FP8 = 1, IAK_FQ_INT8 = 2, IAK_FQ_INT4 = 3, IAK_FQ_INT4_RESIDUAL = 4, IAK_FQ_SKIP = 5 };
+typedef struct {
+  int32_t lead, num_blocks, k_dim, v_dim;
+  const float* k; int64_t k_stride_l, k_stride_t;
+  const float* v; int64_t v_stride_l, v_stride_t;
+  const int32_t* blocks;
+  int32_t max_block_tokens;
+  float* out; int64_t out_stride_l, out_stride_t;
+} iak_fake_quant_blocks_args;
+
+/* Bytes of device workspace that lets iak_fake_quant_blocks split long blocks (0: no split). */
+iak_status iak_fake_quant_blocks_workspace(const iak_fake_quant_blocks_args* args, size_t* bytes);
+
+iak_status iak_fake_quant_blocks(const iak_fake_quant_blocks_args* args, void* workspace, size_t workspace_bytes,
+                                 void* stream);
 
 #ifdef __cplusplus
 }

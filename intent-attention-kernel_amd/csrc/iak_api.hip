@@ -331,6 +331,9 @@ iak_status scratch_address(int dev, void** out) {
 namespace iak {
 hipError_t launch_mla_rows(const iak_mla_rows_args& a, void* workspace, hipStream_t stream);   // mla_rows.hip
 size_t mla_rows_workspace(const iak_mla_rows_args& a);                                      // mla_rows.hip
+hipError_t launch_fake_quant_blocks(const iak_fake_quant_blocks_args& a, void* workspace,
+                                    hipStream_t stream);                    // fake_quant.hip
+size_t fake_quant_blocks_workspace(const iak_fake_quant_blocks_args& a);   // fake_quant.hip
 hipError_t launch_dense_attention(const iak_dense_attention_args& a, void* workspace,
                                   hipStream_t stream);                     // dense_attention.hip
 size_t dense_attention_workspace(const iak_dense_attention_args& a);     // dense_attention.hip
@@ -768,6 +771,49 @@ iak_status iak_dense_attention(const iak_dense_attention_args* a, void* workspac
     if (!aligned16(workspace)) return fail(IAK_EINVAL, "workspace must be 16-byte aligned");
   }
   const hipError_t e = iak::launch_dense_attention(*a, workspace, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(IAK_EHIP, "kernel launch failed: %s", hipGetErrorString(e));
+  return IAK_OK;
+}
+
+static iak_status validate_fake_quant(const iak_fake_quant_blocks_args* a) {
+  if (!a) return fail(IAK_EINVAL, "args is NULL");
+  if (a->lead < 0 || a->num_blocks < 0 || a->k_dim < 0 || a->v_dim < 0 || a->max_block_tokens < 0)
+    return fail(IAK_EINVAL, "negative size (lead=%d, num_blocks=%d, k_dim=%d, v_dim=%d, max_block_tokens=%d)",
+                a->lead, a->num_blocks, a->k_dim, a->v_dim, a->max_block_tokens);
+  if ((long long)a->k_dim + a->v_dim > (1LL << 20))
+    return fail(IAK_ENOTSUP, "k_dim + v_dim = %lld is not supported (at most 2^20)", (long long)a->k_dim + a->v_dim);
+  if (a->num_blocks >= (1 << 22))   // the grid's x extent in work-items stays below 2^32
+    return fail(IAK_ENOTSUP, "num_blocks = %d is not supported (below 2^22)", a->num_blocks);
+  if (a->lead == 0 || a->num_blocks == 0 || a->k_dim + a->v_dim == 0) return IAK_OK;
+  if (!a->blocks || !a->out || (a->k_dim > 0 && !a->k) || (a->v_dim > 0 && !a->v))
+    return fail(IAK_EINVAL, "k/v/blocks/out is NULL");
+  const long long strides[] = {a->k_stride_l, a->k_stride_t, a->v_stride_l, a->v_stride_t, a->out_stride_l,
+                               a->out_stride_t};
+  for (long long st : strides)
+    if (st < 0) return fail(IAK_EINVAL, "negative stride %lld", st);
+  return IAK_OK;
+}
+
+iak_status iak_fake_quant_blocks_workspace(const iak_fake_quant_blocks_args* a, size_t* bytes) {
+  if (!bytes) return fail(IAK_EINVAL, "bytes is NULL");
+  const iak_status st = validate_fake_quant(a);
+  if (st != IAK_OK) return st;
+  *bytes = (a->lead == 0 || a->num_blocks == 0 || a->k_dim + a->v_dim == 0) ? 0 : iak::fake_quant_blocks_workspace(*a);
+  return IAK_OK;
+}
+
+iak_status iak_fake_quant_blocks(const iak_fake_quant_blocks_args* a, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  const iak_status st = validate_fake_quant(a);
+  if (st != IAK_OK) return st;
+  if (a->lead == 0 || a->num_blocks == 0 || a->k_dim + a->v_dim == 0) return IAK_OK;
+  if (workspace) {
+    const size_t need = iak::fake_quant_blocks_workspace(*a);
+    if (workspace_bytes < need)
+      return fail(IAK_EINVAL, "workspace of %zu bytes is smaller than the %zu bytes required", workspace_bytes, need);
+    if (!aligned16(workspace)) return fail(IAK_EINVAL, "workspace must be 16-byte aligned");
+  }
+  const hipError_t e = iak::launch_fake_quant_blocks(*a, workspace, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(IAK_EHIP, "kernel launch failed: %s", hipGetErrorString(e));
   return IAK_OK;
 }

@@ -14,7 +14,7 @@ from typing import Optional
 _HERE = os.path.dirname(os.path.abspath(__file__))
 # IAK_LIBRARY selects another build of the same ABI (e.g. a tuning variant)
 LIB_PATH = os.environ.get("IAK_LIBRARY") or os.path.join(_HERE, "libiak.so")
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 IAK_OK, IAK_EINVAL, IAK_ENOTSUP, IAK_EHIP = 0, 1, 2, 3
 
@@ -145,6 +145,21 @@ class MlaRowsArgs(ctypes.Structure):
     ]
 
 
+FQ_FP16, FQ_FP8, FQ_INT8, FQ_INT4, FQ_INT4_RESIDUAL, FQ_SKIP = 0, 1, 2, 3, 4, 5   # IAK_FQ_*
+
+
+class FakeQuantBlocksArgs(ctypes.Structure):
+    """Mirror of ``iak_fake_quant_blocks_args`` (include/iak.h)."""
+
+    _fields_ = [
+        ("lead", c_i32), ("num_blocks", c_i32), ("k_dim", c_i32), ("v_dim", c_i32),
+        ("k", c_void_p), ("k_stride_l", c_i64), ("k_stride_t", c_i64),
+        ("v", c_void_p), ("v_stride_l", c_i64), ("v_stride_t", c_i64),
+        ("blocks", c_void_p), ("max_block_tokens", c_i32),
+        ("out", c_void_p), ("out_stride_l", c_i64), ("out_stride_t", c_i64),
+    ]
+
+
 class DenseAttentionArgs(ctypes.Structure):
     """Mirror of ``iak_dense_attention_args`` (include/iak.h)."""
 
@@ -170,7 +185,8 @@ EXPORTED = ("iak_abi_version", "iak_status_string", "iak_last_error",
             "iak_paged_decode_noalloc", "iak_transcode_pages", "iak_prefetch_pages", "iak_paged_decode_plan",
             "iak_mla_decode_rows", "iak_pack_page_descriptors",
             "iak_pack_entry_records", "iak_dense_attention", "iak_dense_attention_workspace",
-            "iak_mla_decode_rows_workspace")
+            "iak_mla_decode_rows_workspace", "iak_fake_quant_blocks",
+            "iak_fake_quant_blocks_workspace")
 NOALLOC_SCRATCH_BYTES = 16 << 20   # IAK_NOALLOC_SCRATCH_BYTES
 
 _lib: Optional[ctypes.CDLL] = None
@@ -226,6 +242,11 @@ def load() -> ctypes.CDLL:
     lib.iak_build_page_tables.restype = ctypes.c_int
     lib.iak_mla_decode_rows.restype = ctypes.c_int
     lib.iak_mla_decode_rows.argtypes = [ctypes.POINTER(MlaRowsArgs), c_void_p, ctypes.c_size_t, c_void_p]
+    lib.iak_fake_quant_blocks.restype = ctypes.c_int
+    lib.iak_fake_quant_blocks.argtypes = [ctypes.POINTER(FakeQuantBlocksArgs), c_void_p, ctypes.c_size_t, c_void_p]
+    lib.iak_fake_quant_blocks_workspace.restype = ctypes.c_int
+    lib.iak_fake_quant_blocks_workspace.argtypes = [ctypes.POINTER(FakeQuantBlocksArgs),
+                                                    ctypes.POINTER(ctypes.c_size_t)]
     lib.iak_mla_decode_rows_workspace.restype = ctypes.c_int
     lib.iak_mla_decode_rows_workspace.argtypes = [ctypes.POINTER(MlaRowsArgs), ctypes.POINTER(ctypes.c_size_t)]
     lib.iak_build_page_tables.argtypes = [ctypes.POINTER(PageTableArgs), c_void_p]
@@ -350,6 +371,16 @@ def mla_decode_rows(args: MlaRowsArgs, stream: int, workspace: int = 0, workspac
 
 def build_page_tables(args: PageTableArgs, stream: int) -> None:
     check(load().iak_build_page_tables(ctypes.byref(args), stream or None))
+
+
+def fake_quant_blocks_workspace(args: FakeQuantBlocksArgs) -> int:
+    n = ctypes.c_size_t(0)
+    check(load().iak_fake_quant_blocks_workspace(ctypes.byref(args), ctypes.byref(n)))
+    return n.value
+
+
+def fake_quant_blocks(args: FakeQuantBlocksArgs, stream: int, workspace: int = 0, workspace_bytes: int = 0) -> None:
+    check(load().iak_fake_quant_blocks(ctypes.byref(args), workspace or None, workspace_bytes, stream or None))
 
 
 def dense_attention_workspace(args: DenseAttentionArgs) -> int:

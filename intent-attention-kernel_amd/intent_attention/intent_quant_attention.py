@@ -34,11 +34,13 @@ Device tensors only: host tensors raise RuntimeError.
 from __future__ import annotations
 
 import functools
+import math
 from typing import Any, Dict, List
 
 import numpy as np
 import torch
 
+from . import _native as N
 from .block_metadata import BlockLayout
 from .decode_core import require_device
 from .intent_quant import IntentQuantizer, KVPrecision, QuantPolicy, _tdiv, compute_quant_error
@@ -113,6 +115,8 @@ def _reconstruct_selected(k: torch.Tensor, v: torch.Tensor, blocks: List, precs:
         groups.setdefault((p, n), []).append(i)
     pos_np = [(starts[idx][:, None] + np.arange(n, dtype=np.int64)[None, :]).reshape(-1)
               for (_, n), idx in groups.items()]
+    if _native_blocks_apply(k, v, total, precs):
+        return _reconstruct_native(k, v, lens, first, starts, tok_np, precs)
     flat = torch.from_numpy(np.concatenate([tok_np] + pos_np))
     if k.is_cuda:
         # staged in pinned memory (torch's caching host allocator keeps the
@@ -138,6 +142,63 @@ def _reconstruct_selected(k: torch.Tensor, v: torch.Tensor, blocks: List, precs:
     else:
         k_rec, v_rec = recs
     return k_rec, v_rec, tok, starts.tolist()
+
+
+_FQ_CODE = {KVPrecision.FP16: N.FQ_FP16, KVPrecision.FP8: N.FQ_FP8, KVPrecision.INT8: N.FQ_INT8,
+            KVPrecision.INT4: N.FQ_INT4, KVPrecision.INT4_RESIDUAL: N.FQ_INT4_RESIDUAL,
+            KVPrecision.SKIP: N.FQ_SKIP}
+
+
+def _native_blocks_apply(k: torch.Tensor, v: torch.Tensor, total: int, precs: List[KVPrecision]) -> bool:
+    """Whether libiak's fake-quant kernel builds the reconstruction: float32
+    device K and V with the same leading shape (K | V share one output
+    buffer), at least one block that is not FP16 (so torch.cat's result is
+    float32: FP16 blocks alone concatenate to float16), and a non-empty
+    leading shape and channel count, all within the kernel's int32 token and
+    row indices and its 2^20 channels."""
+    if not (k.is_cuda and k.dtype == torch.float32 and v.dtype == torch.float32
+            and k.shape[:-1] == v.shape[:-1] and k.dim() >= 2
+            and any(p != KVPrecision.FP16 for p in precs)):
+        return False
+    lead = math.prod(k.shape[:-2])
+    return (0 < total and k.size(-2) < 2 ** 31 and 0 < lead < 2 ** 31
+            and 0 < k.size(-1) + v.size(-1) <= 2 ** 20)
+
+
+def _reconstruct_native(k: torch.Tensor, v: torch.Tensor, lens: np.ndarray, first: np.ndarray,
+                        starts: np.ndarray, tok_np: np.ndarray, precs: List[KVPrecision]):
+    """``_reconstruct_selected`` on libiak's ``iak_fake_quant_blocks``: one
+    launch writes every block's K | V reconstruction (float32, bit for bit
+    the torch chain's) into ``[..., total, Dk + Dv]``, long blocks split over
+    several workgroups through a workspace. The token index and the per-block
+    table (source start, length, output start, precision) go up in one pinned
+    copy."""
+    total = int(starts[-1])
+    dk, dv = k.size(-1), v.size(-1)
+    meta = np.stack([first, lens, starts[:-1],
+                     np.array([_FQ_CODE[p] for p in precs], dtype=np.int64)], axis=1).astype(np.int32)
+    flat = torch.from_numpy(np.concatenate([tok_np, meta.reshape(-1).view(np.int64)]))
+    flat = flat.pin_memory().to(k.device, non_blocking=True)
+    tok = flat[:total]
+    blocks_dev = flat[total:].view(torch.int32)
+    lead_shape = k.shape[:-2]
+    k3 = k.reshape(-1, k.size(-2), dk)
+    v3 = v.reshape(-1, v.size(-2), dv)
+    k3 = k3 if k3.stride(-1) == 1 or dk <= 1 else k3.contiguous()
+    v3 = v3 if v3.stride(-1) == 1 or dv <= 1 else v3.contiguous()
+    out = torch.empty((k3.size(0), total, dk + dv), dtype=torch.float32, device=k.device)
+    a = N.FakeQuantBlocksArgs()
+    a.lead, a.num_blocks, a.k_dim, a.v_dim = k3.size(0), len(precs), dk, dv
+    a.k, a.k_stride_l, a.k_stride_t = k3.data_ptr(), k3.stride(0), k3.stride(1)
+    a.v, a.v_stride_l, a.v_stride_t = v3.data_ptr(), v3.stride(0), v3.stride(1)
+    a.blocks, a.max_block_tokens = blocks_dev.data_ptr(), int(lens.max())
+    a.out, a.out_stride_l, a.out_stride_t = out.data_ptr(), out.stride(0), out.stride(1)
+    nws = N.fake_quant_blocks_workspace(a)
+    ws = torch.empty(nws, dtype=torch.uint8, device=k.device) if nws else None
+    N.fake_quant_blocks(a, torch.cuda.current_stream(k.device).cuda_stream,
+                        ws.data_ptr() if ws is not None else 0, nws)
+    out = out.reshape(*lead_shape, total, dk + dv)
+    return out[..., :dk], out[..., dk:], tok, starts.tolist()
 
 
 def intent_quant_attention_reference(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layout: BlockLayout,

@@ -257,6 +257,64 @@ void invalid_launches() {
     std::printf("abi-asan: a 100-key shape should not be split\n");
     std::exit(1);
   }
+
+  // fake-quant reconstruction: a negative size, a NULL operand, a negative
+  // stride or more than 2^20 channels is rejected; empty work returns OK
+  // without a launch
+  iak_fake_quant_blocks_args fq;
+  for (int i = 0; i < 300; ++i) {
+    random_bytes(fq);
+    switch (rng() % 4) {
+      case 0: fq.lead = -1 - (int32_t)(rng() % 50); break;
+      case 1: fq.k_dim = (1 << 20) + 1 + (int32_t)(rng() % 50); fq.v_dim = (int32_t)(rng() % 50); break;
+      case 2: fq.lead = 1; fq.num_blocks = 1; fq.k_dim = 4; fq.v_dim = 4; fq.blocks = nullptr; break;
+      default:
+        fq.lead = 1; fq.num_blocks = 1; fq.k_dim = 4; fq.v_dim = 4;
+        fq.k = fq.v = reinterpret_cast<const float*>(0x1000); fq.out = reinterpret_cast<float*>(0x1000);
+        fq.blocks = reinterpret_cast<const int32_t*>(0x1000); fq.v_stride_t = -1 - (int64_t)(rng() % 50);
+        break;
+    }
+    count(iak_fake_quant_blocks(&fq, nullptr, 0, nullptr));
+  }
+  count(iak_fake_quant_blocks(nullptr, nullptr, 0, nullptr));
+  std::memset(&fq, 0, sizeof(fq));
+  fq.lead = 3; fq.k_dim = 64; fq.v_dim = 64;   // no blocks: nothing to launch
+  if (iak_fake_quant_blocks(&fq, nullptr, 0, nullptr) != IAK_OK) {
+    std::printf("abi-asan: an empty fake-quant call was not accepted\n");
+    std::exit(1);
+  }
+  // workspace sizes of random and of valid arguments (host queries); a long
+  // block asks for a split workspace, and one byte short is rejected
+  for (int i = 0; i < 2000; ++i) {
+    random_bytes(fq);
+    if (rng() % 2) {
+      fq.lead = pick_int(); fq.num_blocks = pick_int(); fq.k_dim = pick_int() & 0xFFFF;
+      fq.v_dim = pick_int() & 0xFFFF; fq.max_block_tokens = pick_int();
+      fq.k = fq.v = reinterpret_cast<const float*>(0x1000); fq.out = reinterpret_cast<float*>(0x1000);
+      fq.blocks = reinterpret_cast<const int32_t*>(0x1000);
+      fq.k_stride_l = fq.k_stride_t = fq.v_stride_l = fq.v_stride_t = fq.out_stride_l = fq.out_stride_t = 1;
+    }
+    count(iak_fake_quant_blocks_workspace(&fq, &wsb));
+  }
+  count(iak_fake_quant_blocks_workspace(nullptr, &wsb));
+  std::memset(&fq, 0, sizeof(fq));
+  fq.lead = 8; fq.num_blocks = 16; fq.k_dim = 64; fq.v_dim = 64; fq.max_block_tokens = 256;
+  fq.k = fq.v = reinterpret_cast<const float*>(0x1000); fq.out = reinterpret_cast<float*>(0x1000);
+  fq.blocks = reinterpret_cast<const int32_t*>(0x1000);
+  count(iak_fake_quant_blocks_workspace(&fq, nullptr));
+  if (iak_fake_quant_blocks_workspace(&fq, &wsb) != IAK_OK || wsb == 0) {
+    std::printf("abi-asan: 16 blocks of 8 x 256 rows should ask for a split workspace\n");
+    std::exit(1);
+  }
+  if (iak_fake_quant_blocks(&fq, reinterpret_cast<void*>(0x1000), wsb - 1, nullptr) != IAK_EINVAL) {
+    std::printf("abi-asan: a short fake-quant workspace was not rejected\n");
+    std::exit(1);
+  }
+  fq.max_block_tokens = 16;
+  if (iak_fake_quant_blocks_workspace(&fq, &wsb) != IAK_OK || wsb != 0) {
+    std::printf("abi-asan: blocks of 8 x 16 rows should not be split\n");
+    std::exit(1);
+  }
 }
 
 }  // namespace

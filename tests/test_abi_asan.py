@@ -16,7 +16,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(ROOT, "intent-attention-kernel_amd", "csrc")
 BUILD = os.path.join(CSRC, "_build")
 ROCM = "/opt/rocm"
-OTHERS = ("paged_decode", "mla_decode", "mla_rows", "dense_attention", "quantize", "page_tables", "memory_manager")
+OTHERS = ("paged_decode", "mla_decode", "mla_rows", "dense_attention", "fake_quant", "quantize", "page_tables", "memory_manager")
 
 
 def test_abi_validation_under_host_asan(tmp_path):
