@@ -652,6 +652,7 @@ def run_quantize(args, cpu=None) -> None:
            "config": {"workload": f"{args.config}: {sum(j['src'].shape[0] for j in wl['jobs'])} pages of 16x128 "
                                   f"quantised into 1,048,576-slot K and V pools (6 launches per step)",
                       "algorithmic_bytes": ab},
+           "kernel_source_digest": source_digest(["quantize.hip", "iak_internal.h", "iak_device.h"]),
            "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None}}
     if cpu is not None:
@@ -765,6 +766,7 @@ def run_tables(args, cpu=None) -> None:
                                   f"{wl['begin'].numel()} routed blocks, {pairs} selected pages per KV head "
                                   f"summed over sequences, width {cfg['W']}, {wl['NP']}-page precision array",
                       "algorithmic_bytes": ab},
+           "kernel_source_digest": source_digest(["page_tables.hip", "iak_internal.h"]),
            "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None}}
     if cpu is not None:
@@ -850,6 +852,7 @@ def run_transcode(args, cpu=None) -> None:
            "config": {"workload": f"{args.config}: {n} random slots of a {NP}-page pool of 16x128 float16 pages "
                                   f"demoted to INT8 and promoted back (2 launches per step)",
                       "algorithmic_bytes": ab, "kernels": kern},
+           "kernel_source_digest": source_digest(["memory_manager.hip", "iak_internal.h", "iak_device.h"]),
            "roofline": {"bound": "hbm", "achieved": kern[dom]["GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                         "frac": round(kern[dom]["GBps"] / HBM_PEAK_GBPS, 4), "traffic": None,
                         "kernel": f"transcode_{dom}_kernel", "kernel_us": kern[dom]["us"]}}
