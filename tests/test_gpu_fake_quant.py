@@ -245,3 +245,42 @@ def test_split_equals_one_pass_through_the_c_abi(dev):
     assert _bits_equal(split, one)
     assert _bits_equal(one[..., :dk], _oracle_cat(k, spans, names))
     assert _bits_equal(one[..., dk:], _oracle_cat(v, spans, names))
+
+
+def test_fuzz_bit_exact(dev):
+    """24 seeded cases: leading shapes of 1-3 dims, 1-40 leading rows, K and V
+    widths from 1 to 200 channels, 1-12 blocks of 1-300 tokens in shuffled
+    order with random precisions, magnitudes spread over a few decades and a
+    token stride wider than the rows; each against the oracle bit for bit
+    (one pass or split, as the workspace rule picks)."""
+    import torch
+    rng = np.random.default_rng(2026)
+    for case in range(24):
+        nlead = int(rng.integers(1, 4))
+        lead = tuple(int(x) for x in rng.integers(1, 5, size=nlead))
+        if case % 6 == 5:
+            lead = (int(rng.integers(20, 41)),)
+        dk, dv = int(rng.integers(1, 201)), int(rng.integers(1, 201))
+        nb = int(rng.integers(1, 13))
+        lens = [int(x) for x in rng.integers(1, 301 if case % 4 == 0 else 40, size=nb)]
+        gaps = [int(x) for x in rng.integers(0, 5, size=nb)]
+        spans, t = [], 0
+        for n, gp in zip(lens, gaps):
+            spans.append((t + gp, t + gp + n))
+            t += gp + n
+        T = t + int(rng.integers(0, 8))
+        order = rng.permutation(nb)
+        spans = [spans[i] for i in order]
+        precs = [str(p) for p in rng.choice(PRECS, size=nb)]
+        if all(p == "FP16" for p in precs):
+            precs[0] = "INT8"
+        scale = (10.0 ** rng.uniform(-3, 2, size=(dk,))).astype(np.float32)
+        k = (rng.standard_normal((*lead, T, dk)) * scale).astype(np.float32)
+        v = (rng.standard_normal((*lead, T, dv)) * 10.0 ** rng.uniform(-2, 1)).astype(np.float32)
+        _say("fake-quant fuzz", case, lead, T, dk, dv, nb, precs)
+        wide = torch.zeros((*lead, T, dk + 3), device=dev)
+        wide[..., 1:dk + 1] = torch.from_numpy(k).to(dev)
+        k_dev = wide[..., 1:dk + 1]                          # token stride dk + 3
+        kr, vr = _run(dev, k, v, spans, precs, k_dev=k_dev)
+        assert _bits_equal(kr, _oracle_cat(k, spans, precs)), (case, lead, dk, dv, spans, precs)
+        assert _bits_equal(vr, _oracle_cat(v, spans, precs)), (case, lead, dk, dv, spans, precs)
