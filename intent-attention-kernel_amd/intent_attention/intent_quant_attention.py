@@ -35,6 +35,7 @@ from __future__ import annotations
 
 import functools
 import math
+from collections import OrderedDict
 from typing import Any, Dict, List
 
 import numpy as np
@@ -104,6 +105,9 @@ def _reconstruct_selected(k: torch.Tensor, v: torch.Tensor, blocks: List, precs:
         return functools.reduce(torch.promote_types, {
             torch.float16 if p == KVPrecision.FP16 else
             (x.dtype if p == KVPrecision.SKIP else torch.promote_types(torch.float32, x.dtype)) for p in precs})
+    spans = tuple((b.start, b.end) for b in blocks)
+    if _native_blocks_apply(k, v, sum(e - s for s, e in spans), precs):
+        return _reconstruct_native(k, v, spans, precs)
     lens = np.array([b.end - b.start for b in blocks], dtype=np.int64)
     first = np.array([b.start for b in blocks], dtype=np.int64)
     starts = np.concatenate(([0], np.cumsum(lens)))
@@ -115,8 +119,6 @@ def _reconstruct_selected(k: torch.Tensor, v: torch.Tensor, blocks: List, precs:
         groups.setdefault((p, n), []).append(i)
     pos_np = [(starts[idx][:, None] + np.arange(n, dtype=np.int64)[None, :]).reshape(-1)
               for (_, n), idx in groups.items()]
-    if _native_blocks_apply(k, v, total, precs):
-        return _reconstruct_native(k, v, lens, first, starts, tok_np, precs)
     flat = torch.from_numpy(np.concatenate([tok_np] + pos_np))
     if k.is_cuda:
         # staged in pinned memory (torch's caching host allocator keeps the
@@ -165,22 +167,49 @@ def _native_blocks_apply(k: torch.Tensor, v: torch.Tensor, total: int, precs: Li
             and 0 < k.size(-1) + v.size(-1) <= 2 ** 20)
 
 
-def _reconstruct_native(k: torch.Tensor, v: torch.Tensor, lens: np.ndarray, first: np.ndarray,
-                        starts: np.ndarray, tok_np: np.ndarray, precs: List[KVPrecision]):
-    """``_reconstruct_selected`` on libiak's ``iak_fake_quant_blocks``: one
-    launch writes every block's K | V reconstruction (float32, bit for bit
-    the torch chain's) into ``[..., total, Dk + Dv]``, long blocks split over
-    several workgroups through a workspace. The token index and the per-block
-    table (source start, length, output start, precision) go up in one pinned
-    copy."""
+# block tables of recent layouts: (device, stream, spans, precisions) ->
+# (token index, kernel block table, block starts, longest block), on the device
+_TABLES: "OrderedDict[tuple, tuple]" = OrderedDict()
+_TABLES_SIZE = 16
+
+
+def _block_tables(dev: torch.device, spans: tuple, precs: List[KVPrecision]):
+    """The selected tokens' index and ``iak_fake_quant_blocks``' block table
+    (source start, length, output start, precision per block) for these spans
+    and precisions, uploaded in one pinned copy on the current stream, and kept
+    for later calls over the same layout on the same stream (the tables are
+    read-only; at most ``_TABLES_SIZE`` layouts, least recently used first
+    out)."""
+    key = (dev, torch.cuda.current_stream(dev).cuda_stream, spans, tuple(precs))
+    ent = _TABLES.get(key)
+    if ent is not None:
+        _TABLES.move_to_end(key)
+        return ent
+    lens = np.array([e - s for s, e in spans], dtype=np.int64)
+    first = np.array([s for s, _ in spans], dtype=np.int64)
+    starts = np.concatenate(([0], np.cumsum(lens)))
     total = int(starts[-1])
-    dk, dv = k.size(-1), v.size(-1)
+    tok_np = np.repeat(first - starts[:-1], lens) + np.arange(total, dtype=np.int64)
     meta = np.stack([first, lens, starts[:-1],
                      np.array([_FQ_CODE[p] for p in precs], dtype=np.int64)], axis=1).astype(np.int32)
     flat = torch.from_numpy(np.concatenate([tok_np, meta.reshape(-1).view(np.int64)]))
-    flat = flat.pin_memory().to(k.device, non_blocking=True)
-    tok = flat[:total]
-    blocks_dev = flat[total:].view(torch.int32)
+    flat = flat.pin_memory().to(dev, non_blocking=True)
+    ent = (flat[:total], flat[total:].view(torch.int32), tuple(starts.tolist()), int(lens.max()))
+    _TABLES[key] = ent
+    if len(_TABLES) > _TABLES_SIZE:
+        _TABLES.popitem(last=False)
+    return ent
+
+
+def _reconstruct_native(k: torch.Tensor, v: torch.Tensor, spans: tuple, precs: List[KVPrecision]):
+    """``_reconstruct_selected`` on libiak's ``iak_fake_quant_blocks``: one
+    launch writes every block's K | V reconstruction (float32, bit for bit
+    the torch chain's) into ``[..., total, Dk + Dv]``, long blocks split over
+    several workgroups through a workspace. The block table comes from
+    ``_block_tables`` (one upload per layout and stream)."""
+    tok, blocks_dev, starts, longest = _block_tables(k.device, spans, precs)
+    total = starts[-1]
+    dk, dv = k.size(-1), v.size(-1)
     lead_shape = k.shape[:-2]
     k3 = k.reshape(-1, k.size(-2), dk)
     v3 = v.reshape(-1, v.size(-2), dv)
@@ -191,14 +220,14 @@ def _reconstruct_native(k: torch.Tensor, v: torch.Tensor, lens: np.ndarray, firs
     a.lead, a.num_blocks, a.k_dim, a.v_dim = k3.size(0), len(precs), dk, dv
     a.k, a.k_stride_l, a.k_stride_t = k3.data_ptr(), k3.stride(0), k3.stride(1)
     a.v, a.v_stride_l, a.v_stride_t = v3.data_ptr(), v3.stride(0), v3.stride(1)
-    a.blocks, a.max_block_tokens = blocks_dev.data_ptr(), int(lens.max())
+    a.blocks, a.max_block_tokens = blocks_dev.data_ptr(), longest
     a.out, a.out_stride_l, a.out_stride_t = out.data_ptr(), out.stride(0), out.stride(1)
     nws = N.fake_quant_blocks_workspace(a)
     ws = torch.empty(nws, dtype=torch.uint8, device=k.device) if nws else None
     N.fake_quant_blocks(a, torch.cuda.current_stream(k.device).cuda_stream,
                         ws.data_ptr() if ws is not None else 0, nws)
     out = out.reshape(*lead_shape, total, dk + dv)
-    return out[..., :dk], out[..., dk:], tok, starts.tolist()
+    return out[..., :dk], out[..., dk:], tok, list(starts)
 
 
 def intent_quant_attention_reference(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layout: BlockLayout,
