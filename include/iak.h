@@ -23,6 +23,7 @@
  *                               entry by entry) packed into one 32-byte record per entry)
  *   iak_paged_decode_timed,     (no counterpart: the same calls with HIP events around the split
  *   iak_mla_decode_timed         kernel, for timing it apart from the merge)
+ *   iak_timing_event_*          (no counterpart: fence-free HIP timing events for those calls)
  *   iak_mla_decode              mla_decode_triton() / _mla_decode_cpu()    triton_mla_decode.py:110-186
  *                               (the latent context; mla_sparse_decode_reference mla.py:61-92,
  *                               mla_triton_decode mla.py:95-136)
@@ -62,7 +63,7 @@
 extern "C" {
 #endif
 
-#define IAK_ABI_VERSION 10
+#define IAK_ABI_VERSION 11
 
 /* Grid size from which merge_in_kernel = 2 merges inside the decode kernel. */
 #define IAK_MERGE_IN_KERNEL_MIN_WORKGROUPS 1024
@@ -315,6 +316,18 @@ iak_status iak_mla_decode(const iak_mla_decode_args* args, void* workspace, size
  * (no counterpart in the reference). */
 iak_status iak_mla_decode_timed(const iak_mla_decode_args* args, void* workspace, size_t workspace_bytes,
                                 void* stream, void* ev_begin, void* ev_end);
+
+/* Timing events for the _timed entry points and for a harness's own brackets (no
+ * counterpart in the reference; bench.py's per-launch figures). They are hipEvent_t
+ * handles created with hipEventDisableSystemFence: recording one does not write back
+ * and invalidate the caches, whose cost a default event adds to the interval it
+ * closes after a kernel that wrote many MB (the MLA split kernel's partials). They
+ * order nothing for the host: read them with iak_timing_event_elapsed (milliseconds
+ * from `start` to `end`) only after a device synchronize. */
+iak_status iak_timing_event_create(void** event);
+iak_status iak_timing_event_record(void* event, void* stream);
+iak_status iak_timing_event_elapsed(void* start, void* end, float* ms);
+iak_status iak_timing_event_destroy(void* event);
 
 /*
  * Quantise-on-write: float16 pages [num_pages, page_size, head_dim] -> codes and

@@ -609,6 +609,36 @@ iak_status iak_mla_decode_timed(const iak_mla_decode_args* a, void* workspace, s
   return mla_decode_impl(a, workspace, workspace_bytes, stream, ev_begin, ev_end);
 }
 
+iak_status iak_timing_event_create(void** event) {
+  if (!event) return fail(IAK_EINVAL, "event is NULL");
+  hipEvent_t e = nullptr;
+  const hipError_t err = hipEventCreateWithFlags(&e, hipEventDisableSystemFence);
+  if (err != hipSuccess) return fail(IAK_EHIP, "hipEventCreateWithFlags failed: %s", hipGetErrorString(err));
+  *event = e;
+  return IAK_OK;
+}
+
+iak_status iak_timing_event_record(void* event, void* stream) {
+  if (!event) return fail(IAK_EINVAL, "event is NULL");
+  const hipError_t err = hipEventRecord(static_cast<hipEvent_t>(event), static_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(IAK_EHIP, "hipEventRecord failed: %s", hipGetErrorString(err));
+  return IAK_OK;
+}
+
+iak_status iak_timing_event_elapsed(void* start, void* end, float* ms) {
+  if (!start || !end || !ms) return fail(IAK_EINVAL, "start/end/ms is NULL");
+  const hipError_t err = hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(end));
+  if (err != hipSuccess) return fail(IAK_EHIP, "hipEventElapsedTime failed: %s", hipGetErrorString(err));
+  return IAK_OK;
+}
+
+iak_status iak_timing_event_destroy(void* event) {
+  if (!event) return IAK_OK;
+  const hipError_t err = hipEventDestroy(static_cast<hipEvent_t>(event));
+  if (err != hipSuccess) return fail(IAK_EHIP, "hipEventDestroy failed: %s", hipGetErrorString(err));
+  return IAK_OK;
+}
+
 iak_status iak_quantize_pages(const iak_quantize_args* a, void* stream) {
   if (!a) return fail(IAK_EINVAL, "args is NULL");
   if (a->num_pages < 0 || a->pool_pages < 0) return fail(IAK_EINVAL, "negative page count");

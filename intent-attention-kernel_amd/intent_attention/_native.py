@@ -14,7 +14,7 @@ from typing import Optional
 _HERE = os.path.dirname(os.path.abspath(__file__))
 # IAK_LIBRARY selects another build of the same ABI (e.g. a tuning variant)
 LIB_PATH = os.environ.get("IAK_LIBRARY") or os.path.join(_HERE, "libiak.so")
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 IAK_OK, IAK_EINVAL, IAK_ENOTSUP, IAK_EHIP = 0, 1, 2, 3
 
@@ -186,7 +186,8 @@ EXPORTED = ("iak_abi_version", "iak_status_string", "iak_last_error",
             "iak_mla_decode_rows", "iak_pack_page_descriptors",
             "iak_pack_entry_records", "iak_dense_attention", "iak_dense_attention_workspace",
             "iak_mla_decode_rows_workspace", "iak_fake_quant_blocks",
-            "iak_fake_quant_blocks_workspace")
+            "iak_fake_quant_blocks_workspace", "iak_timing_event_create", "iak_timing_event_record",
+            "iak_timing_event_elapsed", "iak_timing_event_destroy")
 NOALLOC_SCRATCH_BYTES = 16 << 20   # IAK_NOALLOC_SCRATCH_BYTES
 
 _lib: Optional[ctypes.CDLL] = None
@@ -242,6 +243,14 @@ def load() -> ctypes.CDLL:
     lib.iak_build_page_tables.restype = ctypes.c_int
     lib.iak_mla_decode_rows.restype = ctypes.c_int
     lib.iak_mla_decode_rows.argtypes = [ctypes.POINTER(MlaRowsArgs), c_void_p, ctypes.c_size_t, c_void_p]
+    lib.iak_timing_event_create.restype = ctypes.c_int
+    lib.iak_timing_event_create.argtypes = [ctypes.POINTER(c_void_p)]
+    lib.iak_timing_event_record.restype = ctypes.c_int
+    lib.iak_timing_event_record.argtypes = [c_void_p, c_void_p]
+    lib.iak_timing_event_elapsed.restype = ctypes.c_int
+    lib.iak_timing_event_elapsed.argtypes = [c_void_p, c_void_p, ctypes.POINTER(ctypes.c_float)]
+    lib.iak_timing_event_destroy.restype = ctypes.c_int
+    lib.iak_timing_event_destroy.argtypes = [c_void_p]
     lib.iak_fake_quant_blocks.restype = ctypes.c_int
     lib.iak_fake_quant_blocks.argtypes = [ctypes.POINTER(FakeQuantBlocksArgs), c_void_p, ctypes.c_size_t, c_void_p]
     lib.iak_fake_quant_blocks_workspace.restype = ctypes.c_int
@@ -371,6 +380,35 @@ def mla_decode_rows(args: MlaRowsArgs, stream: int, workspace: int = 0, workspac
 
 def build_page_tables(args: PageTableArgs, stream: int) -> None:
     check(load().iak_build_page_tables(ctypes.byref(args), stream or None))
+
+
+class TimingEvent:
+    """A fence-free HIP timing event (``iak_timing_event_create``): ``record``,
+    ``elapsed_time`` (ms, read after a device synchronize) and ``cuda_event``
+    (the handle the ``_timed`` entry points take), as torch.cuda.Event offers
+    them; destroyed with the object."""
+
+    def __init__(self) -> None:
+        h = c_void_p()
+        check(load().iak_timing_event_create(ctypes.byref(h)))
+        self._h = h.value
+
+    @property
+    def cuda_event(self) -> int:
+        return self._h
+
+    def record(self, stream) -> None:
+        check(load().iak_timing_event_record(self._h, getattr(stream, "cuda_stream", stream) or None))
+
+    def elapsed_time(self, end: "TimingEvent") -> float:
+        ms = ctypes.c_float(0.0)
+        check(load().iak_timing_event_elapsed(self._h, end._h, ctypes.byref(ms)))
+        return ms.value
+
+    def __del__(self) -> None:
+        h, self._h = getattr(self, "_h", None), None
+        if h and _lib is not None:
+            _lib.iak_timing_event_destroy(h)
 
 
 def fake_quant_blocks_workspace(args: FakeQuantBlocksArgs) -> int:

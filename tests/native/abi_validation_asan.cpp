@@ -315,6 +315,19 @@ void invalid_launches() {
     std::printf("abi-asan: blocks of 8 x 16 rows should not be split\n");
     std::exit(1);
   }
+
+  // timing events: NULL handles and outputs are rejected before any HIP call
+  float ms = 0.f;
+  if (iak_timing_event_create(nullptr) != IAK_EINVAL || iak_timing_event_record(nullptr, nullptr) != IAK_EINVAL ||
+      iak_timing_event_elapsed(nullptr, nullptr, &ms) != IAK_EINVAL ||
+      iak_timing_event_elapsed(reinterpret_cast<void*>(0x1000), reinterpret_cast<void*>(0x1000), nullptr) !=
+          IAK_EINVAL ||
+      iak_timing_event_destroy(nullptr) != IAK_OK) {
+    std::printf("abi-asan: a NULL timing-event argument was not handled\n");
+    std::exit(1);
+  }
+  calls += 5;
+  rejected += 4;
 }
 
 }  // namespace
