@@ -155,16 +155,16 @@ def _native_blocks_apply(k: torch.Tensor, v: torch.Tensor, total: int, precs: Li
     """Whether libiak's fake-quant kernel builds the reconstruction: float32
     device K and V with the same leading shape (K | V share one output
     buffer), at least one block that is not FP16 (so torch.cat's result is
-    float32: FP16 blocks alone concatenate to float16), and a non-empty
-    leading shape and channel count, all within the kernel's int32 token and
-    row indices and its 2^20 channels."""
+    float32: FP16 blocks alone concatenate to float16), a non-empty leading
+    shape and channels in both K and V, all within the kernel's int32 token
+    and row indices and its 2^20 channels."""
     if not (k.is_cuda and k.dtype == torch.float32 and v.dtype == torch.float32
             and k.shape[:-1] == v.shape[:-1] and k.dim() >= 2
             and any(p != KVPrecision.FP16 for p in precs)):
         return False
     lead = math.prod(k.shape[:-2])
     return (0 < total and k.size(-2) < 2 ** 31 and 0 < lead < 2 ** 31
-            and 0 < k.size(-1) + v.size(-1) <= 2 ** 20)
+            and k.size(-1) > 0 and v.size(-1) > 0 and k.size(-1) + v.size(-1) <= 2 ** 20)
 
 
 # block tables of recent layouts: (device, stream, spans, precisions) ->
