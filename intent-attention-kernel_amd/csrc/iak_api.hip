@@ -131,13 +131,21 @@ iak_status validate(const iak_paged_decode_args* a, Plan* plan, bool tiers = tru
     // 64-entry splits keep HBM busy from 2048 waves on. Smaller grids are
     // latency-bound: there the splits shrink until there is one workgroup per
     // CU (the same work on every CU; a grid of 2 or 3 workgroups per CU, or an
-    // uneven one, measured slower), but not below 8 entries
+    // uneven one, measured slower), but not below ceil(W / 64) entries clamped
+    // to [2, 8]: at most ~64 splits per row for the merge to read, and never
+    // the single-entry splits whose prologue outweighs their page. Measured
+    // (random pages of a 65,536-page pool, best split length in brackets):
+    // 8 rows x 64 entries 12.0 -> 10.2 us (2), 32 x 64 13.9 -> 12.2 (2),
+    // 8 x 256 14.2 -> 13.4 (4), 16 x 200 14.3 -> 13.3 (4), 64 x 100 15.0 ->
+    // 14.4 (7); 2 x 512 and 1 x 1,000 keep 8, their best (1 x 1,000: 17.4 us,
+    // against 19.6 at 16 entries and 19.8 at 4)
     chunk = 64;
     if (rows * ((W + 63) / 64) < 2048) {
       const long long want = (long long)IAK_GPU_CUS * IAK_WAVES_PER_BLOCK;   // waves = splits x rows
       const long long splits_per_row = (want + rows - 1) / (rows > 0 ? rows : 1);
+      const int least = (W + 63) / 64 < 2 ? 2 : ((W + 63) / 64 > 8 ? 8 : (W + 63) / 64);
       chunk = (int)((W + splits_per_row - 1) / splits_per_row);
-      chunk = chunk < 8 ? 8 : (chunk > 64 ? 64 : chunk);
+      chunk = chunk < least ? least : (chunk > 64 ? 64 : chunk);
     }
     // the same number of splits with even lengths (cfg3: 26 splits of 63
     // entries instead of 25 of 64 and one of 38; kernel 329.1 -> 327.7 us)
