@@ -65,8 +65,14 @@ extern "C" {
 
 #define IAK_ABI_VERSION 11
 
-/* Grid size from which merge_in_kernel = 2 merges inside the decode kernel. */
+/* Grid size from which merge_in_kernel = 2 merges inside the decode kernel; it
+ * also does so on grids of at most IAK_MERGE_IN_KERNEL_SMALL_WORKGROUPS workgroups
+ * whose rows hold at most IAK_MERGE_IN_KERNEL_SMALL_PARTIALS split partials
+ * (splits x query heads per KV head), where a second launch costs more than the
+ * last workgroup's merge. */
 #define IAK_MERGE_IN_KERNEL_MIN_WORKGROUPS 1024
+#define IAK_MERGE_IN_KERNEL_SMALL_WORKGROUPS 128
+#define IAK_MERGE_IN_KERNEL_SMALL_PARTIALS 256
 
 typedef enum {
   IAK_OK = 0,
@@ -131,7 +137,8 @@ enum { IAK_DTYPE_F16 = 0, IAK_DTYPE_F32 = 1, IAK_DTYPE_BF16 = 2 };
  *   merge_in_kernel  0: a merge kernel combines the split partials after the decode kernel.
  *                1: the decode kernel merges them itself. 2: automatic -- in-kernel for grids
  *                of at least IAK_MERGE_IN_KERNEL_MIN_WORKGROUPS workgroups (where the merges
- *                overlap other workgroups' page streaming), else the merge kernel. In-kernel,
+ *                overlap other workgroups' page streaming) and for the small grids named
+ *                beside that constant (one launch instead of two), else the merge kernel. In-kernel,
  *                the four waves of a workgroup
  *                reduce four consecutive splits of one row (the split count is rounded up
  *                to a multiple of four) and combine them in LDS into one partial; the

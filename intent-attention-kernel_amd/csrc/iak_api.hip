@@ -186,9 +186,19 @@ iak_status validate(const iak_paged_decode_args* a, Plan* plan, bool tiers = tru
   // overlaps other workgroups' page streaming; its three dependent memory
   // round trips otherwise lengthen the tail: cfg3, 1,792 workgroups, 337.6 ->
   // 333.9 us per step; cfg2, 512, unchanged; cfg4, 256, 42.4 -> 43.0 us)
+  // (automatic, small grids: the same when the grid has at most 128
+  // workgroups and a row at most 256 partials to merge, where the merge
+  // kernel's launch costs more than the last workgroup's merge: 8 rows x 64
+  // entries, one query head per KV head, 10.5 -> 8.5 us; four heads 10.9 ->
+  // 9.8 us; 8 x 256 entries 13.2 -> 12.6 us; against 1 row x 64 splits x 16
+  // heads 17.6 -> 35.2 us and 32 rows x 32 splits 12.0 -> 12.5 us)
   bool fused = a->merge_in_kernel != 0 && splits > 1;
-  if (fused && a->merge_in_kernel == 2)
-    fused = rows * (long long)((splits + 3) / 4) >= IAK_MERGE_IN_KERNEL_MIN_WORKGROUPS;
+  if (fused && a->merge_in_kernel == 2) {
+    const long long wgs = rows * (long long)((splits + 3) / 4);
+    fused = wgs >= IAK_MERGE_IN_KERNEL_MIN_WORKGROUPS ||
+            (wgs <= IAK_MERGE_IN_KERNEL_SMALL_WORKGROUPS &&
+             (long long)((splits + 3) / 4 * 4) * G <= IAK_MERGE_IN_KERNEL_SMALL_PARTIALS);
+  }
   if (fused && splitsA == splits) {
     splits = (splits + 3) / 4 * 4;
     splitsA = splits;
