@@ -208,6 +208,28 @@ def _decode_args(N, B, Hkv, G, W):
     return a
 
 
+def test_small_grid_plans_without_gpu():
+    """Latency-bound grids: the automatic split length falls to one workgroup
+    per CU but not below ceil(W / 64) entries clamped to [2, 8], and grids of
+    at most IAK_MERGE_IN_KERNEL_SMALL_WORKGROUPS workgroups whose rows hold at
+    most IAK_MERGE_IN_KERNEL_SMALL_PARTIALS partials (splits x query heads per
+    KV head) merge inside the decode kernel (one launch); others keep the merge
+    kernel."""
+    from intent_attention import _native as N
+    cases = [  # (B, Hkv, G, W) -> (splits, entries per split, in-kernel merge)
+        ((1, 8, 1, 64), (32, 2, True)),      # cfg1's grid: 64 workgroups, 32 partials per row
+        ((1, 8, 4, 256), (64, 4, True)),     # 128 workgroups, 256 partials per row
+        ((4, 8, 4, 64), (32, 2, False)),     # 256 workgroups
+        ((1, 1, 16, 1000), (125, 8, False)),  # 2,000 partials per row; the floor of 8 entries
+    ]
+    for shape, want in cases:
+        a = _decode_args(N, *shape)
+        a.merge_in_kernel = 2
+        p = N.plan_info(a)
+        assert (p["splits"], p["pages_per_split"], p["merge_in_kernel"]) == want, (shape, p)
+        assert p["tail_splits"] == 0
+
+
 def test_split_plan_and_merge_form_without_gpu():
     """merge_in_kernel: 0 keeps the split count and the merge kernel; 1 rounds
     the split count up to whole workgroups of four and sizes one partial per
