@@ -284,3 +284,43 @@ def test_fuzz_bit_exact(dev):
         kr, vr = _run(dev, k, v, spans, precs, k_dev=k_dev)
         assert _bits_equal(kr, _oracle_cat(k, spans, precs)), (case, lead, dk, dv, spans, precs)
         assert _bits_equal(vr, _oracle_cat(v, spans, precs)), (case, lead, dk, dv, spans, precs)
+
+
+def test_block_table_cache(dev):
+    """The kernel path keeps each layout's device block table (per device,
+    stream, spans and precisions): a repeated call reuses it and gives the same
+    bits, a changed precision or another stream builds a new one, and at most
+    _TABLES_SIZE layouts stay cached."""
+    import torch
+    from intent_attention import KVPrecision
+    from intent_attention import intent_quant_attention as IQ
+    _say("fake-quant block-table cache")
+    k, v = _kv(31, (1, 4), 120, 64, 64)
+    kd, vd = torch.from_numpy(k).to(dev), torch.from_numpy(v).to(dev)
+    precs = [KVPrecision(p) for p in ["INT8", "FP8", "INT4", "INT4_RESIDUAL", "FP16", "SKIP", "INT8", "FP8"]]
+    IQ._TABLES.clear()
+    kr1, vr1, tok1, _ = IQ._reconstruct_selected(kd, vd, _blocks(SPANS), precs)
+    kr2, vr2, tok2, _ = IQ._reconstruct_selected(kd, vd, _blocks(SPANS), precs)
+    torch.cuda.synchronize()
+    assert len(IQ._TABLES) == 1 and tok1 is tok2                 # one upload, reused
+    assert torch.equal(kr1.view(torch.int32), kr2.view(torch.int32))
+    assert torch.equal(vr1.view(torch.int32), vr2.view(torch.int32))
+    precs2 = list(precs)
+    precs2[0] = KVPrecision.INT4
+    kr3, _, _, _ = IQ._reconstruct_selected(kd, vd, _blocks(SPANS), precs2)
+    assert len(IQ._TABLES) == 2
+    names = [p.value for p in precs2]
+    assert _bits_equal(kr3.cpu().numpy(), _oracle_cat(k, SPANS, names))
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        kr4, _, _, _ = IQ._reconstruct_selected(kd, vd, _blocks(SPANS), precs)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize()
+    assert len(IQ._TABLES) == 3                                   # per stream
+    assert torch.equal(kr4.view(torch.int32), kr1.view(torch.int32))
+    for i in range(IQ._TABLES_SIZE + 4):                          # distinct layouts: the LRU bound
+        IQ._reconstruct_selected(kd, vd, _blocks([(i, i + 3), (50, 60)]), [KVPrecision.INT8, KVPrecision.FP8])
+    torch.cuda.synchronize()
+    assert len(IQ._TABLES) == IQ._TABLES_SIZE
+    IQ._TABLES.clear()
