@@ -383,6 +383,64 @@ def test_reference_causal_attention_cases():
 
 
 @pytest.mark.gpu
+def test_reference_correctness_cases():
+    """The reference's tests/test_reference_correctness.py cases on device
+    tensors: semantic_block_attention equals dense attention over the selected
+    tokens (SKIP left out), a layout that selects nothing gives zeros and an
+    empty debug record, the five policies together select ALWAYS + ATTEND +
+    RECENT + GLOBAL, causal attention is finite, never looks ahead (the
+    reference's triu construction, here in float64), and a single ALWAYS block
+    under the causal mask equals dense causal attention."""
+    from intent_attention import BlockLayout, BlockPolicy, SemanticBlock, dense_attention, semantic_block_attention
+    dev = torch.device("cuda:0")
+    _say("reference test_reference_correctness cases")
+    g = torch.Generator().manual_seed(1)
+    r = lambda *s: torch.randn(*s, generator=g).to(dev)  # noqa: E731
+    S, BP = SemanticBlock, BlockPolicy
+
+    q, k, v = r(2, 4, 16, 64), r(2, 4, 128, 64), r(2, 4, 128, 64)
+    out, dbg = semantic_block_attention(q, k, v, BlockLayout([S("a", 0, 64, BP.ALWAYS), S("b", 64, 128, BP.SKIP)]),
+                                        return_debug=True)
+    want = dense_attention(q, k[:, :, :64], v[:, :, :64])
+    assert torch.allclose(out, want) and dbg["selected_token_count"] == 64 and out.shape == (2, 4, 16, 64)
+
+    q, k, v = r(1, 1, 8, 32), r(1, 1, 16, 32), r(1, 1, 16, 32)
+    skip = BlockLayout([S("a", 0, 16, BP.SKIP)])
+    assert torch.equal(semantic_block_attention(q, k, v, skip), torch.zeros_like(q))
+    out, dbg = semantic_block_attention(q, k, v, skip, return_debug=True)
+    assert torch.equal(out, torch.zeros_like(q))
+    assert dbg["selected_token_count"] == 0 and dbg["selected_block_names"] == []
+
+    q, k, v = r(1, 2, 8, 32), r(1, 2, 128, 32), r(1, 2, 128, 32)
+    lay = BlockLayout([S("always", 0, 32, BP.ALWAYS), S("attend", 32, 64, BP.ATTEND, score=0.9),
+                       S("skip", 64, 96, BP.SKIP), S("recent", 96, 112, BP.RECENT),
+                       S("global", 112, 128, BP.GLOBAL)])
+    out, dbg = semantic_block_attention(q, k, v, lay, return_debug=True)
+    assert out.shape == (1, 2, 8, 32) and dbg["selected_token_count"] == 96 and dbg["total_kv_tokens"] == 128
+    sel = torch.cat([torch.arange(0, 64), torch.arange(96, 128)]).to(dev)
+    assert torch.allclose(out, dense_attention(q, k.index_select(-2, sel), v.index_select(-2, sel)))
+
+    q, k, v = r(1, 2, 8, 32), r(1, 2, 16, 32), r(1, 2, 16, 32)
+    out = dense_attention(q, k, v, causal=True)
+    assert out.shape == (1, 2, 8, 32) and torch.isfinite(out).all()
+
+    q = r(1, 1, 4, 8)
+    k = torch.eye(4, 8).unsqueeze(0).unsqueeze(0).to(dev)
+    v = torch.ones(1, 1, 4, 8, device=dev)
+    out = dense_attention(q, k, v, causal=True)
+    qd, kd, vd = q.double().cpu(), k.double().cpu(), v.double().cpu()
+    manual = torch.matmul(torch.softmax(torch.matmul(qd, kd.transpose(-2, -1)) / (8 ** 0.5)
+                                        + torch.triu(torch.full((4, 4), float("-inf"), dtype=torch.float64), diagonal=1),
+                                        dim=-1), vd)
+    assert torch.allclose(out.cpu().double(), manual, atol=1e-5)
+
+    q, k, v = r(1, 2, 8, 32), r(1, 2, 16, 32), r(1, 2, 16, 32)
+    out_sel, _ = semantic_block_attention(q, k, v, BlockLayout([S("a", 0, 16, BP.ALWAYS)]), causal=True,
+                                          return_debug=True)
+    assert torch.allclose(out_sel, dense_attention(q, k, v, causal=True), atol=1e-5)
+
+
+@pytest.mark.gpu
 def test_semantic_block_attention_dynamic_scores():
     """ATTEND blocks without a score are scored by the cosine probe before
     validation (reference.py:52-78), the scores land in the blocks and the debug
