@@ -441,6 +441,80 @@ def test_reference_correctness_cases():
 
 
 @pytest.mark.gpu
+def test_reference_intent_quant_attention_and_router_cases():
+    """The reference's tests/test_intent_quant_attention.py and
+    tests/test_end_to_end_router.py cases on device tensors (float32, so the
+    reconstruction runs on the fake-quant kernel), each output also against the
+    oracle's intent_quant_attention_reference (2e-5): output shape, the debug
+    keys and counts, finite error metrics, non-negative byte savings, an ALWAYS
+    block at least as precise as a low-score ATTEND block, zeros when nothing
+    is selected, and the router -> kernel metadata -> attention chain."""
+    from intent_attention import (BlockLayout, BlockPolicy as BP, BlockRouter, IntentQuantizer, RouterConfig,
+                                  SemanticBlock as S, intent_quant_attention_reference, routing_to_kernel_metadata,
+                                  semantic_block_attention)
+    dev = torch.device("cuda:0")
+    _say("reference test_intent_quant_attention / test_end_to_end_router cases")
+    g = torch.Generator().manual_seed(12)
+
+    def qkv(kv_len=64, q_len=8, heads=2, d=32):
+        return tuple(torch.randn(1, heads, n, d, generator=g) for n in (q_len, kv_len, kv_len))
+
+    def oracle(q, k, v, lay, pressure):
+        olay = P.BlockLayout([P.SemanticBlock(b.name, b.start, b.end, b.policy.value, b.score) for b in lay.blocks])
+        return A.intent_quant_attention_reference(q.numpy(), k.numpy(), v.numpy(), olay,
+                                                  P.IntentQuantizer(memory_pressure=pressure))
+
+    basic = BlockLayout([S("always", 0, 16, BP.ALWAYS), S("attend_high", 16, 32, BP.ATTEND, score=0.9),
+                         S("attend_low", 32, 48, BP.ATTEND, score=0.3), S("skip", 48, 64, BP.SKIP)])
+    for pressure in (0.3, 0.5, 0.8):
+        q, k, v = qkv()
+        out, dbg = intent_quant_attention_reference(q.to(dev), k.to(dev), v.to(dev), basic,
+                                                    IntentQuantizer(memory_pressure=pressure), return_debug=True)
+        assert out.shape == q.shape and torch.isfinite(out).all()
+        assert {"precision_by_block", "bytes_saved_pct", "reconstruction_mse_k", "reconstruction_mse_v",
+                "output_mse_vs_fp16_selected"} <= set(dbg)
+        assert len(dbg["selected_block_names"]) == 3 and dbg["selected_tokens"] == 48
+        assert dbg["output_mse_vs_fp16_selected"] >= 0.0 and -1.0 <= dbg["output_cosine_vs_fp16_selected"] <= 1.0
+        assert dbg["bytes_saved_pct"] >= 0.0
+        err = float(np.abs(out.cpu().numpy() - oracle(q, k, v, basic, pressure)).max())
+        assert err <= 2e-5, (pressure, err)
+
+    lay = BlockLayout([S("always", 0, 16, BP.ALWAYS), S("low_score", 16, 32, BP.ATTEND, score=0.1),
+                       S("skip_me", 32, 48, BP.SKIP)])
+    q, k, v = qkv(kv_len=48)
+    _, dbg = intent_quant_attention_reference(q.to(dev), k.to(dev), v.to(dev), lay,
+                                              IntentQuantizer(memory_pressure=0.7), return_debug=True)
+    order = {"fp16": 0, "fp8": 1, "int8": 2, "int4_residual": 3, "int4": 4, "skip": 5}
+    assert order.get(dbg["precision_by_block"]["always"], 99) <= order.get(dbg["precision_by_block"]["low_score"], 99)
+
+    q, k, v = qkv(kv_len=16)
+    out = intent_quant_attention_reference(q.to(dev), k.to(dev), v.to(dev), BlockLayout([S("skip", 0, 16, BP.SKIP)]),
+                                           IntentQuantizer())
+    assert torch.equal(out, torch.zeros_like(out))
+
+    routed_layout = BlockLayout([S("system", 0, 64, BP.ALWAYS), S("doc_high", 64, 192, BP.ATTEND, score=0.85),
+                                 S("doc_low", 192, 320, BP.ATTEND, score=0.15), S("recent", 320, 384, BP.RECENT),
+                                 S("unused", 384, 448, BP.SKIP)])
+    config = RouterConfig(memory_pressure=0.5)
+    routed = BlockRouter(config).route_layout(routed_layout, 448)
+    meta = routing_to_kernel_metadata(routed, page_size=16)
+    assert meta["selected_page_ids"] and all(isinstance(p, int) for p in meta["selected_page_ids"])
+    q, k, v = qkv(kv_len=448, q_len=4)
+    out, dbg = semantic_block_attention(q.to(dev), k.to(dev), v.to(dev), routed_layout, return_debug=True)
+    assert tuple(out.shape) == (1, 2, 4, 32) and dbg["selected_token_count"] > 0
+    assert set(meta["selected_block_names"]) <= {b.name for b in routed_layout.selected_blocks()}
+    out, dbg = intent_quant_attention_reference(q.to(dev), k.to(dev), v.to(dev), routed_layout,
+                                                IntentQuantizer(memory_pressure=config.memory_pressure),
+                                                return_debug=True)
+    assert tuple(out.shape) == (1, 2, 4, 32)
+    for name, prec in dbg["precision_by_block"].items():
+        if name in meta["selected_block_names"]:
+            assert prec.lower() in ("fp16", "fp8", "int8", "int4", "int4_residual")
+    err = float(np.abs(out.cpu().numpy() - oracle(q, k, v, routed_layout, 0.5)).max())
+    assert err <= 2e-5, err
+
+
+@pytest.mark.gpu
 def test_semantic_block_attention_dynamic_scores():
     """ATTEND blocks without a score are scored by the cosine probe before
     validation (reference.py:52-78), the scores land in the blocks and the debug
