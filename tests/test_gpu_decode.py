@@ -381,6 +381,55 @@ def test_fused_api_reference_test_facts(dev):
     del fake_int8_pages_from_fp16
 
 
+def test_fused_api_reference_precision_cases(dev):
+    """The per-precision and per-count cases of test_fused_selected_quant_decode.py
+    (:158-255) on the GPU, each compared with the oracle's restatement of the
+    reference loop (fused_selected_quant_decode.py:267-336): all INT8; FP16 and
+    INT8 halves; FP16 with page 1 INT8 and page 2 SKIP; one page per row; and
+    counts of 1, 2 and 3 across the rows. The reference's tests assert only the
+    shape; these also hold the values to the loop."""
+    import torch
+    from intent_attention import FusedDecodeConfig, FusedKVPrecision
+    from intent_attention.fused_selected_quant_decode import (fake_int8_pages_from_fp16,
+                                                              fused_selected_quant_decode_reference)
+    g = torch.Generator().manual_seed(1)
+    B, H, D, PS, NP, W = 2, 4, 64, 16, 8, 4
+    k16 = torch.randn(NP, PS, D, generator=g).half()
+    v16 = torch.randn(NP, PS, D, generator=g).half()
+    k8, ks = fake_int8_pages_from_fp16(k16)
+    v8, vs = fake_int8_pages_from_fp16(v16)
+    q = torch.randn(B, H, 1, D, generator=g).half()
+    pt = torch.arange(W, dtype=torch.int32).repeat(B, H, 1)
+    full = torch.full((B, H), W, dtype=torch.int32)
+    cfg = FusedDecodeConfig(page_size=PS, head_dim=D, max_selected_pages=W)
+    fp16, int8, skip = int(FusedKVPrecision.FP16), int(FusedKVPrecision.INT8), int(FusedKVPrecision.SKIP)
+
+    def prec(*pairs, default=fp16):
+        p = torch.full((NP,), default, dtype=torch.int32)
+        for idx, tag in pairs:
+            p[idx] = tag
+        return p
+
+    uneven = torch.full((B, H), 2, dtype=torch.int32)
+    uneven[0, 0], uneven[B - 1, H - 1] = 1, 3
+    cases = {"int8": (prec(default=int8), full),
+             "mixed": (prec((slice(NP // 2, None), int8)), full),
+             "mixed_with_skip": (prec((1, int8), (2, skip)), full),
+             "single_page": (prec(), torch.ones(B, H, dtype=torch.int32)),
+             "uneven_counts": (prec((1, int8)), uneven)}
+    for name, (p, pc) in cases.items():
+        _say("fused reference case", name)
+        args = [x.to(dev) for x in (q, k16, v16, k8, v8, ks, vs, pt, p, pc)]
+        out = fused_selected_quant_decode_reference(*args, cfg)
+        assert out.shape == (B, H, 1, D) and out.dtype == torch.float16 and out.is_cuda
+        ref = Dm.fused_decode_reference_loop(q.numpy(), k16.numpy(), v16.numpy(), k8.numpy(), v8.numpy(),
+                                             ks.float().numpy(), vs.float().numpy(), pt.numpy(), p.numpy(),
+                                             pc.numpy(), D)
+        err = np.abs(out.float().cpu().numpy() - ref.astype(np.float32)).max()
+        tol = TOL_FP16 if bool((p[:W] == fp16).all()) else TOL_QUANT
+        assert err <= tol, (name, err)
+
+
 def test_sibling_api_triton_numbering(dev):
     """intent_quant_decode_attention_triton: tag 0 FP16; 5 or an id < 0 invalid;
     every other tag -- 1-4, 6, 7, negative, 8 and above -- reads the INT8 pool

@@ -1,7 +1,8 @@
 """The reference's own unit-test cases for this path's Python API, restated
 against this package (CPU unless marked gpu): tests/test_triton_intent_quant_attention.py,
-test_intent_quant.py, test_block_router.py, test_block_metadata.py, test_mla.py
-and the BlockPrefetcher cases of test_prefetch.py. Each case asserts what the
+test_intent_quant.py, test_block_router.py, test_block_metadata.py, test_mla.py,
+the metadata conversion cases of test_fused_selected_quant_decode.py and the
+BlockPrefetcher cases of test_prefetch.py. Each case asserts what the
 reference's test asserts, so a caller of the reference finds the same behaviour
 (names, defaults, return shapes and dtypes, error types and messages). Where
 this package deliberately differs the case says so: kernel entry points refuse
@@ -18,6 +19,7 @@ import torch
 from intent_attention.block_metadata import SELECTED_POLICIES, BlockLayout, BlockPolicy as BP, SemanticBlock as S
 from intent_attention.block_router import (BlockDecision, BlockRouter, RoutedBlock, RouterConfig, compute_block_scores,
                                            routing_to_kernel_metadata)
+from intent_attention.fused_selected_quant_decode import FusedDecodeConfig, FusedKVPrecision, metadata_to_kernel_tensors
 from intent_attention.intent_quant import (_BYTES_PER_VALUE, IntentQuantizer, KVPrecision, QuantPolicy,
                                            compute_quant_error, fake_quantize_tensor)
 from intent_attention.mla import MLABlockTable, MLAConfig, absorb_weights, mla_sparse_decode_reference
@@ -74,6 +76,21 @@ def test_precision_tensor_and_fake_int8_pages():
     codes, scales = fake_int8_pages_from_fp16(torch.randn(4, 16, 32))
     assert codes.shape == (4, 16, 32) and codes.dtype == torch.int8
     assert scales.shape == (4,) and scales.dtype == torch.float32
+
+
+def test_fused_metadata_to_kernel_tensors():
+    """test_fused_selected_quant_decode.py:258-291: ids [0, 3, 5] with FP16 /
+    INT8 / SKIP give a [1, 1, 64] table, [8] tags and one count of 3; an empty
+    selection gives zeros and FP16 everywhere."""
+    meta = {"selected_page_ids": [0, 3, 5], "block_precision_by_page": {"0": "FP16", "3": "INT8", "5": "SKIP"}}
+    pt, prec, pc = metadata_to_kernel_tensors(meta, num_pages=8)
+    assert pt.shape == (1, 1, 64) and prec.shape == (8,) and pc.shape == (1, 1)
+    assert all(t.dtype == torch.int32 for t in (pt, prec, pc))
+    assert (prec[0], prec[3], prec[5]) == (FusedKVPrecision.FP16, FusedKVPrecision.INT8, FusedKVPrecision.SKIP)
+    assert pc[0, 0].item() == 3 and pt[0, 0, :3].tolist() == [0, 3, 5] and pt[0, 0, 3:].eq(0).all()
+    pt, prec, pc = metadata_to_kernel_tensors({"selected_page_ids": [], "block_precision_by_page": {}}, num_pages=4)
+    assert pt.sum().item() == 0 and pc.sum().item() == 0 and bool((prec == FusedKVPrecision.FP16).all())
+    assert FusedDecodeConfig().max_selected_pages == pt.shape[-1]
 
 
 def test_sibling_decode_refuses_host_tensors():
