@@ -8,6 +8,11 @@ from enum import Enum
 
 
 class StrEnum(Enum):
+    # members are singletons compared by identity: the C-level identity hash
+    # agrees with that equality and costs less than Enum's hash of the name
+    # (the precision tables look members up on every call)
+    __hash__ = object.__hash__
+
     @staticmethod
     def _generate_next_value_(name, start, count, last_values):  # noqa: D401
         return name

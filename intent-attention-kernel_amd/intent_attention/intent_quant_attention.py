@@ -43,7 +43,7 @@ import torch
 
 from . import _native as N
 from .block_metadata import BlockLayout
-from .decode_core import require_device
+from .decode_core import current_stream_handle, require_device
 from .intent_quant import IntentQuantizer, KVPrecision, QuantPolicy, _tdiv, compute_quant_error
 from .reference import dense_attention, semantic_block_attention
 
@@ -146,6 +146,9 @@ def _reconstruct_selected(k: torch.Tensor, v: torch.Tensor, blocks: List, precs:
     return k_rec, v_rec, tok, starts.tolist()
 
 
+# each precision's metadata string (the member's value), looked up once per block
+_VALUE = {p: p.value for p in KVPrecision}
+
 _FQ_CODE = {KVPrecision.FP16: N.FQ_FP16, KVPrecision.FP8: N.FQ_FP8, KVPrecision.INT8: N.FQ_INT8,
             KVPrecision.INT4: N.FQ_INT4, KVPrecision.INT4_RESIDUAL: N.FQ_INT4_RESIDUAL,
             KVPrecision.SKIP: N.FQ_SKIP}
@@ -180,7 +183,7 @@ def _block_tables(dev: torch.device, spans: tuple, precs: List[KVPrecision]):
     for later calls over the same layout on the same stream (the tables are
     read-only; at most ``_TABLES_SIZE`` layouts, least recently used first
     out)."""
-    key = (dev, torch.cuda.current_stream(dev).cuda_stream, spans, tuple(precs))
+    key = (dev, current_stream_handle(dev), spans, tuple(precs))
     ent = _TABLES.get(key)
     if ent is not None:
         _TABLES.move_to_end(key)
@@ -224,8 +227,7 @@ def _reconstruct_native(k: torch.Tensor, v: torch.Tensor, spans: tuple, precs: L
     a.out, a.out_stride_l, a.out_stride_t = out.data_ptr(), out.stride(0), out.stride(1)
     nws = N.fake_quant_blocks_workspace(a)
     ws = torch.empty(nws, dtype=torch.uint8, device=k.device) if nws else None
-    N.fake_quant_blocks(a, torch.cuda.current_stream(k.device).cuda_stream,
-                        ws.data_ptr() if ws is not None else 0, nws)
+    N.fake_quant_blocks(a, current_stream_handle(k.device), ws.data_ptr() if ws is not None else 0, nws)
     out = out.reshape(*lead_shape, total, dk + dv)
     return out[..., :dk], out[..., dk:], tok, list(starts)
 
@@ -258,7 +260,8 @@ def intent_quant_attention_reference(q: torch.Tensor, k: torch.Tensor, v: torch.
     for i, block in enumerate(blocks):
         n = block.end - block.start
         policy: QuantPolicy = quantizer.assign_block_precision(block)
-        precision_by_block[block.name] = policy.precision.value
+        name = _VALUE.get(policy.precision)
+        precision_by_block[block.name] = name if name is not None else policy.precision.value
         fp16_bytes += 2 * n * head_dim * 2
         quant_bytes += int(round(2 * n * head_dim * policy.estimated_bytes_per_value))
         precs.append(policy.precision)

@@ -42,7 +42,7 @@ import torch
 
 from . import _native as N
 from .block_metadata import BlockLayout, BlockPolicy
-from .decode_core import require_device
+from .decode_core import current_stream_handle, require_device
 
 _DTYPES = {torch.float16: N.DTYPE_F16, torch.float32: N.DTYPE_F32, torch.bfloat16: N.DTYPE_BF16}
 _MAX_DIM = 1024
@@ -89,7 +89,9 @@ def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: b
         raise ValueError(f"dtype {q.dtype} is not supported (float16, float32, bfloat16)")
     if D > _MAX_DIM or Dv > _MAX_DIM:
         raise ValueError(f"head_dim {D} / v_dim {Dv} exceeds the widest supported ({_MAX_DIM})")
-    lead = tuple(torch.broadcast_shapes(q.shape[:-2], k.shape[:-2], v.shape[:-2]))
+    lead = tuple(q.shape[:-2])
+    if k.shape[:-2] != lead or v.shape[:-2] != lead:
+        lead = tuple(torch.broadcast_shapes(q.shape[:-2], k.shape[:-2], v.shape[:-2]))
     mask_rows = None
     if mask is not None:
         if mask.dtype != torch.bool and mask.dtype not in _DTYPES:
@@ -137,8 +139,7 @@ def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: b
     # allocator reuses their memory only after these kernels
     ws_bytes = N.dense_attention_workspace(a)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
-    N.dense_attention(a, torch.cuda.current_stream(dev).cuda_stream,
-                      ws.data_ptr() if ws is not None else 0, ws_bytes)
+    N.dense_attention(a, current_stream_handle(dev), ws.data_ptr() if ws is not None else 0, ws_bytes)
     return out
 
 
