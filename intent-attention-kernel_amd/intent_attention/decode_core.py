@@ -366,7 +366,7 @@ class DecodePlan:
         if out is None:
             out = torch.empty((NP, N.PAGE_DESC_BYTES // 4), dtype=torch.int32, device=self.device)
         _check_descriptors(out, NP, self.device)
-        s = torch.cuda.current_stream(self.device).cuda_stream if stream is None else stream
+        s = current_stream_handle(self.device) if stream is None else stream
         N.pack_page_descriptors(self.args, out.data_ptr(), s)
         self.use_descriptors(out)
         return out
@@ -390,7 +390,7 @@ class DecodePlan:
         return out
 
     def _pack_records_into(self, out: torch.Tensor, stream: Optional[int]) -> None:
-        s = torch.cuda.current_stream(self.device).cuda_stream if stream is None else stream
+        s = current_stream_handle(self.device) if stream is None else stream
         saved = (self.args.page_desc, self.args.entry_records)
         N.pack_entry_records(self.args, out.data_ptr(), s)
         self.args.page_desc, self.args.entry_records = saved

@@ -48,7 +48,7 @@ import torch
 
 from . import _native as N
 from .block_metadata import BlockLayout, BlockPolicy
-from .decode_core import PagePools, paged_decode
+from .decode_core import PagePools, current_stream_handle, paged_decode
 from .prefetch import BlockPrefetcher
 
 
@@ -202,7 +202,7 @@ class KVMemoryManager:
         a.num_pages, a.page_elems, a.mode = len(pids), self._elems, mode
         a.pages, a.pool_pages = ids.data_ptr(), fp16.shape[0]
         a.fp16, a.int8, a.scales = fp16.data_ptr(), int8.data_ptr(), scales.data_ptr()
-        N.transcode_pages(a, torch.cuda.current_stream(self.device).cuda_stream)
+        N.transcode_pages(a, current_stream_handle(self.device))
         torch.autograd.graph.increment_version([fp16, int8, scales])   # written through raw pointers
 
     def _zero_rows(self, pids: Sequence[int]) -> None:

@@ -16,7 +16,7 @@ from typing import Dict, Optional, Sequence
 import torch
 
 from . import _native as N
-from .decode_core import PAGE_SIZE, _DT, _check_pool, _ptr, _scale_dtype, require_device
+from .decode_core import PAGE_SIZE, _DT, _check_pool, _ptr, _scale_dtype, current_stream_handle, require_device
 
 SUPPORTED_SHAPES = ((64, 64), (128, 128), (256, 256), (512, 512), (576, 512), (576, 64))
 
@@ -63,7 +63,7 @@ class MlaPlan:
     def run(self, stream: Optional[int] = None, events: Optional[tuple] = None) -> None:
         """Launch on ``stream`` (default: torch's current stream). ``events``: an
         optional pair of torch.cuda.Event recorded around the split kernel alone."""
-        s = torch.cuda.current_stream(self.device).cuda_stream if stream is None else stream
+        s = current_stream_handle(self.device) if stream is None else stream
         ev = None if events is None else (events[0].cuda_event, events[1].cuda_event)
         N.mla_decode(self.args, self._ws.data_ptr() if self._ws is not None else 0, self.workspace_bytes, s, ev)
 

@@ -28,6 +28,7 @@ import torch
 
 from . import _native as N
 from .block_router import RoutedBlock, _SELECTING
+from .decode_core import current_stream_handle
 from .fused_selected_quant_decode import FusedDecodeConfig, FusedKVPrecision, precision_tag
 
 __all__ = ["build_page_tables", "routing_to_kernel_tensors"]
@@ -112,7 +113,7 @@ def build_page_tables(span_offsets, span_begin, span_end, span_tag, *, num_rows:
     a.page_table = table.data_ptr() if table.numel() else None
     a.page_counts = counts.data_ptr() if counts.numel() else None
     a.page_precision = prec.data_ptr() if prec is not None and prec.numel() else None
-    N.build_page_tables(a, torch.cuda.current_stream(dev).cuda_stream)
+    N.build_page_tables(a, current_stream_handle(dev))
     return table, prec, counts
 
 

@@ -21,7 +21,7 @@ from typing import Optional, Tuple
 import torch
 
 from . import _native as N
-from .decode_core import PAGE_SIZE, require_device
+from .decode_core import PAGE_SIZE, current_stream_handle, require_device
 
 _PREC = {"FP8": N.TAG_FP8, "INT8": N.TAG_INT8, "INT4": N.TAG_INT4, "INT4_RESIDUAL": N.TAG_INT4_RESIDUAL}
 
@@ -36,7 +36,7 @@ def _launch(pages: torch.Tensor, tag: int, mode: int, codes: torch.Tensor, scale
     a.precision, a.mode, a.int4_group = tag, mode, int4_group
     a.codes, a.scales = codes.data_ptr(), scales.data_ptr()
     a.scale_dtype = N.DTYPE_F32 if scales.dtype == torch.float32 else N.DTYPE_F16
-    N.quantize_pages(a, torch.cuda.current_stream(pages.device).cuda_stream)
+    N.quantize_pages(a, current_stream_handle(pages.device))
     # the kernel writes through raw pointers: tell torch's version counters (decode
     # plans that packed these scales into entry records see the change)
     torch.autograd.graph.increment_version([codes, scales])

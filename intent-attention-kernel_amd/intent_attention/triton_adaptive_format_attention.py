@@ -41,7 +41,7 @@ from typing import Optional, Tuple
 import torch
 
 from . import _native as N
-from .decode_core import PAGE_SIZE, PagePools, paged_decode
+from .decode_core import PAGE_SIZE, PagePools, current_stream_handle, paged_decode
 
 
 class AdaptivePageFormat(IntEnum):
@@ -90,7 +90,7 @@ def _promote(codes: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
     a = N.TranscodeArgs()
     a.num_pages, a.page_elems, a.mode, a.pages, a.pool_pages = n, E, N.TRANSCODE_PROMOTE_FP16, None, n
     a.fp16, a.int8, a.scales = out.data_ptr(), codes.data_ptr(), scales.data_ptr()
-    N.transcode_pages(a, torch.cuda.current_stream(codes.device).cuda_stream)
+    N.transcode_pages(a, current_stream_handle(codes.device))
     return out
 
 

@@ -21,7 +21,7 @@ import math
 import torch
 
 from . import _native as N
-from .decode_core import require_device
+from .decode_core import current_stream_handle, require_device
 
 _DT = {torch.float32: N.DTYPE_F32, torch.float16: N.DTYPE_F16, torch.bfloat16: N.DTYPE_BF16}
 MAX_LATENT = 1024
@@ -76,7 +76,7 @@ def mla_latent_context(q_absorb: torch.Tensor, C: torch.Tensor, page_table: torc
     # row's keys over several workgroups (allocated on this stream, as the rest)
     ws_bytes = N.mla_decode_rows_workspace(a)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
-    N.mla_decode_rows(a, torch.cuda.current_stream(dev).cuda_stream, ws.data_ptr() if ws is not None else 0, ws_bytes)
+    N.mla_decode_rows(a, current_stream_handle(dev), ws.data_ptr() if ws is not None else 0, ws_bytes)
     return ctx
 
 
