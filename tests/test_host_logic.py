@@ -252,3 +252,20 @@ def test_grouped_reconstruction_equals_cat_of_blocks():
             want_v2 = torch.cat([fake_quantize_tensor(v2[..., b.start:b.end, :], p)[0]
                                  for b, p in zip(blocks, precs)], dim=-2)
             assert torch.equal(kr2.to(want_k.dtype), want_k) and torch.equal(vr2.to(want_v2.dtype), want_v2)
+
+
+def test_precision_enums_are_singletons_under_identity_hash():
+    """The string enums hash by identity (their members are singletons compared by
+    identity): dict and set lookups, lookups by value and by name, pickling and
+    copying all give the same members, and str() is still the metadata string."""
+    import copy
+    import pickle
+    for enum in (ia.KVPrecision, ia.BlockPolicy):
+        members = list(enum)
+        table = {m: i for i, m in enumerate(members)}
+        assert [table[m] for m in members] == list(range(len(members)))
+        for m in members:
+            assert enum(m.value) is m and enum[m.name] is m
+            assert pickle.loads(pickle.dumps(m)) is m and copy.deepcopy(m) is m
+            assert str(m) == m.value and len({m, enum(m.value)}) == 1
+    assert ia.QuantPolicy(ia.KVPrecision.INT4_RESIDUAL).estimated_bytes_per_value == 1.0
